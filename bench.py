@@ -1,0 +1,351 @@
+"""Optimizer-step benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c1,c3,c4,c5] [--no-cpu]
+
+Headline (the JSON line's ``value``): BASELINE config 2 — multi-tensor fp32
+AdamW over the GPT-2-124M parameter list (148 tensors, 124,439,808 params,
+weight decay 0.1 on matrices and 0 on vectors, lr 3e-4, betas (0.9, 0.999),
+eps 1e-8), one ``optimizer.step()`` through the public API per step, inputs
+resident in HBM.  ``value`` = params/s over K timed steps bracketed by
+``torch.cuda.synchronize()``.
+
+``roofline`` is the dominant kernel (the multi-tensor AdamW pass): 28
+algorithmic bytes per parameter (read p, g, m, v; write p, m, v) times the
+parameters of one launch, over its average duration measured here with HIP
+events on the launch stream.  ``traffic`` is read from the committed
+rocprofv3 PMC summary when present.  ``cpu_baseline`` times the NumPy oracle
+(the reference's NumPy path restated op for op) on a bounded sample of the
+same workload on this host, one core.
+
+The other BASELINE configs (C1 flat 4M fp32 hot and MALL-flushed, C3 AMP
+GPT-2, C4 GPT-1.3B bf16 + clip, C5 Llama-7B AMP + clip) are reported under
+``extra`` with their own B/param accounting.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "AdamW step params/sec + achieved HBM GB/s (% of peak), GPT-2 124M & 1.3B"
+HBM_PEAK_GBPS = 8000.0
+PROFILE_PMC = ROOT / "profiles" / "adamw_mt_f32_gpt2-124m_pmc.json"
+
+
+def log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--configs", default="c2,c1,c3,c4,c5")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--kernel-only", action="store_true", help="only the C2 kernel loop (for profilers)")
+    return parser.parse_args()
+
+
+# ---- workload construction ---------------------------------------------------------------------
+def make_params(nt, torch, shapes, dtype, seed=1337, sigma=0.02):
+    generator = torch.Generator(device="cuda").manual_seed(seed)
+    params = []
+    for shape in shapes:
+        data = torch.randn(shape, generator=generator, device="cuda", dtype=torch.float32).mul_(sigma)
+        storage = data.to(dtype.torch_dtype) if dtype is not nt.float32 else data
+        param = nt.Parameter.__new__(nt.Parameter)
+        nt.Tensor._initialize(param, storage.contiguous(), True)
+        params.append(param)
+    return params
+
+
+def attach_grads(nt, torch, params, dtype, sigma=1e-3, scale=1.0, seed=2337):
+    generator = torch.Generator(device="cuda").manual_seed(seed)
+    for param in params:
+        data = torch.randn(param.shape, generator=generator, device="cuda", dtype=torch.float32).mul_(sigma * scale)
+        param.grad = nt.Tensor._from_storage(data.to(dtype.torch_dtype).contiguous())
+
+
+def decay_groups(params):
+    return [{"params": [p for p in params if p.ndim >= 2], "weight_decay": 0.1},
+            {"params": [p for p in params if p.ndim < 2], "weight_decay": 0.0}]
+
+
+def event_pair(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+# ---- C2: the headline ----------------------------------------------------------------------------
+def bench_c2(nt, torch, steps, warmup):
+    from namitorch_amd.param_lists import gpt2_shapes, total_params
+    shapes = gpt2_shapes()
+    n = total_params(shapes)
+    params = make_params(nt, torch, shapes, nt.float32)
+    attach_grads(nt, torch, params, nt.float32)
+    optimizer = nt.optim.AdamW(decay_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8)
+    for _ in range(warmup):
+        optimizer.step()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        optimizer.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    ms_per_step = elapsed * 1e3 / steps
+    # Dominant kernel: re-launch the cached plan back to back between HIP events
+    # on the launch stream (torch's current stream, where the library launches).
+    kernel_ms = kernel_time_c2(nt, torch, optimizer, params, steps)
+    result = dict(params=n, tensors=len(shapes), ms_per_step=ms_per_step, params_per_s=n / (ms_per_step / 1e3),
+                  kernel_ms=kernel_ms, bytes_per_param=28)
+    del optimizer, params
+    torch.cuda.empty_cache()
+    return result
+
+
+def kernel_time_c2(nt, torch, optimizer, params, launches):
+    backend = nt.get_backend("cuda:0")
+    plans = list(backend._plans.values())
+    plan = max(plans, key=lambda p: p.numel)
+    from namitorch_amd import _native
+    group = optimizer.param_groups
+    records = []
+    for g in group:
+        options = optimizer._prepare_options({k: v for k, v in g.items() if k != "params"}, "g")
+        step = optimizer.state[id(g["params"][0])]["step"] + 1
+        records.append(optimizer._coefficients(nt.float32, options, step, True))
+    slots = (_native.AdamWCoefs * len(records))(*records)
+    start, stop = event_pair(torch)
+    backend.adamw_multi(plan, slots, None)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(launches):
+        backend.adamw_multi(plan, slots, None)
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / launches
+
+
+# ---- C1: flat 4,194,304 fp32 ------------------------------------------------------------------------
+def bench_c1(nt, torch, steps, warmup):
+    n = 4_194_304
+    (param,) = make_params(nt, torch, [(n,)], nt.float32)
+    attach_grads(nt, torch, [param], nt.float32)
+    optimizer = nt.optim.AdamW([param], lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    for _ in range(warmup):
+        optimizer.step()
+    torch.cuda.synchronize()
+    start, stop = event_pair(torch)
+    start.record()
+    for _ in range(steps):
+        optimizer.step()
+    stop.record()
+    stop.synchronize()
+    hot_ms = start.elapsed_time(stop) / steps
+    # MALL flush: stream 1 GiB through HBM between steps; time only the step.
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    total = 0.0
+    for _ in range(steps):
+        scratch.fill_(1.0)
+        a, b = event_pair(torch)
+        a.record()
+        optimizer.step()
+        b.record()
+        b.synchronize()
+        total += a.elapsed_time(b)
+    flushed_ms = total / steps
+    del scratch, optimizer, param
+    torch.cuda.empty_cache()
+    return dict(params=n, bytes_per_param=28, hot_ms=hot_ms, flushed_ms=flushed_ms,
+                hot_GBps=28 * n / hot_ms / 1e6, flushed_GBps=28 * n / flushed_ms / 1e6)
+
+
+# ---- C3 / C4 / C5: mixed precision through the public API -------------------------------------------
+def amp_step(nt, scaler, optimizer, params, max_norm):
+    scaler.scale(nt.Tensor._from_storage(__import__("torch").ones((), device="cuda")))
+    finite = scaler.unscale_(optimizer)
+    if finite and max_norm is not None:
+        nt.optim.clip_grad_norm_(params, max_norm)
+    scaler.step(optimizer)
+    scaler.update()
+
+
+def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype, amp, max_norm, bytes_per_param,
+                steps, warmup):
+    from namitorch_amd.param_lists import total_params
+    n = total_params(shapes)
+    params = make_params(nt, torch, shapes, param_dtype)
+    attach_grads(nt, torch, params, grad_dtype, scale=65536.0 if amp else 1.0)
+    optimizer = nt.optim.AdamW(decay_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8,
+                               master_weights=True, state_dtype=state_dtype)
+    scaler = nt.GradScaler(init_scale=65536.0) if amp else None
+    grads = [p.grad for p in params]
+    storages = [g._storage for g in grads]
+
+    def one_step():
+        # The pending unscale/clip of the previous step is dropped by giving
+        # the gradients fresh Tensor handles over the same storage (as a new
+        # backward would), so every step reads the same scaled values.
+        for param, storage in zip(params, storages):
+            param.grad = nt.Tensor._from_storage(storage)
+        if amp:
+            amp_step(nt, scaler, optimizer, params, max_norm)
+        else:
+            if max_norm is not None:
+                nt.optim.clip_grad_norm_(params, max_norm)
+            optimizer.step()
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    start_wall = time.perf_counter()
+    start, stop = event_pair(torch)
+    start.record()
+    for _ in range(steps):
+        one_step()
+    stop.record()
+    stop.synchronize()
+    wall_ms = (time.perf_counter() - start_wall) * 1e3 / steps
+    gpu_ms = start.elapsed_time(stop) / steps
+    result = dict(params=n, tensors=len(shapes), bytes_per_param=bytes_per_param, ms_per_step=wall_ms,
+                  params_per_s=n / (wall_ms / 1e3), GBps=bytes_per_param * n / wall_ms / 1e6,
+                  pct_hbm_peak=100 * bytes_per_param * n / wall_ms / 1e6 / HBM_PEAK_GBPS,
+                  scale=None if scaler is None else scaler.get_scale())
+    del optimizer, params, grads, storages, scaler
+    torch.cuda.empty_cache()
+    return result
+
+
+# ---- CPU baseline ---------------------------------------------------------------------------------------
+def cpu_baseline(sample_params=12_000_000, steps=4):
+    """NumPy oracle AdamW (reference NumPy path restated) on the first tensors
+    of the GPT-2-124M list up to `sample_params`, steps 2..steps+1 timed."""
+    import numpy as np
+    from namitorch_amd.param_lists import gpt2_shapes
+    from oracle import adam as oadam
+    shapes = []
+    total = 0
+    for shape in gpt2_shapes()[1:]:          # skip the 38.6M embedding: keep the sample bounded
+        size = int(np.prod(shape))
+        if total + size > sample_params:
+            continue
+        shapes.append(shape)
+        total += size
+    rng = np.random.Generator(np.random.PCG64(1337))
+    params = [(rng.standard_normal(int(np.prod(s)), dtype=np.float32) * np.float32(0.02)) for s in shapes]
+    grads = [(rng.standard_normal(p.size, dtype=np.float32) * np.float32(1e-3)) for p in params]
+    ms = [np.zeros_like(p) for p in params]
+    vs = [np.zeros_like(p) for p in params]
+    wds = [0.1 if len(s) >= 2 else 0.0 for s in shapes]
+
+    def step(k):
+        for p, g, m, v, wd in zip(params, grads, ms, vs, wds):
+            oadam.adam_step(p, g, m, v, k, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+
+    step(1)
+    start = time.perf_counter()
+    for k in range(2, steps + 2):
+        step(k)
+    elapsed = time.perf_counter() - start
+    value = total * steps / elapsed
+    return dict(value=value, unit="params/s", cores=1, kind="port",
+                sample=f"NumPy oracle AdamW, {len(shapes)} GPT-2-124M tensors ({total} params, embedding excluded), "
+                       f"{steps} timed steps after 1 warm-up step; {elapsed:.2f} s; host {platform.processor() or platform.machine()}, "
+                       f"os.cpu_count()={os.cpu_count()} (NumPy ufuncs are single-threaded)",
+                GBps=28 * value / 1e9)
+
+
+def pmc_traffic():
+    if not PROFILE_PMC.exists():
+        return None
+    try:
+        data = json.loads(PROFILE_PMC.read_text())
+        return data.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "namitorch_amd benchmarks one GPU; the optimizer step has no multi-GPU path in this build "
+                                   "(see DESIGN.md for how it would shard).", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    import namitorch_amd as nt
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a HIP device")
+    log(f"device {torch.cuda.get_device_name(0)}")
+    wanted = [c.strip() for c in args.configs.split(",") if c.strip()]
+    extra = {}
+    log("C2 gpt2-124m fp32 multi-tensor AdamW")
+    c2 = bench_c2(nt, torch, args.steps, args.warmup)
+    log(f"C2: {c2['ms_per_step']:.3f} ms/step, kernel {c2['kernel_ms']:.3f} ms")
+    if args.kernel_only:
+        print(json.dumps(c2))
+        return
+    from namitorch_amd.param_lists import gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes
+    if "c1" in wanted:
+        log("C1 flat 4M fp32")
+        extra["c1_flat4m_fp32"] = bench_c1(nt, torch, args.steps, args.warmup)
+    if "c3" in wanted:
+        log("C3 gpt2-124m AMP (bf16 model, fp32 master, fp16 grads x65536)")
+        extra["c3_gpt2_amp"] = bench_mixed(nt, torch, "c3", gpt2_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.float16,
+                                           state_dtype=None, amp=True, max_norm=None, bytes_per_param=30,
+                                           steps=args.steps, warmup=args.warmup)
+    if "c4" in wanted:
+        log("C4 gpt-1.3b bf16 params/m/v/grads, fp32 master, clip 1.0")
+        extra["c4_gpt1p3b_bf16_clip"] = bench_mixed(nt, torch, "c4", gpt_1p3b_shapes(), param_dtype=nt.bfloat16,
+                                                    grad_dtype=nt.bfloat16, state_dtype=nt.bfloat16, amp=False,
+                                                    max_norm=1.0, bytes_per_param=22,
+                                                    steps=max(5, args.steps // 2), warmup=args.warmup)
+    if "c5" in wanted:
+        log("C5 llama-7b fp32 master/m/v, bf16 grads/params, AMP + clip")
+        extra["c5_llama7b_amp_clip"] = bench_mixed(nt, torch, "c5", llama7b_shapes(), param_dtype=nt.bfloat16,
+                                                   grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
+                                                   bytes_per_param=30, steps=max(5, args.steps // 5),
+                                                   warmup=min(args.warmup, 3))
+    baseline = None
+    if not args.no_cpu:
+        log("CPU baseline (NumPy oracle)")
+        baseline = cpu_baseline()
+    achieved = 28 * c2["params"] / (c2["kernel_ms"] / 1e3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": c2["params_per_s"],
+        "unit": "params/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": c2["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) params, N(0,1e-3) grads, resident in HBM)",
+        "config": {"workload": "C2: GPT-2-124M parameter list, multi-tensor fp32 AdamW (148 tensors, 124,439,808 params, "
+                               "2 weight-decay groups), one optimizer.step() per step",
+                   "params": c2["params"], "tensors": c2["tensors"], "bytes_per_param": 28,
+                   "step_GBps": 28 * c2["params_per_s"] / 1e9,
+                   "step_pct_hbm_peak": 100 * 28 * c2["params_per_s"] / 1e9 / HBM_PEAK_GBPS},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": pmc_traffic(),
+                     "kernel": "nt::adamw_mt_kernel<TF32,TF32,TF32,TNone,RoundF32,false>",
+                     "kernel_ms": c2["kernel_ms"]},
+        "cpu_baseline": baseline,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

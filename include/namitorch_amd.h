@@ -1,0 +1,279 @@
+/*
+ * namitorch_amd.h — C ABI of the MI355X (gfx950) optimizer-step library.
+ *
+ * This is the drop-in boundary for NamiTorch's optimizer-step hot path:
+ * AdamW.step(), GradScaler unscale_/finite-check/update and clip_grad_norm_.
+ * Every entry point takes plain pointers, sizes and a hipStream_t passed as
+ * `void*`; no framework types cross the boundary.  Callers (the Python host
+ * layer in namitorch_amd/, through ctypes) own every tensor buffer.  The
+ * library owns only multi-tensor plans (descriptor table, task map and
+ * reduction workspace), released by nt_plan_destroy().
+ *
+ * Status codes: 0 = OK; a negative code names the exception class the
+ * Python layer raises, with the message from nt_last_error() (per thread).
+ *
+ * Reference citations are paths under renderityai/NamiTorch.
+ */
+#ifndef NAMITORCH_AMD_H
+#define NAMITORCH_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define NT_OK 0
+#define NT_ERR_VALUE (-1)   /* ValueError  */
+#define NT_ERR_TYPE (-2)    /* TypeError   */
+#define NT_ERR_RUNTIME (-3) /* RuntimeError (contract violations)   */
+#define NT_ERR_HIP (-4)     /* RuntimeError (HIP runtime failure)   */
+
+/* ---- storage dtype codes ----------------------------------------------- */
+#define NT_DTYPE_NONE (-1)
+#define NT_F32 0
+#define NT_F16 1
+#define NT_BF16 2
+#define NT_F64 3
+
+/* ---- multi-tensor plan limits ------------------------------------------ */
+#define NT_MAX_SLOTS 16     /* coefficient sets per nt_adamw_mt launch */
+
+/*
+ * One tensor of a multi-tensor plan.  `param` is the array the update is
+ * computed on (fp32 master weights in master mode, else the parameter
+ * itself); `model_copy` is an optional low-precision copy written in the same
+ * pass (NULL when absent).  Unused roles are NULL (a grad-only plan for
+ * clip_grad_norm_ has only `grad`).  `slot` selects the coefficient set.
+ */
+typedef struct nt_mt_tensor {
+    void *param;
+    void *grad;
+    void *exp_avg;
+    void *exp_avg_sq;
+    void *model_copy;
+    uint64_t numel;
+    uint32_t slot;
+    uint32_t reserved;
+} nt_mt_tensor; /* 56 bytes; padded to 64 on device */
+
+/* Storage dtypes of the roles; identical for every tensor of one plan. */
+typedef struct nt_mt_layout {
+    int32_t param_dtype;  /* NT_F32 (master or plain), NT_F16, NT_F64 */
+    int32_t grad_dtype;   /* NT_F32, NT_F16, NT_BF16, NT_F64 */
+    int32_t state_dtype;  /* NT_F32, NT_BF16 (or the param dtype) */
+    int32_t copy_dtype;   /* NT_DTYPE_NONE, NT_F16, NT_BF16 */
+} nt_mt_layout;
+
+/*
+ * The ten AdamW coefficients, each already rounded to the parameter dtype
+ * on the host exactly as the reference does (optim/adam.py:82-86 via
+ * optim/_common.py:39-47), plus the two launch flags of the reference kernel
+ * (backends/cuda/adamw.py:7-11).  `coupled_weight_decay` selects the
+ * reference's Adam (L2 term added to the gradient, optim/_common.py:62-63)
+ * instead of AdamW's decoupled decay.
+ */
+typedef struct nt_adamw_coefs {
+    float lr, beta1, beta2, complement1, complement2;
+    float eps, weight_decay, decay_factor, correction1, correction2;
+    int32_t maximize;
+    int32_t update_parameter;
+    int32_t coupled_weight_decay;
+    int32_t reserved;
+} nt_adamw_coefs; /* 56 bytes */
+
+/* fp64 twin for float64 parameters (array path only). */
+typedef struct nt_adamw_coefs64 {
+    double lr, beta1, beta2, complement1, complement2;
+    double eps, weight_decay, decay_factor, correction1, correction2;
+    int32_t maximize;
+    int32_t update_parameter;
+    int32_t coupled_weight_decay;
+    int32_t reserved;
+} nt_adamw_coefs64; /* 96 bytes */
+
+/*
+ * Device-resident control block of one AMP/clip iteration.  Written by
+ * nt_amp_finalize(); read by nt_adamw_mt() when a grad transform points at it.
+ */
+typedef struct nt_amp_ctrl {
+    double sumsq;          /* sum of squares of the (unscaled) grads, fp64 */
+    double amax;           /* max |g| over finite grads, fp64 */
+    double norm;           /* global grad norm (fp64), reference semantics */
+    double clip_coef;      /* max_norm / (norm + 1e-6) */
+    float scale;           /* loss scale of the next iteration */
+    float scale_used;      /* loss scale this iteration's grads divide by */
+    int32_t found_inf;     /* any unscaled grad non-finite */
+    int32_t has_nan;       /* any unscaled grad NaN */
+    int32_t clip;          /* clip_coef < 1: pass 2 multiplies by clip_coef */
+    int32_t skip;          /* pass 2 leaves params/states untouched */
+    int32_t growth_tracker;
+    int32_t iterations;    /* finalize calls since the block was reset */
+    int32_t skipped;       /* of which found non-finite grads */
+    int32_t reserved;
+} nt_amp_ctrl; /* 72 bytes */
+
+/*
+ * How pass 2 turns a stored grad into the one AdamW consumes.  With
+ * `ctrl == NULL` the host-known values below are used: unscale divides by
+ * `scale` in fp32 and rounds to the grad dtype (amp.py:190-191); clip
+ * multiplies in fp64 by `clip_coef` and rounds to the grad dtype
+ * (optim/clip_grad.py:111).  With `ctrl != NULL` the scale, clip flag, clip
+ * coefficient and skip flag are read from that device block instead
+ * (scale_used, clip, clip_coef, skip).
+ */
+typedef struct nt_grad_xform {
+    float scale;
+    int32_t unscale;
+    double clip_coef;
+    int32_t clip;
+    int32_t honor_skip;    /* with ctrl: skip the update when ctrl->skip */
+    const nt_amp_ctrl *ctrl;
+} nt_grad_xform;
+
+typedef struct nt_plan nt_plan; /* opaque multi-tensor plan */
+
+/* ---- library / device -------------------------------------------------- */
+
+/* Thread-local message of the last failing call ("" if none). */
+const char *nt_last_error(void);
+
+/* ABI version of this library (bumped when a struct layout changes). */
+int32_t nt_abi_version(void);
+
+/* Number of visible HIP devices. */
+int32_t nt_device_count(int32_t *count);
+
+/* Name of the gfx target of `device` (e.g. "gfx950") into buf[len]. */
+int32_t nt_device_arch(int32_t device, char *buf, int32_t len);
+
+/* Wait for all work queued on `stream`. */
+int32_t nt_stream_synchronize(void *stream);
+
+/* Copy `bytes` between host and device on `stream` and wait for it. */
+int32_t nt_memcpy_d2h(void *dst, const void *src, uint64_t bytes, void *stream);
+int32_t nt_memcpy_h2d(void *dst, const void *src, uint64_t bytes, void *stream);
+
+/* ---- per-tensor AdamW: the reference kernel's own ABI ------------------ */
+
+/*
+ * Replaces `namitorch_adamw_float32` (backends/cuda/adamw.py:7-28, launched
+ * by AdamWCUDAKernel.run, backends/cuda/adamw.py:54-73): one fp32 tensor,
+ * same arguments in the same order, plus the stream.  Returns NT_OK with
+ * nothing launched for count == 0.
+ */
+int32_t nt_adamw_f32(float *parameter, const float *gradient, float *exp_avg,
+                     float *exp_avg_sq, float lr, float beta1, float beta2,
+                     float complement1, float complement2, float eps,
+                     float weight_decay, float decay_factor, float correction1,
+                     float correction2, int32_t maximize,
+                     int32_t update_parameter, uint64_t count, void *stream);
+
+/* ---- multi-tensor plans ------------------------------------------------ */
+
+/*
+ * Build a plan over `n` tensors on `device`: uploads the descriptor table
+ * and a workgroup->(tensor, chunk) task map.  Replaces the per-parameter
+ * Python loop of _FirstOrderOptimizer.step (optim/_common.py:165-166) and
+ * the per-gradient loops of GradScaler.unscale_/_finite (amp.py:152-192)
+ * and _total_norm (optim/clip_grad.py:63-79) with one launch per pass.
+ * `chunk` is the elements per workgroup task (0 = default).  The tables
+ * are staged in pinned host memory owned by the plan and copied
+ * asynchronously on `stream`, so creation does not wait for queued work.
+ * nt_plan_destroy() waits for the device before freeing.
+ */
+int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
+                       const nt_mt_layout *layout, int64_t chunk,
+                       void *stream, nt_plan **out);
+int32_t nt_plan_destroy(nt_plan *plan);
+
+/* Elements, tensors and workgroup tasks in a plan. */
+int32_t nt_plan_info(const nt_plan *plan, uint64_t *numel, int32_t *tensors,
+                     int64_t *tasks);
+
+/*
+ * Pass 2: multi-tensor AdamW over every tensor of `plan` in one launch.
+ * `slots[nslots]` holds the coefficient sets tensors select by `slot`
+ * (fp32 params: nt_adamw_coefs; fp64 params: nt_adamw_coefs64).  The
+ * element arithmetic is the reference's, operation for operation and
+ * without FMA contraction (backends/cuda/adamw.py:15-25 ==
+ * optim/adam.py:35-42 + optim/_common.py:67-73).  `xform` may be NULL.
+ */
+int32_t nt_adamw_mt(nt_plan *plan, const void *slots, int32_t nslots,
+                    const nt_grad_xform *xform, void *stream);
+
+/*
+ * Pass 1 of an AMP/clip iteration over the grads of `plan`: per element
+ * g' = to_grad_dtype(f32(g) / scale) when `unscale` (amp.py:190-191),
+ * finiteness of g' (amp.py:152-167) and the fp64 sum of squares and max of
+ * |g'| (optim/clip_grad.py:63-79).  Writes per-workgroup partials into the
+ * plan's workspace; grads are not written.  With `ctrl != NULL` the scale
+ * is read from ctrl->scale on the device (the sync-free path).
+ */
+int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale,
+                       const nt_amp_ctrl *ctrl, void *stream);
+
+/*
+ * Stage 2: reduce the partials of the last nt_amp_prepass in a fixed order
+ * into `ctrl` (device memory).  norm_type 2 or +inf; other norm types call
+ * nt_grad_norm_pow afterwards.  With `max_norm >= 0` also computes
+ * clip_coef = max_norm / (norm + 1e-6) and clip = clip_coef < 1
+ * (optim/clip_grad.py:106-107).  Always sets skip = found_inf and
+ * scale_used = scale.  With `scaler_update` the GradScaler state machine
+ * of amp.py:225-233 then runs on the device, advancing ctrl->scale and
+ * ctrl->growth_tracker.
+ */
+int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type,
+                        double max_norm, int32_t scaler_update,
+                        double growth_factor, double backoff_factor,
+                        int32_t growth_interval, void *stream);
+
+/*
+ * General p-norm (0 < p < inf, p != 2) of optim/clip_grad.py:70-79:
+ * sum over grads of (|g'|/amax)^p in fp64, with amax from the previous
+ * prepass already in `ctrl`; leaves the norm in ctrl->norm, the raw sum
+ * in ctrl->sumsq and, with max_norm >= 0, the clip coefficient.  A
+ * non-finite or zero amax leaves the block as nt_amp_finalize wrote it.
+ */
+int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type,
+                         double max_norm, float scale, int32_t unscale,
+                         int32_t scale_from_ctrl, void *stream);
+
+/*
+ * Write the transformed grads back in place: the deferred form of
+ * GradScaler.unscale_'s grad.copy_(grad / scale) (amp.py:191) and of
+ * clip_grad_norm_'s grad.copy_(f64(grad) * coef) (optim/clip_grad.py:111).
+ */
+int32_t nt_grad_apply(nt_plan *plan, const nt_grad_xform *xform,
+                      void *stream);
+
+/* Set ctrl->scale / growth_tracker and clear every other field (a kernel,
+ * not a memset, so the call can be captured in a HIP graph). */
+int32_t nt_ctrl_reset(nt_amp_ctrl *ctrl, float scale, int32_t growth_tracker,
+                      void *stream);
+
+/* ---- small single-array kernels ---------------------------------------- */
+
+/*
+ * out[i] = to_dtype(in[i] * scale) for a loss of `count` elements
+ * (GradScaler.scale, amp.py:137-138: loss * self._scale); with
+ * `ctrl != NULL` the scale is ctrl->scale.
+ */
+int32_t nt_scale_array(const void *in, void *out, int32_t dtype,
+                       double scale, const nt_amp_ctrl *ctrl, uint64_t count,
+                       void *stream);
+
+/*
+ * *flag = 1 if any element of `array` is < 0 (the exp_avg_sq check of
+ * _check_state, optim/_common.py:114-115); `flag` is device memory and is
+ * cleared first.
+ */
+int32_t nt_any_negative(const void *array, int32_t dtype, uint64_t count,
+                        int32_t *flag, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NAMITORCH_AMD_H */

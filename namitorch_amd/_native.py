@@ -1,0 +1,181 @@
+"""ctypes binding of ``libnamitorch_amd.so`` (the C ABI in ``include/namitorch_amd.h``).
+
+The library is loaded on first use from ``namitorch_amd/_lib``.  There is no
+fallback: when the library is missing every device operation raises
+:class:`NativeLibraryError`, which names the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libnamitorch_amd.so"
+
+NT_OK = 0
+NT_ERR_VALUE = -1
+NT_ERR_TYPE = -2
+NT_ERR_RUNTIME = -3
+NT_ERR_HIP = -4
+
+NT_DTYPE_NONE = -1
+NT_F32 = 0
+NT_F16 = 1
+NT_BF16 = 2
+NT_F64 = 3
+
+NT_MAX_SLOTS = 16
+ABI_VERSION = 1
+
+c_void_p = ctypes.c_void_p
+c_int32 = ctypes.c_int32
+c_int64 = ctypes.c_int64
+c_uint64 = ctypes.c_uint64
+c_float = ctypes.c_float
+c_double = ctypes.c_double
+
+
+class NativeLibraryError(RuntimeError):
+    """The gfx950 library is not built or cannot be loaded."""
+
+
+class MtTensor(ctypes.Structure):
+    _fields_ = [
+        ("param", c_void_p),
+        ("grad", c_void_p),
+        ("exp_avg", c_void_p),
+        ("exp_avg_sq", c_void_p),
+        ("model_copy", c_void_p),
+        ("numel", c_uint64),
+        ("slot", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+class MtLayout(ctypes.Structure):
+    _fields_ = [
+        ("param_dtype", c_int32),
+        ("grad_dtype", c_int32),
+        ("state_dtype", c_int32),
+        ("copy_dtype", c_int32),
+    ]
+
+
+class AdamWCoefs(ctypes.Structure):
+    _fields_ = [(name, c_float) for name in (
+        "lr", "beta1", "beta2", "complement1", "complement2",
+        "eps", "weight_decay", "decay_factor", "correction1", "correction2",
+    )] + [("maximize", c_int32), ("update_parameter", c_int32), ("coupled_weight_decay", c_int32), ("reserved", c_int32)]
+
+
+class AdamWCoefs64(ctypes.Structure):
+    _fields_ = [(name, c_double) for name in (
+        "lr", "beta1", "beta2", "complement1", "complement2",
+        "eps", "weight_decay", "decay_factor", "correction1", "correction2",
+    )] + [("maximize", c_int32), ("update_parameter", c_int32), ("coupled_weight_decay", c_int32), ("reserved", c_int32)]
+
+
+class AmpCtrl(ctypes.Structure):
+    _fields_ = [
+        ("sumsq", c_double),
+        ("amax", c_double),
+        ("norm", c_double),
+        ("clip_coef", c_double),
+        ("scale", c_float),
+        ("scale_used", c_float),
+        ("found_inf", c_int32),
+        ("has_nan", c_int32),
+        ("clip", c_int32),
+        ("skip", c_int32),
+        ("growth_tracker", c_int32),
+        ("iterations", c_int32),
+        ("skipped", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+class GradXform(ctypes.Structure):
+    _fields_ = [
+        ("scale", c_float),
+        ("unscale", c_int32),
+        ("clip_coef", c_double),
+        ("clip", c_int32),
+        ("honor_skip", c_int32),
+        ("ctrl", c_void_p),
+    ]
+
+
+assert ctypes.sizeof(MtTensor) == 56
+assert ctypes.sizeof(AdamWCoefs) == 56
+assert ctypes.sizeof(AdamWCoefs64) == 96
+assert ctypes.sizeof(AmpCtrl) == 72
+assert ctypes.sizeof(GradXform) == 32
+
+# name -> (restype, argtypes); every entry point returns an int32 status.
+SIGNATURES = {
+    "nt_last_error": (ctypes.c_char_p, []),
+    "nt_abi_version": (c_int32, []),
+    "nt_device_count": (c_int32, [ctypes.POINTER(c_int32)]),
+    "nt_device_arch": (c_int32, [c_int32, ctypes.c_char_p, c_int32]),
+    "nt_stream_synchronize": (c_int32, [c_void_p]),
+    "nt_memcpy_d2h": (c_int32, [c_void_p, c_void_p, c_uint64, c_void_p]),
+    "nt_memcpy_h2d": (c_int32, [c_void_p, c_void_p, c_uint64, c_void_p]),
+    "nt_adamw_f32": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p] + [c_float] * 10 + [c_int32, c_int32, c_uint64, c_void_p]),
+    "nt_plan_create": (c_int32, [c_int32, ctypes.POINTER(MtTensor), c_int32, ctypes.POINTER(MtLayout), c_int64, c_void_p, ctypes.POINTER(c_void_p)]),
+    "nt_plan_destroy": (c_int32, [c_void_p]),
+    "nt_plan_info": (c_int32, [c_void_p, ctypes.POINTER(c_uint64), ctypes.POINTER(c_int32), ctypes.POINTER(c_int64)]),
+    "nt_adamw_mt": (c_int32, [c_void_p, c_void_p, c_int32, ctypes.POINTER(GradXform), c_void_p]),
+    "nt_amp_prepass": (c_int32, [c_void_p, c_float, c_int32, c_void_p, c_void_p]),
+    "nt_amp_finalize": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_int32, c_double, c_double, c_int32, c_void_p]),
+    "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_void_p]),
+    "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
+    "nt_ctrl_reset": (c_int32, [c_void_p, c_float, c_int32, c_void_p]),
+    "nt_scale_array": (c_int32, [c_void_p, c_void_p, c_int32, c_double, c_void_p, c_uint64, c_void_p]),
+    "nt_any_negative": (c_int32, [c_void_p, c_int32, c_uint64, c_void_p, c_void_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the library (once) and declare every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise NativeLibraryError(
+                f"{LIB_PATH} is missing; build it with `python -m namitorch_amd.build` "
+                "(hipcc --offload-arch=gfx950)."
+            )
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as error:
+            raise NativeLibraryError(f"cannot load {LIB_PATH}: {error}") from error
+        for name, (restype, argtypes) in SIGNATURES.items():
+            function = getattr(lib, name)
+            function.restype = restype
+            function.argtypes = argtypes
+        if lib.nt_abi_version() != ABI_VERSION:
+            raise NativeLibraryError(f"{LIB_PATH} has ABI {lib.nt_abi_version()}, expected {ABI_VERSION}; rebuild it.")
+        _lib = lib
+        return lib
+
+
+_ERRORS = {NT_ERR_VALUE: ValueError, NT_ERR_TYPE: TypeError, NT_ERR_RUNTIME: RuntimeError, NT_ERR_HIP: RuntimeError}
+
+
+def check(status: int) -> None:
+    """Raise the exception class a negative status code names."""
+    if status == NT_OK:
+        return
+    message = load().nt_last_error().decode("utf-8", "replace")
+    raise _ERRORS.get(status, RuntimeError)(message)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

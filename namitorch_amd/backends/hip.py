@@ -1,0 +1,285 @@
+"""HIP (MI355X) device backend.
+
+Protocol of the reference's CUDA backend object
+(namitorch/backends/cuda/__init__.py:23-225) as far as the optimizer step
+uses it: ``device``, ``context``, ``result``, ``item``, ``writable`` and the
+optional kernel attribute ``adamw``.  Storage arrays are torch tensors on
+the device; every operation launches the gfx950 kernels of
+``libnamitorch_amd.so`` on torch's current stream for the device.
+
+Multi-tensor plans (descriptor table + workgroup task map, see
+``include/namitorch_amd.h``) are cached per backend, keyed by the raw
+pointers, sizes, dtypes and coefficient slots they were built from; a key
+match means the cached device tables describe exactly the current buffers.
+"""
+
+from __future__ import annotations
+
+import atexit
+import ctypes
+import math
+import threading
+import weakref
+from collections import OrderedDict
+from contextlib import contextmanager
+
+import numpy as np
+import torch
+
+from .. import _native
+from ..device import Device
+
+PLAN_CACHE_SIZE = 16
+DEFAULT_CHUNK = 16384
+_backends_alive: "weakref.WeakSet[HIPBackend]" = weakref.WeakSet()
+_shutting_down = False
+
+
+@atexit.register
+def _release_plans() -> None:
+    """Free cached plans while the HIP runtime is still up (before interpreter teardown)."""
+    global _shutting_down
+    for backend in list(_backends_alive):
+        with backend._lock:
+            backend._plans.clear()
+    _shutting_down = True
+
+
+class Plan:
+    """A multi-tensor plan owned by the library; destroyed with this object."""
+
+    __slots__ = ("handle", "numel", "ntensors", "ntasks", "layout", "__weakref__")
+
+    def __init__(self, handle: int, layout: tuple):
+        self.handle = handle
+        self.layout = layout
+        numel = ctypes.c_uint64()
+        tensors = ctypes.c_int32()
+        tasks = ctypes.c_int64()
+        _native.call("nt_plan_info", handle, ctypes.byref(numel), ctypes.byref(tensors), ctypes.byref(tasks))
+        self.numel = numel.value
+        self.ntensors = tensors.value
+        self.ntasks = tasks.value
+
+    def __del__(self):
+        handle, self.handle = self.handle, None
+        if handle and not _shutting_down:
+            try:
+                _native.load().nt_plan_destroy(handle)
+            except Exception:
+                pass
+
+
+class AdamWHIPKernel:
+    """The reference's per-tensor fused AdamW hook (backends/cuda/adamw.py:32-73).
+
+    Arguments are raw storage arrays (torch tensors on this device), exactly
+    as the reference passes ``._data``; the caller owns version counters and
+    ``state['step']``.
+    """
+
+    def __init__(self, backend: "HIPBackend"):
+        self._backend = backend
+
+    def supports(self, parameter, gradient, first=None, second=None) -> bool:
+        arrays = (parameter, gradient, first, second)
+        if parameter is None or gradient is None:
+            return False
+        present = tuple(array for array in arrays if array is not None)
+        index = self._backend.device.index
+        for array in present:
+            if not isinstance(array, torch.Tensor):
+                return False
+            if array.device.type != "cuda" or array.device.index != index or array.dtype != torch.float32:
+                return False
+            if not array.is_contiguous() or array.data_ptr() % 4 or tuple(array.shape) != tuple(parameter.shape):
+                return False
+        ranges = [(array.data_ptr(), array.data_ptr() + array.numel() * 4) for array in present if array.numel()]
+        return not any(
+            max(start, other_start) < min(end, other_end)
+            for position, (start, end) in enumerate(ranges)
+            for other_start, other_end in ranges[position + 1:]
+        )
+
+    def run(self, parameter, gradient, first, second, *, coefficients, maximize, update_parameter) -> bool:
+        if first is None or second is None or not self.supports(parameter, gradient, first, second):
+            raise RuntimeError("Fused AdamW requires non-overlapping contiguous float32 CUDA arrays with identical shapes and device.")
+        if len(coefficients) != 10 or any(not isinstance(value, np.float32) or not np.isfinite(value) for value in coefficients):
+            raise ValueError("Fused AdamW requires ten finite float32 coefficients.")
+        if coefficients[5] <= 0 or coefficients[8] <= 0 or coefficients[9] <= 0:
+            raise ValueError("Fused AdamW eps and bias corrections must be positive.")
+        if type(maximize) is not bool or type(update_parameter) is not bool:
+            raise TypeError("Fused AdamW flags must be Python bools.")
+        count = parameter.numel()
+        if count == 0:
+            return False
+        with self._backend.context():
+            _native.call(
+                "nt_adamw_f32",
+                parameter.data_ptr(), gradient.data_ptr(), first.data_ptr(), second.data_ptr(),
+                *(float(value) for value in coefficients),
+                int(maximize), int(update_parameter), count, self._backend.stream(),
+            )
+        return True
+
+
+class HIPBackend:
+    def __init__(self, device: Device):
+        lib = _native.load()
+        count = ctypes.c_int32()
+        _native.check(lib.nt_device_count(ctypes.byref(count)))
+        if device.index >= count.value:
+            raise RuntimeError(f"CUDA device {device} is unavailable; found {count.value} CUDA devices.")
+        self.device = device
+        self.adamw = AdamWHIPKernel(self)
+        self._plans: OrderedDict = OrderedDict()
+        self._lock = threading.RLock()
+        _backends_alive.add(self)
+
+    def __repr__(self):
+        return f"HIPBackend({self.device})"
+
+    # ---- reference protocol --------------------------------------------------------------
+    @contextmanager
+    def context(self, *operands):
+        with torch.cuda.device(self.device.index):
+            yield
+
+    def result(self, value):
+        return value
+
+    def item(self, array):
+        return array.item()
+
+    def writable(self, array):
+        return True
+
+    # ---- streams ---------------------------------------------------------------------------
+    def stream(self) -> int:
+        """Handle of torch's current stream on this device (a hipStream_t)."""
+        return torch.cuda.current_stream(self.device.index).cuda_stream
+
+    def synchronize(self) -> None:
+        _native.call("nt_stream_synchronize", self.stream())
+
+    # ---- plans -----------------------------------------------------------------------------
+    def plan(self, rows: list[tuple], layout: tuple, chunk: int = 0) -> Plan:
+        """Plan for rows of (param, grad, exp_avg, exp_avg_sq, copy, numel, slot)
+        raw pointers (0 = absent); cached by content."""
+        key = (layout, chunk, tuple(rows))
+        with self._lock:
+            plan = self._plans.get(key)
+            if plan is not None:
+                self._plans.move_to_end(key)
+                return plan
+            table = (_native.MtTensor * max(1, len(rows)))()
+            for index, (param, grad, first, second, copy, numel, slot) in enumerate(rows):
+                table[index] = _native.MtTensor(param or None, grad or None, first or None, second or None, copy or None, numel, slot, 0)
+            spec = _native.MtLayout(*layout)
+            handle = ctypes.c_void_p()
+            with self.context():
+                _native.call("nt_plan_create", self.device.index, table, len(rows), ctypes.byref(spec), chunk, self.stream(), ctypes.byref(handle))
+            plan = Plan(handle.value, layout)
+            self._plans[key] = plan
+            while len(self._plans) > PLAN_CACHE_SIZE:
+                self._plans.popitem(last=False)
+            return plan
+
+    # ---- multi-tensor kernels --------------------------------------------------------------
+    def adamw_multi(self, plan: Plan, slots, xform: _native.GradXform | None) -> None:
+        with self.context():
+            _native.call("nt_adamw_mt", plan.handle, ctypes.byref(slots), len(slots),
+                         None if xform is None else ctypes.byref(xform), self.stream())
+
+    def grad_prepass(self, plan: Plan, scale: float | None, ctrl_ptr: int | None = None, unscale: bool = False) -> None:
+        with self.context():
+            _native.call("nt_amp_prepass", plan.handle, 1.0 if scale is None else scale,
+                         int(unscale or scale is not None), ctrl_ptr, self.stream())
+
+    def grad_finalize(self, plan: Plan, ctrl_ptr: int, norm_type: float = 2.0, max_norm: float = -1.0,
+                      scaler_update: bool = False, growth: float = 2.0, backoff: float = 0.5, interval: int = 2000) -> None:
+        with self.context():
+            _native.call("nt_amp_finalize", plan.handle, ctrl_ptr, norm_type, max_norm, int(scaler_update),
+                         growth, backoff, interval, self.stream())
+
+    def grad_norm_pow(self, plan: Plan, ctrl_ptr: int, norm_type: float, max_norm: float,
+                      scale: float | None, scale_from_ctrl: bool = False) -> None:
+        with self.context():
+            _native.call("nt_grad_norm_pow", plan.handle, ctrl_ptr, norm_type, max_norm,
+                         1.0 if scale is None else scale, int(scale is not None or scale_from_ctrl),
+                         int(scale_from_ctrl), self.stream())
+
+    def grad_apply(self, plan: Plan, xform: _native.GradXform) -> None:
+        with self.context():
+            _native.call("nt_grad_apply", plan.handle, ctypes.byref(xform), self.stream())
+
+    # ---- control blocks ----------------------------------------------------------------------
+    def new_ctrl(self, scale: float = 1.0, growth_tracker: int = 0) -> torch.Tensor:
+        block = torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, device=self.device.torch)
+        self.reset_ctrl(block, scale, growth_tracker)
+        return block
+
+    def reset_ctrl(self, block: torch.Tensor, scale: float, growth_tracker: int = 0) -> None:
+        with self.context():
+            _native.call("nt_ctrl_reset", block.data_ptr(), scale, growth_tracker, self.stream())
+
+    def read_ctrl(self, block: torch.Tensor) -> _native.AmpCtrl:
+        out = _native.AmpCtrl()
+        with self.context():
+            _native.call("nt_memcpy_d2h", ctypes.addressof(out), block.data_ptr(), ctypes.sizeof(out), self.stream())
+        return out
+
+    # ---- single-tensor helpers --------------------------------------------------------------
+    def grad_rows(self, tensors) -> list[tuple]:
+        return [(0, tensor._ptr, 0, 0, 0, tensor.size, 0) for tensor in tensors]
+
+    def apply_grad_transform(self, tensors, transform) -> None:
+        """Write pending GradTransforms back in place (one launch per dtype)."""
+        by_dtype: dict = {}
+        for tensor in tensors:
+            by_dtype.setdefault(tensor.dtype, []).append(tensor)
+        for dtype, group in by_dtype.items():
+            layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
+            plan = self.plan(self.grad_rows(group), layout)
+            self.grad_apply(plan, make_xform(transform))
+
+    def scale_tensor(self, tensor, scale: float, ctrl: torch.Tensor | None = None):
+        from ..tensor import Tensor
+        if tensor.dtype.code == _native.NT_DTYPE_NONE:
+            raise TypeError("Only floating Tensors can be scaled on the device.")
+        out = torch.empty_like(tensor._data)
+        with self.context():
+            _native.call("nt_scale_array", tensor._data.data_ptr(), out.data_ptr(), tensor.dtype.code, float(scale),
+                         None if ctrl is None else ctrl.data_ptr(), tensor.size, self.stream())
+        return Tensor._from_storage(out, tensor.requires_grad)
+
+    def any_negative(self, array: torch.Tensor, code: int) -> bool:
+        flag = torch.empty(1, dtype=torch.int32, device=self.device.torch)
+        with self.context():
+            _native.call("nt_any_negative", array.data_ptr(), code, array.numel(), flag.data_ptr(), self.stream())
+        return bool(flag.item())
+
+
+def make_xform(transform, ctrl_ptr: int | None = None, honor_skip: bool = False) -> _native.GradXform:
+    """C-ABI grad transform from a GradTransform (or from a device ctrl block)."""
+    xform = _native.GradXform()
+    xform.scale = 1.0
+    xform.clip_coef = 1.0
+    if transform is not None:
+        if transform.scale is not None:
+            xform.scale = transform.scale
+            xform.unscale = 1
+        if transform.clip is not None:
+            xform.clip = 1
+            xform.clip_coef = transform.clip
+    xform.honor_skip = int(honor_skip)
+    xform.ctrl = ctrl_ptr
+    return xform
+
+
+def is_power_of_two(value: float) -> bool:
+    mantissa, _ = math.frexp(value)
+    return mantissa == 0.5
+
+
+__all__ = ["HIPBackend", "AdamWHIPKernel", "Plan", "make_xform"]

@@ -1,0 +1,346 @@
+// nt_adamw.hip — AdamW update kernels for gfx950.
+//
+// Element arithmetic follows the reference operation for operation
+// (backends/cuda/adamw.py:15-25, identical to the NumPy path of
+// optim/adam.py:35-42 + optim/_common.py:67-73):
+//
+//   g   = maximize ? -g : g
+//   g   = g + wd*p                      (Adam only: coupled L2 decay)
+//   m   = (b1*m) + (c1*g)
+//   v   = (b2*v) + ((c2*g)*g)
+//   if update_parameter:
+//     p   = (wd != 0) ? p*decay : p      (AdamW only: decoupled decay)
+//     p   = p - lr*((m/bc1) / (sqrt(v/bc2) + eps))
+//
+// Every operation rounds to fp32 (no FMA contraction, IEEE divide and
+// sqrt), so results are bit-identical to NumPy on the same inputs.  For
+// float16 parameters each operation additionally rounds to fp16, which is
+// what NumPy's float16 ufuncs compute; float64 parameters use fp64.
+#include <hip/hip_runtime.h>
+
+#include "nt_internal.hpp"
+
+namespace nt {
+
+// Rounding policy after every arithmetic operation.
+struct RoundF32 {
+    __device__ static float r(float x) { return x; }
+};
+struct RoundF16 {
+    __device__ static float r(float x) { return TF16::round_f32(x); }
+};
+
+template <class R>
+__device__ __forceinline__ void adamw_elem(float &p, float g, float &m, float &v,
+                                           const nt_adamw_coefs &c) {
+    if (c.maximize) g = -g;
+    if (c.coupled_weight_decay && c.weight_decay != 0.0f) g = R::r(g + R::r(c.weight_decay * p));
+    m = R::r(R::r(c.beta1 * m) + R::r(c.complement1 * g));
+    v = R::r(R::r(c.beta2 * v) + R::r(R::r(c.complement2 * g) * g));
+    if (c.update_parameter) {
+        float value = p;
+        if (!c.coupled_weight_decay && c.weight_decay != 0.0f) value = R::r(value * c.decay_factor);
+        float corrected = R::r(m / c.correction1);
+        float denominator = R::r(R::r(__builtin_sqrtf(R::r(v / c.correction2))) + c.eps);
+        p = R::r(value - R::r(c.lr * R::r(corrected / denominator)));
+    }
+}
+
+__device__ __forceinline__ void adamw_elem64(double &p, double g, double &m, double &v,
+                                             const nt_adamw_coefs64 &c) {
+    if (c.maximize) g = -g;
+    if (c.coupled_weight_decay && c.weight_decay != 0.0) g = g + c.weight_decay * p;
+    m = c.beta1 * m + c.complement1 * g;
+    v = c.beta2 * v + (c.complement2 * g) * g;
+    if (c.update_parameter) {
+        double value = p;
+        if (!c.coupled_weight_decay && c.weight_decay != 0.0) value *= c.decay_factor;
+        double corrected = m / c.correction1;
+        double denominator = __builtin_sqrt(v / c.correction2) + c.eps;
+        p = value - c.lr * (corrected / denominator);
+    }
+}
+
+// ---- per-tensor kernel: the reference kernel's ABI ------------------------------
+// 8 elements per thread per iteration with 128-bit accesses when all four
+// pointers are 16-byte aligned; grid-stride over the tensor.
+__global__ __launch_bounds__(kBlock) void adamw_f32_kernel(
+    float *__restrict__ param, const float *__restrict__ grad, float *__restrict__ m1,
+    float *__restrict__ m2, nt_adamw_coefs c, uint64_t count, int vectorized) {
+    const uint64_t tid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
+    uint64_t scalar_from = 0;
+    if (vectorized) {
+        const uint64_t nvec = count / kVec;
+        for (uint64_t v = tid; v < nvec; v += nthreads) {
+            const uint64_t i = v * kVec;
+            float p[kVec], g[kVec], a[kVec], b[kVec];
+            Vec8IO<TF32, true>::load(grad, i, g);
+            Vec8IO<TF32, true>::load(m1, i, a);
+            Vec8IO<TF32, true>::load(m2, i, b);
+            if (c.update_parameter) Vec8IO<TF32, true>::load(param, i, p);
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) adamw_elem<RoundF32>(p[k], g[k], a[k], b[k], c);
+            Vec8IO<TF32, true>::store(m1, i, a);
+            Vec8IO<TF32, true>::store(m2, i, b);
+            if (c.update_parameter) Vec8IO<TF32, true>::store(param, i, p);
+        }
+        scalar_from = nvec * kVec;
+    }
+    for (uint64_t i = scalar_from + tid; i < count; i += nthreads) {
+        float p = c.update_parameter ? param[i] : 0.0f, a = m1[i], b = m2[i];
+        adamw_elem<RoundF32>(p, grad[i], a, b, c);
+        m1[i] = a;
+        m2[i] = b;
+        if (c.update_parameter) param[i] = p;
+    }
+}
+
+// ---- multi-tensor kernel ------------------------------------------------------------
+struct MtArgs {
+    nt_adamw_coefs slots[NT_MAX_SLOTS];
+    Xform xf;
+    const nt_amp_ctrl *ctrl;
+    int64_t chunk;
+    int32_t honor_skip;
+};
+
+struct MtArgs64 {
+    nt_adamw_coefs64 slots[NT_MAX_SLOTS];
+    Xform xf;
+    const nt_amp_ctrl *ctrl;
+    int64_t chunk;
+    int32_t honor_skip;
+};
+
+// Transform parameters from the device control block (sync-free path).
+__device__ __forceinline__ bool xform_from_ctrl(const nt_amp_ctrl *ctrl, int honor_skip, Xform &xf) {
+    if (ctrl == nullptr) return true;
+    if (honor_skip && ctrl->skip) return false;
+    if (xf.unscale) {
+        const float s = ctrl->scale_used;
+        const uint32_t b = f32_bits(s);
+        const uint32_t e = (b >> 23) & 0xffu;
+        xf.scale = s;
+        if ((b & 0x807fffffu) == 0u && e >= 1u && e <= 253u) {
+            xf.unscale = 2;                       // power of two: exact inverse
+            xf.inv_scale = bits_f32((254u - e) << 23);
+        } else {
+            xf.unscale = 1;
+        }
+    }
+    xf.clip = ctrl->clip;
+    xf.clip_coef = ctrl->clip_coef;
+    return true;
+}
+
+template <class P, class G, class S, class C, class R, bool HAS_COPY>
+__global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__restrict__ tensors,
+                                                          const Task *__restrict__ tasks, MtArgs args) {
+    Xform xf = args.xf;
+    if (!xform_from_ctrl(args.ctrl, args.honor_skip, xf)) return;
+    const Task task = tasks[blockIdx.x];
+    const DevTensor d = tensors[task.tensor];
+    const nt_adamw_coefs c = args.slots[d.slot];
+    const uint64_t start = (uint64_t)task.chunk * (uint64_t)args.chunk;
+    const uint64_t end = min(start + (uint64_t)args.chunk, d.numel);
+
+    auto *pp = reinterpret_cast<typename P::raw *>(d.param);
+    auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
+    auto *ap = reinterpret_cast<typename S::raw *>(d.exp_avg);
+    auto *bp = reinterpret_cast<typename S::raw *>(d.exp_avg_sq);
+    auto *cp = reinterpret_cast<typename C::raw *>(d.model_copy);
+    const bool update = c.update_parameter != 0;
+    const bool read_param = update || (c.coupled_weight_decay && c.weight_decay != 0.0f);
+
+    uint64_t scalar_from = start;
+    if (d.flags & kAligned16) {
+        const uint64_t vend = start + ((end - start) / kVec) * kVec;
+        for (uint64_t i = start + (uint64_t)threadIdx.x * kVec; i < vend; i += (uint64_t)kBlock * kVec) {
+            float p[kVec], g[kVec], a[kVec], b[kVec];
+            Vec8IO<G, true>::load(gp, i, g);
+            Vec8IO<S, true>::load(ap, i, a);
+            Vec8IO<S, true>::load(bp, i, b);
+            if (read_param) Vec8IO<P, true>::load(pp, i, p);
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) {
+                float gk = clip_one<G>(unscale_one<G>(g[k], xf), xf);
+                adamw_elem<R>(p[k], gk, a[k], b[k], c);
+            }
+            if constexpr (S::code != NT_F32) {
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) { a[k] = S::round_f32(a[k]); b[k] = S::round_f32(b[k]); }
+            }
+            Vec8IO<S, true>::store(ap, i, a);
+            Vec8IO<S, true>::store(bp, i, b);
+            if (update) {
+                Vec8IO<P, true>::store(pp, i, p);
+                if constexpr (HAS_COPY) {
+#pragma unroll
+                    for (int k = 0; k < kVec; ++k) p[k] = C::round_f32(p[k]);
+                    Vec8IO<C, true>::store(cp, i, p);
+                }
+            }
+        }
+        scalar_from = vend;
+    }
+    for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock) {
+        float p = read_param ? load1<P>(pp, i) : 0.0f;
+        float a = load1<S>(ap, i), b = load1<S>(bp, i);
+        float g = clip_one<G>(unscale_one<G>(load1<G>(gp, i), xf), xf);
+        adamw_elem<R>(p, g, a, b, c);
+        store1<S>(ap, i, a);
+        store1<S>(bp, i, b);
+        if (update) {
+            store1<P>(pp, i, p);
+            if constexpr (HAS_COPY) store1<C>(cp, i, p);
+        }
+    }
+}
+
+// float64 parameters, grads and states (array path).
+__global__ __launch_bounds__(kBlock) void adamw_mt_f64_kernel(const DevTensor *__restrict__ tensors,
+                                                              const Task *__restrict__ tasks, MtArgs64 args) {
+    Xform xf = args.xf;
+    if (!xform_from_ctrl(args.ctrl, args.honor_skip, xf)) return;
+    const Task task = tasks[blockIdx.x];
+    const DevTensor d = tensors[task.tensor];
+    const nt_adamw_coefs64 c = args.slots[d.slot];
+    const uint64_t start = (uint64_t)task.chunk * (uint64_t)args.chunk;
+    const uint64_t end = min(start + (uint64_t)args.chunk, d.numel);
+    double *pp = reinterpret_cast<double *>(d.param);
+    const double *gp = reinterpret_cast<const double *>(d.grad);
+    double *ap = reinterpret_cast<double *>(d.exp_avg);
+    double *bp = reinterpret_cast<double *>(d.exp_avg_sq);
+    for (uint64_t i = start + threadIdx.x; i < end; i += kBlock) {
+        double g = gp[i];
+        if (xf.unscale) g = g / (double)xf.scale;
+        if (xf.clip) g = g * xf.clip_coef;
+        double p = (c.update_parameter || c.coupled_weight_decay) ? pp[i] : 0.0, a = ap[i], b = bp[i];
+        adamw_elem64(p, g, a, b, c);
+        ap[i] = a;
+        bp[i] = b;
+        if (c.update_parameter) pp[i] = p;
+    }
+}
+
+// Dummy trait for "no model copy".
+struct TNone {
+    using raw = uint16_t;
+    static constexpr int code = NT_DTYPE_NONE;
+    __device__ static float to_f32(raw) { return 0.0f; }
+    __device__ static raw from_f32(float) { return 0; }
+    __device__ static float round_f32(float x) { return x; }
+};
+
+template <class P, class G, class S, class C, class R, bool HAS_COPY>
+static int32_t launch_mt(nt_plan *plan, const MtArgs &args, hipStream_t stream) {
+    adamw_mt_kernel<P, G, S, C, R, HAS_COPY><<<dim3((unsigned)plan->ntasks), dim3(kBlock), 0, stream>>>(
+        plan->d_tensors, plan->d_tasks, args);
+    NT_LAUNCH_CHECK("adamw_mt_kernel launch");
+    return NT_OK;
+}
+
+template <class G, class S>
+static int32_t dispatch_copy(nt_plan *plan, const MtArgs &args, hipStream_t stream) {
+    switch (plan->layout.copy_dtype) {
+        case NT_DTYPE_NONE: return launch_mt<TF32, G, S, TNone, RoundF32, false>(plan, args, stream);
+        case NT_BF16: return launch_mt<TF32, G, S, TBF16, RoundF32, true>(plan, args, stream);
+        case NT_F16: return launch_mt<TF32, G, S, TF16, RoundF32, true>(plan, args, stream);
+        case NT_F32: return launch_mt<TF32, G, S, TF32, RoundF32, true>(plan, args, stream);
+        default: return fail(NT_ERR_TYPE, "unsupported model-copy dtype for fp32 AdamW");
+    }
+}
+
+template <class G>
+static int32_t dispatch_state(nt_plan *plan, const MtArgs &args, hipStream_t stream) {
+    switch (plan->layout.state_dtype) {
+        case NT_F32: return dispatch_copy<G, TF32>(plan, args, stream);
+        case NT_BF16: return dispatch_copy<G, TBF16>(plan, args, stream);
+        default: return fail(NT_ERR_TYPE, "unsupported optimizer-state dtype for fp32 AdamW");
+    }
+}
+
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int32_t nt_adamw_f32(float *parameter, const float *gradient, float *exp_avg, float *exp_avg_sq, float lr,
+                     float beta1, float beta2, float complement1, float complement2, float eps,
+                     float weight_decay, float decay_factor, float correction1, float correction2,
+                     int32_t maximize, int32_t update_parameter, uint64_t count, void *stream) {
+    clear_error();
+    if (count == 0) return NT_OK;
+    if (gradient == nullptr || exp_avg == nullptr || exp_avg_sq == nullptr || (update_parameter && parameter == nullptr))
+        return fail(NT_ERR_VALUE, "nt_adamw_f32: NULL array");
+    nt_adamw_coefs c{lr, beta1, beta2, complement1, complement2, eps, weight_decay, decay_factor,
+                     correction1, correction2, maximize ? 1 : 0, update_parameter ? 1 : 0, 0, 0};
+    const int vectorized = ((((uintptr_t)parameter | (uintptr_t)gradient | (uintptr_t)exp_avg |
+                               (uintptr_t)exp_avg_sq) & 15u) == 0) ? 1 : 0;
+    // Enough workgroups to fill 256 CUs several times over, capped by the work.
+    const uint64_t per_block = (uint64_t)kBlock * kVec;
+    uint64_t blocks = (count + per_block - 1) / per_block;
+    if (blocks > 8192) blocks = 8192;
+    adamw_f32_kernel<<<dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream>>>(
+        parameter, gradient, exp_avg, exp_avg_sq, c, count, vectorized);
+    NT_LAUNCH_CHECK("adamw_f32_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_adamw_mt(nt_plan *plan, const void *slots, int32_t nslots, const nt_grad_xform *xform, void *stream) {
+    clear_error();
+    int32_t rc = check_plan(plan);
+    if (rc != NT_OK) return rc;
+    if (nslots < 1 || nslots > NT_MAX_SLOTS || slots == nullptr)
+        return fail(NT_ERR_VALUE, "nt_adamw_mt: 1..16 coefficient slots required");
+    if ((uint32_t)nslots <= plan->max_slot)
+        return fail(NT_ERR_VALUE, "nt_adamw_mt: the plan selects coefficient slot " + std::to_string(plan->max_slot) +
+                                      " but only " + std::to_string(nslots) + " slots were given");
+    if (plan->ntasks == 0) return NT_OK;
+    const nt_mt_layout &L = plan->layout;
+    if (L.param_dtype == NT_DTYPE_NONE) return fail(NT_ERR_VALUE, "nt_adamw_mt: plan has no parameters");
+    DeviceGuard guard(plan->device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    hipStream_t s = (hipStream_t)stream;
+
+    if (L.param_dtype == NT_F64) {
+        if (L.grad_dtype != NT_F64 || L.state_dtype != NT_F64 || L.copy_dtype != NT_DTYPE_NONE)
+            return fail(NT_ERR_TYPE, "float64 AdamW requires float64 grads and states");
+        MtArgs64 a{};
+        const nt_adamw_coefs64 *src = static_cast<const nt_adamw_coefs64 *>(slots);
+        for (int i = 0; i < nslots; ++i) a.slots[i] = src[i];
+        a.xf = make_xform(xform);
+        a.ctrl = xform ? xform->ctrl : nullptr;
+        a.honor_skip = xform ? xform->honor_skip : 0;
+        a.chunk = plan->chunk;
+        adamw_mt_f64_kernel<<<dim3((unsigned)plan->ntasks), dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, a);
+        NT_LAUNCH_CHECK("adamw_mt_f64_kernel launch");
+        return NT_OK;
+    }
+
+    MtArgs a{};
+    const nt_adamw_coefs *src = static_cast<const nt_adamw_coefs *>(slots);
+    for (int i = 0; i < nslots; ++i) a.slots[i] = src[i];
+    a.xf = make_xform(xform);
+    a.ctrl = xform ? xform->ctrl : nullptr;
+    a.honor_skip = xform ? xform->honor_skip : 0;
+    a.chunk = plan->chunk;
+
+    if (L.param_dtype == NT_F16) {
+        // float16 parameters: NumPy float16 arithmetic, states and grads float16.
+        if (L.grad_dtype != NT_F16 || L.state_dtype != NT_F16 || L.copy_dtype != NT_DTYPE_NONE)
+            return fail(NT_ERR_TYPE, "float16 AdamW requires float16 grads and states");
+        return launch_mt<TF16, TF16, TF16, TNone, RoundF16, false>(plan, a, s);
+    }
+    if (L.param_dtype != NT_F32) return fail(NT_ERR_TYPE, "unsupported parameter dtype");
+    switch (L.grad_dtype) {
+        case NT_F32: return dispatch_state<TF32>(plan, a, s);
+        case NT_F16: return dispatch_state<TF16>(plan, a, s);
+        case NT_BF16: return dispatch_state<TBF16>(plan, a, s);
+        default: return fail(NT_ERR_TYPE, "unsupported gradient dtype for fp32 AdamW");
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,554 @@
+// nt_amp.hip — gradient pre-pass (unscale + finite check + fp64 norm partials),
+// the single-workgroup finalize, the general p-norm, in-place grad apply and
+// small helpers of the GradScaler path.
+//
+// Reductions are deterministic: every workgroup writes its partial to a
+// fixed slot and one workgroup reduces the slots in a fixed order.  No
+// atomics are used.
+#include <hip/hip_runtime.h>
+
+#include "nt_internal.hpp"
+
+namespace nt {
+
+struct Acc {
+    double sumsq = 0.0;
+    double amax = 0.0;
+    int nan = 0;
+    int inf = 0;
+    __device__ void add(float g) {
+        if (__builtin_isfinite(g)) {
+            const double d = (double)g;
+            sumsq = __builtin_fma(d, d, sumsq);
+            const double a = __builtin_fabs(d);
+            amax = a > amax ? a : amax;
+        } else if (g != g) {
+            nan = 1;
+        } else {
+            inf = 1;
+        }
+    }
+    __device__ void add64(double g) {
+        if (__builtin_isfinite(g)) {
+            sumsq = __builtin_fma(g, g, sumsq);
+            const double a = __builtin_fabs(g);
+            amax = a > amax ? a : amax;
+        } else if (g != g) {
+            nan = 1;
+        } else {
+            inf = 1;
+        }
+    }
+};
+
+// Reduce an Acc over the workgroup; thread 0 gets the result.
+__device__ Acc block_reduce(Acc a) {
+    __shared__ double s_sum[kBlock / 64];
+    __shared__ double s_max[kBlock / 64];
+    __shared__ int s_flags[kBlock / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    double s = wave_sum(a.sumsq);
+    double m = wave_max(a.amax);
+    int f = wave_or(a.nan | (a.inf << 1));
+    if (lane == 0) {
+        s_sum[wave] = s;
+        s_max[wave] = m;
+        s_flags[wave] = f;
+    }
+    __syncthreads();
+    Acc r;
+    if (threadIdx.x == 0) {
+        double ts = 0.0, tm = 0.0;
+        int tf = 0;
+        for (int w = 0; w < kBlock / 64; ++w) {
+            ts += s_sum[w];
+            tm = s_max[w] > tm ? s_max[w] : tm;
+            tf |= s_flags[w];
+        }
+        r.sumsq = ts;
+        r.amax = tm;
+        r.nan = tf & 1;
+        r.inf = (tf >> 1) & 1;
+    }
+    return r;
+}
+
+__device__ __forceinline__ float ctrl_scale_inv(float s, int &mode, float &inv) {
+    const uint32_t b = f32_bits(s);
+    const uint32_t e = (b >> 23) & 0xffu;
+    if ((b & 0x807fffffu) == 0u && e >= 1u && e <= 253u) {
+        mode = 2;
+        inv = bits_f32((254u - e) << 23);
+    } else {
+        mode = 1;
+        inv = 1.0f;
+    }
+    return s;
+}
+
+template <class G>
+__global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__restrict__ tensors,
+                                                         const Task *__restrict__ tasks, int64_t ntasks,
+                                                         int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
+                                                         Partial *__restrict__ partials) {
+    if (ctrl != nullptr && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale, xf.unscale, xf.inv_scale);
+    Acc acc;
+    for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
+        const Task task = tasks[t];
+        const DevTensor d = tensors[task.tensor];
+        const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
+        const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+        const auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
+        uint64_t scalar_from = start;
+        if (d.flags & kAligned16) {
+            const uint64_t vend = start + ((end - start) / kVec) * kVec;
+            for (uint64_t i = start + (uint64_t)threadIdx.x * kVec; i < vend; i += (uint64_t)kBlock * kVec) {
+                float g[kVec];
+                Vec8IO<G, false>::load(gp, i, g);
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) acc.add(unscale_one<G>(g[k], xf));
+            }
+            scalar_from = vend;
+        }
+        for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock)
+            acc.add(unscale_one<G>(load1<G>(gp, i), xf));
+    }
+    Acc r = block_reduce(acc);
+    if (threadIdx.x == 0) {
+        Partial p;
+        p.sumsq = r.sumsq;
+        p.amax = r.amax;
+        p.has_nan = r.nan;
+        p.has_inf = r.inf;
+        p.pad[0] = p.pad[1] = 0;
+        partials[blockIdx.x] = p;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void prepass_f64_kernel(const DevTensor *__restrict__ tensors,
+                                                             const Task *__restrict__ tasks, int64_t ntasks,
+                                                             int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
+                                                             Partial *__restrict__ partials) {
+    double scale = (ctrl != nullptr) ? (double)ctrl->scale : (double)xf.scale;
+    Acc acc;
+    for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
+        const Task task = tasks[t];
+        const DevTensor d = tensors[task.tensor];
+        const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
+        const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+        const double *gp = reinterpret_cast<const double *>(d.grad);
+        for (uint64_t i = start + threadIdx.x; i < end; i += kBlock) {
+            double g = gp[i];
+            if (xf.unscale) g = g / scale;
+            acc.add64(g);
+        }
+    }
+    Acc r = block_reduce(acc);
+    if (threadIdx.x == 0) {
+        Partial p;
+        p.sumsq = r.sumsq;
+        p.amax = r.amax;
+        p.has_nan = r.nan;
+        p.has_inf = r.inf;
+        p.pad[0] = p.pad[1] = 0;
+        partials[blockIdx.x] = p;
+    }
+}
+
+// Reference scaler update (amp.py:225-233): factors applied in fp64, result
+// rounded to fp32 by _scale_value (amp.py:114-119).
+__device__ __forceinline__ void scaler_update(nt_amp_ctrl *c, int found, double growth, double backoff, int interval) {
+    const double tiny = 1.1754943508222875e-38;    // float32 tiny
+    const double fmax = 3.4028234663852886e+38;    // float32 max
+    if (found) {
+        double s = (double)c->scale * backoff;
+        c->scale = (float)(s > tiny ? s : tiny);
+        c->growth_tracker = 0;
+    } else {
+        c->growth_tracker += 1;
+        if (c->growth_tracker == interval) {
+            double s = (double)c->scale * growth;
+            c->scale = (float)(s < fmax ? s : fmax);
+            c->growth_tracker = 0;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restrict__ partials, int32_t n,
+                                                          nt_amp_ctrl *ctrl, double norm_type, double max_norm,
+                                                          int32_t do_update, double growth, double backoff,
+                                                          int32_t interval) {
+    Acc acc;
+    for (int32_t i = threadIdx.x; i < n; i += kBlock) {
+        const Partial p = partials[i];
+        acc.sumsq += p.sumsq;
+        acc.amax = p.amax > acc.amax ? p.amax : acc.amax;
+        acc.nan |= p.has_nan;
+        acc.inf |= p.has_inf;
+    }
+    Acc r = block_reduce(acc);
+    if (threadIdx.x != 0) return;
+    const double nanv = __builtin_nan("");
+    const double infv = __builtin_inf();
+    // _total_norm (optim/clip_grad.py:63-79): the max-abs prescale is
+    // non-finite or zero => return it; else scale * total^(1/p).
+    double norm;
+    if (r.nan) norm = nanv;
+    else if (r.inf) norm = infv;
+    else if (r.amax == 0.0 || __builtin_isinf(norm_type)) norm = r.amax;
+    else norm = __builtin_sqrt(r.sumsq);   // p == 2; other p: nt_grad_norm_pow
+    nt_amp_ctrl c = *ctrl;
+    c.sumsq = r.sumsq;
+    c.amax = r.amax;
+    c.norm = norm;
+    c.has_nan = r.nan;
+    c.found_inf = r.nan | r.inf;
+    if (max_norm >= 0.0) {
+        c.clip_coef = max_norm / (norm + 1e-6);
+        c.clip = c.clip_coef < 1.0 ? 1 : 0;
+    } else {
+        c.clip_coef = 1.0;
+        c.clip = 0;
+    }
+    c.skip = c.found_inf;
+    c.scale_used = c.scale;
+    c.iterations += 1;
+    c.skipped += c.found_inf;
+    if (do_update) scaler_update(&c, c.found_inf, growth, backoff, interval);
+    *ctrl = c;
+}
+
+// General p-norm second pass: sum of (|g'|/amax)^p in fp64.
+template <class G>
+__global__ __launch_bounds__(kBlock) void norm_pow_kernel(const DevTensor *__restrict__ tensors,
+                                                          const Task *__restrict__ tasks, int64_t ntasks,
+                                                          int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
+                                                          int32_t scale_from_ctrl, double p,
+                                                          double *__restrict__ partials) {
+    if (scale_from_ctrl && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale_used, xf.unscale, xf.inv_scale);
+    const double s = ctrl->amax;
+    double acc = 0.0;
+    for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
+        const Task task = tasks[t];
+        const DevTensor d = tensors[task.tensor];
+        const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
+        const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+        const auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
+        for (uint64_t i = start + threadIdx.x; i < end; i += kBlock) {
+            const double a = __builtin_fabs((double)unscale_one<G>(load1<G>(gp, i), xf)) / s;
+            acc += pow(a, p);
+        }
+    }
+    Acc in;
+    in.sumsq = acc;
+    Acc r = block_reduce(in);
+    if (threadIdx.x == 0) partials[blockIdx.x] = r.sumsq;
+}
+
+__global__ __launch_bounds__(kBlock) void norm_pow_finalize_kernel(const double *__restrict__ partials, int32_t n,
+                                                                   nt_amp_ctrl *ctrl, double p, double max_norm) {
+    Acc acc;
+    for (int32_t i = threadIdx.x; i < n; i += kBlock) acc.sumsq += partials[i];
+    Acc r = block_reduce(acc);
+    if (threadIdx.x != 0) return;
+    nt_amp_ctrl c = *ctrl;
+    const double s = c.amax;
+    // A non-finite or zero max-abs prescale is the norm itself; finalize
+    // already stored it (optim/clip_grad.py:71-72).
+    if (c.found_inf || !(s > 0.0)) return;
+    double total = r.sumsq;
+    double result = s * pow(total, 1.0 / p);
+    if (!__builtin_isfinite(result)) result = exp(log(s) + log(total) / p);
+    c.norm = result;
+    c.sumsq = total;    // the raw sum, for combining several plans on the host
+    if (max_norm >= 0.0) {
+        c.clip_coef = max_norm / (result + 1e-6);
+        c.clip = c.clip_coef < 1.0 ? 1 : 0;
+    }
+    *ctrl = c;
+}
+
+// In-place grad transform: g <- clip(unscale(g)).
+template <class G>
+__global__ __launch_bounds__(kBlock) void grad_apply_kernel(const DevTensor *__restrict__ tensors,
+                                                            const Task *__restrict__ tasks, int64_t chunk, Xform xf,
+                                                            const nt_amp_ctrl *ctrl) {
+    if (ctrl != nullptr) {
+        if (xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale_used, xf.unscale, xf.inv_scale);
+        xf.clip = ctrl->clip;
+        xf.clip_coef = ctrl->clip_coef;
+    }
+    if (!xf.unscale && !xf.clip) return;
+    const Task task = tasks[blockIdx.x];
+    const DevTensor d = tensors[task.tensor];
+    const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
+    const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+    auto *gp = reinterpret_cast<typename G::raw *>(d.grad);
+    uint64_t scalar_from = start;
+    if (d.flags & kAligned16) {
+        const uint64_t vend = start + ((end - start) / kVec) * kVec;
+        for (uint64_t i = start + (uint64_t)threadIdx.x * kVec; i < vend; i += (uint64_t)kBlock * kVec) {
+            float g[kVec];
+            Vec8IO<G, true>::load(gp, i, g);
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) g[k] = clip_one<G>(unscale_one<G>(g[k], xf), xf);
+            Vec8IO<G, true>::store(gp, i, g);
+        }
+        scalar_from = vend;
+    }
+    for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock)
+        store1<G>(gp, i, clip_one<G>(unscale_one<G>(load1<G>(gp, i), xf), xf));
+}
+
+__global__ __launch_bounds__(kBlock) void grad_apply_f64_kernel(const DevTensor *__restrict__ tensors,
+                                                                const Task *__restrict__ tasks, int64_t chunk,
+                                                                Xform xf, const nt_amp_ctrl *ctrl) {
+    double scale = xf.scale;
+    if (ctrl != nullptr) {
+        scale = ctrl->scale_used;
+        xf.clip = ctrl->clip;
+        xf.clip_coef = ctrl->clip_coef;
+    }
+    if (!xf.unscale && !xf.clip) return;
+    const Task task = tasks[blockIdx.x];
+    const DevTensor d = tensors[task.tensor];
+    const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
+    const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+    double *gp = reinterpret_cast<double *>(d.grad);
+    for (uint64_t i = start + threadIdx.x; i < end; i += kBlock) {
+        double g = gp[i];
+        if (xf.unscale) g = g / scale;
+        if (xf.clip) g = g * xf.clip_coef;
+        gp[i] = g;
+    }
+}
+
+__global__ void ctrl_reset_kernel(nt_amp_ctrl *ctrl, float scale, int32_t tracker) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    nt_amp_ctrl c{};
+    c.scale = scale;
+    c.scale_used = scale;
+    c.growth_tracker = tracker;
+    c.clip_coef = 1.0;
+    *ctrl = c;
+}
+
+template <class T>
+__global__ __launch_bounds__(kBlock) void scale_array_kernel(const typename T::raw *in, typename T::raw *out,
+                                                             double scale, const nt_amp_ctrl *ctrl, uint64_t n) {
+    const double s = ctrl != nullptr ? (double)ctrl->scale : scale;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
+        out[i] = T::from_f64((double)T::to_f32(in[i]) * s);
+}
+__global__ __launch_bounds__(kBlock) void scale_array_f64_kernel(const double *in, double *out, double scale,
+                                                                 const nt_amp_ctrl *ctrl, uint64_t n) {
+    const double s = ctrl != nullptr ? (double)ctrl->scale : scale;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
+        out[i] = in[i] * s;
+}
+
+__global__ void clear_flag_kernel(int32_t *flag) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) *flag = 0;
+}
+
+// Any element < 0 sets *flag = 1 (plain stores of the same value; -0.0 and
+// NaN are not negative, as with NumPy's less(array, 0)).
+template <class T>
+__global__ __launch_bounds__(kBlock) void any_negative_kernel(const typename T::raw *a, uint64_t n, int32_t *flag) {
+    int found = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
+        found |= (T::to_f32(a[i]) < 0.0f) ? 1 : 0;
+    if (found) *flag = 1;
+}
+__global__ __launch_bounds__(kBlock) void any_negative_f64_kernel(const double *a, uint64_t n, int32_t *flag) {
+    int found = 0;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
+        found |= (a[i] < 0.0) ? 1 : 0;
+    if (found) *flag = 1;
+}
+
+template <template <class> class K, class... Args>
+static int32_t grad_dispatch(int32_t gdt, dim3 grid, hipStream_t s, Args... args) {
+    switch (gdt) {
+        case NT_F32: K<TF32>::launch(grid, s, args...); break;
+        case NT_F16: K<TF16>::launch(grid, s, args...); break;
+        case NT_BF16: K<TBF16>::launch(grid, s, args...); break;
+        default: return fail(NT_ERR_TYPE, "unsupported gradient dtype");
+    }
+    return NT_OK;
+}
+
+template <class G> struct PrepassL {
+    template <class... A> static void launch(dim3 g, hipStream_t s, A... a) {
+        prepass_kernel<G><<<g, dim3(kBlock), 0, s>>>(a...);
+    }
+};
+template <class G> struct NormPowL {
+    template <class... A> static void launch(dim3 g, hipStream_t s, A... a) {
+        norm_pow_kernel<G><<<g, dim3(kBlock), 0, s>>>(a...);
+    }
+};
+template <class G> struct ApplyL {
+    template <class... A> static void launch(dim3 g, hipStream_t s, A... a) {
+        grad_apply_kernel<G><<<g, dim3(kBlock), 0, s>>>(a...);
+    }
+};
+
+static uint64_t small_grid(uint64_t n) {
+    uint64_t b = (n + kBlock - 1) / kBlock;
+    if (b > 1024) b = 1024;
+    return b ? b : 1;
+}
+
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale, const nt_amp_ctrl *ctrl, void *stream) {
+    clear_error();
+    int32_t rc = check_plan(plan);
+    if (rc != NT_OK) return rc;
+    if (unscale && ctrl == nullptr && !(scale > 0.0f && __builtin_isfinite(scale)))
+        return fail(NT_ERR_VALUE, "loss scale must be finite and positive");
+    DeviceGuard guard(plan->device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    nt_grad_xform hx{};
+    hx.scale = unscale ? scale : 1.0f;
+    hx.unscale = unscale ? 1 : 0;
+    Xform xf = make_xform(unscale && ctrl == nullptr ? &hx : nullptr);
+    if (unscale && ctrl != nullptr) xf.unscale = 1;  // scale read on the device
+    hipStream_t s = (hipStream_t)stream;
+    dim3 grid((unsigned)plan->prepass_grid);
+    if (plan->layout.grad_dtype == NT_F64) {
+        prepass_f64_kernel<<<grid, dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, plan->ntasks, plan->chunk,
+                                                         xf, ctrl, plan->d_partials);
+    } else {
+        rc = grad_dispatch<PrepassL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
+                                     (const Task *)plan->d_tasks, plan->ntasks, plan->chunk, xf, ctrl,
+                                     plan->d_partials);
+        if (rc != NT_OK) return rc;
+    }
+    NT_LAUNCH_CHECK("prepass_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, double max_norm, int32_t scaler_update,
+                        double growth_factor, double backoff_factor, int32_t growth_interval, void *stream) {
+    clear_error();
+    int32_t rc = check_plan(plan);
+    if (rc != NT_OK) return rc;
+    if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
+    if (!(norm_type > 0.0)) return fail(NT_ERR_VALUE, "norm_type must be positive or positive infinity.");
+    if (scaler_update && (growth_interval <= 0 || !(growth_factor > 1.0) || !(backoff_factor > 0.0 && backoff_factor < 1.0)))
+        return fail(NT_ERR_VALUE, "invalid GradScaler growth/backoff settings");
+    DeviceGuard guard(plan->device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    finalize_kernel<<<dim3(1), dim3(kBlock), 0, (hipStream_t)stream>>>(
+        plan->d_partials, plan->prepass_grid, ctrl, norm_type, max_norm, scaler_update, growth_factor,
+        backoff_factor, growth_interval);
+    NT_LAUNCH_CHECK("finalize_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, double max_norm, float scale,
+                         int32_t unscale, int32_t scale_from_ctrl, void *stream) {
+    clear_error();
+    int32_t rc = check_plan(plan);
+    if (rc != NT_OK) return rc;
+    if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
+    if (!(norm_type > 0.0) || __builtin_isinf(norm_type))
+        return fail(NT_ERR_VALUE, "nt_grad_norm_pow needs a finite positive norm_type");
+    if (plan->layout.grad_dtype == NT_F64)
+        return fail(NT_ERR_TYPE, "general p-norm of float64 gradients is not supported on the device");
+    DeviceGuard guard(plan->device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    nt_grad_xform hx{};
+    hx.scale = unscale ? scale : 1.0f;
+    hx.unscale = unscale ? 1 : 0;
+    Xform xf = make_xform(unscale && !scale_from_ctrl ? &hx : nullptr);
+    if (unscale && scale_from_ctrl) xf.unscale = 1;
+    hipStream_t s = (hipStream_t)stream;
+    dim3 grid((unsigned)plan->prepass_grid);
+    rc = grad_dispatch<NormPowL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
+                                 (const Task *)plan->d_tasks, plan->ntasks, plan->chunk, xf,
+                                 (const nt_amp_ctrl *)ctrl, scale_from_ctrl, norm_type, plan->d_pow_partials);
+    if (rc != NT_OK) return rc;
+    NT_LAUNCH_CHECK("norm_pow_kernel launch");
+    norm_pow_finalize_kernel<<<dim3(1), dim3(kBlock), 0, s>>>(plan->d_pow_partials, plan->prepass_grid, ctrl,
+                                                              norm_type, max_norm);
+    NT_LAUNCH_CHECK("norm_pow_finalize_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_grad_apply(nt_plan *plan, const nt_grad_xform *xform, void *stream) {
+    clear_error();
+    int32_t rc = check_plan(plan);
+    if (rc != NT_OK) return rc;
+    if (xform == nullptr || plan->ntasks == 0) return NT_OK;
+    DeviceGuard guard(plan->device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    Xform xf = make_xform(xform);
+    const nt_amp_ctrl *ctrl = xform->ctrl;
+    if (ctrl != nullptr) xf.unscale = xform->unscale ? 1 : 0;
+    hipStream_t s = (hipStream_t)stream;
+    dim3 grid((unsigned)plan->ntasks);
+    if (plan->layout.grad_dtype == NT_F64) {
+        grad_apply_f64_kernel<<<grid, dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, plan->chunk, xf, ctrl);
+    } else {
+        rc = grad_dispatch<ApplyL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
+                                   (const Task *)plan->d_tasks, plan->chunk, xf, ctrl);
+        if (rc != NT_OK) return rc;
+    }
+    NT_LAUNCH_CHECK("grad_apply_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_ctrl_reset(nt_amp_ctrl *ctrl, float scale, int32_t growth_tracker, void *stream) {
+    clear_error();
+    if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
+    ctrl_reset_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>(ctrl, scale, growth_tracker);
+    NT_LAUNCH_CHECK("ctrl_reset_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_scale_array(const void *in, void *out, int32_t dtype, double scale, const nt_amp_ctrl *ctrl,
+                       uint64_t count, void *stream) {
+    clear_error();
+    if (count == 0) return NT_OK;
+    if (in == nullptr || out == nullptr) return fail(NT_ERR_VALUE, "nt_scale_array: NULL array");
+    hipStream_t s = (hipStream_t)stream;
+    dim3 grid((unsigned)small_grid(count));
+    switch (dtype) {
+        case NT_F32: scale_array_kernel<TF32><<<grid, dim3(kBlock), 0, s>>>((const float *)in, (float *)out, scale, ctrl, count); break;
+        case NT_F16: scale_array_kernel<TF16><<<grid, dim3(kBlock), 0, s>>>((const uint16_t *)in, (uint16_t *)out, scale, ctrl, count); break;
+        case NT_BF16: scale_array_kernel<TBF16><<<grid, dim3(kBlock), 0, s>>>((const uint16_t *)in, (uint16_t *)out, scale, ctrl, count); break;
+        case NT_F64: scale_array_f64_kernel<<<grid, dim3(kBlock), 0, s>>>((const double *)in, (double *)out, scale, ctrl, count); break;
+        default: return fail(NT_ERR_TYPE, "nt_scale_array: unsupported dtype");
+    }
+    NT_LAUNCH_CHECK("scale_array_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_any_negative(const void *array, int32_t dtype, uint64_t count, int32_t *flag, void *stream) {
+    clear_error();
+    if (flag == nullptr) return fail(NT_ERR_VALUE, "nt_any_negative: NULL flag");
+    hipStream_t s = (hipStream_t)stream;
+    clear_flag_kernel<<<dim3(1), dim3(64), 0, s>>>(flag);
+    NT_LAUNCH_CHECK("clear_flag_kernel launch");
+    if (count == 0) return NT_OK;
+    if (array == nullptr) return fail(NT_ERR_VALUE, "nt_any_negative: NULL array");
+    dim3 grid((unsigned)small_grid(count));
+    switch (dtype) {
+        case NT_F32: any_negative_kernel<TF32><<<grid, dim3(kBlock), 0, s>>>((const float *)array, count, flag); break;
+        case NT_F16: any_negative_kernel<TF16><<<grid, dim3(kBlock), 0, s>>>((const uint16_t *)array, count, flag); break;
+        case NT_BF16: any_negative_kernel<TBF16><<<grid, dim3(kBlock), 0, s>>>((const uint16_t *)array, count, flag); break;
+        case NT_F64: any_negative_f64_kernel<<<grid, dim3(kBlock), 0, s>>>((const double *)array, count, flag); break;
+        default: return fail(NT_ERR_TYPE, "nt_any_negative: unsupported dtype");
+    }
+    NT_LAUNCH_CHECK("any_negative_kernel launch");
+    return NT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,228 @@
+// nt_common.hpp — device helpers shared by the optimizer-step kernels.
+//
+// Storage types, exact conversions and 128-bit vector I/O for gfx950.
+// All arithmetic here must round exactly like NumPy on the host: the library
+// is compiled with -ffp-contract=off (no FMA contraction), correctly rounded
+// fp32 divide/sqrt and fp32 denormals preserved.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/namitorch_amd.h"
+
+namespace nt {
+
+constexpr int kBlock = 256;        // threads per workgroup (4 wave64s)
+constexpr int kVec = 8;            // elements per thread per iteration
+
+// ---- bit casts ---------------------------------------------------------------
+__device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float bits_f32(uint32_t b) { return __builtin_bit_cast(float, b); }
+
+// ---- bfloat16 (stored as uint16 bit patterns) ---------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
+
+// Round-to-nearest-even fp32 -> bf16.  NaN stays NaN (quieted, sign kept).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = f32_bits(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// ---- float16 (stored as uint16 bit patterns) ----------------------------------
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+// v_cvt_f16_f32: round to nearest even, overflow to inf.
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// fp64 -> fp32 with round-to-odd: truncate toward zero, then force the last
+// bit to 1 when the conversion was inexact.  A second rounding of this value
+// to a format with at least two fewer significand bits (fp16: 11, bf16: 8,
+// against fp32's 24) equals a single correct rounding from fp64, which is
+// what NumPy's direct float64 -> float16 cast produces.
+__device__ __forceinline__ float f64_to_f32_odd(double d) {
+    float f = (float)d;                      // round to nearest even
+    double back = (double)f;
+    if (back != d && d == d) {               // inexact and not NaN
+        uint32_t b = f32_bits(f);
+        if (__builtin_fabs(back) > __builtin_fabs(d)) b -= 1u;  // undo rounding away from zero
+        b |= 1u;
+        f = bits_f32(b);
+    }
+    return f;
+}
+
+// ---- storage type traits -----------------------------------------------------
+// Each trait: `raw` storage type, exact widening to fp32/fp64, rounding of an
+// fp32 (or fp64) value to the storage format and back.
+struct TF32 {
+    using raw = float;
+    static constexpr int code = NT_F32;
+    __device__ static float to_f32(raw x) { return x; }
+    __device__ static raw from_f32(float x) { return x; }
+    __device__ static float round_f32(float x) { return x; }
+    __device__ static raw from_f64(double x) { return (float)x; }
+};
+struct TF16 {
+    using raw = uint16_t;
+    static constexpr int code = NT_F16;
+    __device__ static float to_f32(raw x) { return f16_to_f32(x); }
+    __device__ static raw from_f32(float x) { return f32_to_f16(x); }
+    __device__ static float round_f32(float x) { return f16_to_f32(f32_to_f16(x)); }
+    __device__ static raw from_f64(double x) { return f32_to_f16(f64_to_f32_odd(x)); }
+};
+struct TBF16 {
+    using raw = uint16_t;
+    static constexpr int code = NT_BF16;
+    __device__ static float to_f32(raw x) { return bf16_to_f32(x); }
+    __device__ static raw from_f32(float x) { return f32_to_bf16(x); }
+    __device__ static float round_f32(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+    __device__ static raw from_f64(double x) { return f32_to_bf16(f64_to_f32_odd(x)); }
+};
+
+// ---- 8-element vector I/O ------------------------------------------------------
+// Loads/stores of 8 consecutive elements at a 8-element-aligned index: two
+// dwordx4 for fp32, one dwordx4 for 16-bit types.  Streams touched once per
+// step use nontemporal accesses so they do not evict each other from L2/MALL.
+template <bool NT, class V>
+__device__ __forceinline__ V ld(const V *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <bool NT, class V>
+__device__ __forceinline__ void st(V *p, V v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <class T, bool NT> struct Vec8IO;
+
+template <bool NT> struct Vec8IO<TF32, NT> {
+    __device__ static void load(const float *base, uint64_t i, float (&out)[kVec]) {
+        const f32x4 *p = reinterpret_cast<const f32x4 *>(base + i);
+        f32x4 a = ld<NT>(p), b = ld<NT>(p + 1);
+        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+    }
+    __device__ static void store(float *base, uint64_t i, const float (&in)[kVec]) {
+        f32x4 *p = reinterpret_cast<f32x4 *>(base + i);
+        f32x4 a = {in[0], in[1], in[2], in[3]};
+        f32x4 b = {in[4], in[5], in[6], in[7]};
+        st<NT>(p, a);
+        st<NT>(p + 1, b);
+    }
+};
+
+template <class T, bool NT> struct Vec8IO16 {
+    __device__ static void load(const uint16_t *base, uint64_t i, float (&out)[kVec]) {
+        u32x4 w = ld<NT>(reinterpret_cast<const u32x4 *>(base + i));
+        uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            out[2 * k] = T::to_f32((uint16_t)(ws[k] & 0xffffu));
+            out[2 * k + 1] = T::to_f32((uint16_t)(ws[k] >> 16));
+        }
+    }
+    // `in` must already hold values exactly representable in T.
+    __device__ static void store(uint16_t *base, uint64_t i, const float (&in)[kVec]) {
+        uint32_t ws[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            ws[k] = (uint32_t)T::from_f32(in[2 * k]) | ((uint32_t)T::from_f32(in[2 * k + 1]) << 16);
+        u32x4 w = {ws[0], ws[1], ws[2], ws[3]};
+        st<NT>(reinterpret_cast<u32x4 *>(base + i), w);
+    }
+};
+template <bool NT> struct Vec8IO<TF16, NT> : Vec8IO16<TF16, NT> {};
+template <bool NT> struct Vec8IO<TBF16, NT> : Vec8IO16<TBF16, NT> {};
+
+// Scalar element access for tails and unaligned tensors.
+template <class T>
+__device__ __forceinline__ float load1(const typename T::raw *base, uint64_t i) {
+    return T::to_f32(base[i]);
+}
+template <class T>
+__device__ __forceinline__ void store1(typename T::raw *base, uint64_t i, float v) {
+    base[i] = T::from_f32(v);
+}
+
+// ---- device descriptor / task tables ---------------------------------------------
+struct alignas(64) DevTensor {
+    void *param;
+    void *grad;
+    void *exp_avg;
+    void *exp_avg_sq;
+    void *model_copy;
+    uint64_t numel;
+    uint32_t slot;
+    uint32_t flags;       // bit 0: every role pointer is 16-byte aligned
+};
+constexpr uint32_t kAligned16 = 1u;
+
+struct Task {
+    uint32_t tensor;
+    uint32_t chunk;
+};
+
+// Per-workgroup partial of the grad pre-pass.
+struct alignas(32) Partial {
+    double sumsq;
+    double amax;
+    int32_t has_nan;
+    int32_t has_inf;
+    int32_t pad[2];
+};
+
+// ---- grad transform (unscale then clip), exactly as stored grads would be -------
+// g' = to_G(f32(g) / scale)           (amp.py:190-191; division or an exact
+//                                      multiply by 1/scale for powers of two)
+// g''= to_G(f64(g') * clip_coef)      (optim/clip_grad.py:111)
+struct Xform {
+    float scale;
+    float inv_scale;
+    double clip_coef;
+    int32_t unscale;      // 0: none, 1: divide, 2: multiply by exact inverse
+    int32_t clip;
+};
+
+template <class G>
+__device__ __forceinline__ float unscale_one(float g, const Xform &x) {
+    if (x.unscale == 1) return G::round_f32(g / x.scale);
+    if (x.unscale == 2) return G::round_f32(g * x.inv_scale);
+    return g;
+}
+template <class G>
+__device__ __forceinline__ float clip_one(float g, const Xform &x) {
+    if (!x.clip) return g;
+    return G::to_f32(G::from_f64((double)g * x.clip_coef));
+}
+
+// ---- wavefront / workgroup reductions (fixed order => deterministic) --------------
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_max(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        double o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v |= __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace nt

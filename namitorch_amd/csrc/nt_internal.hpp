@@ -1,0 +1,64 @@
+// nt_internal.hpp — host-side internals shared by the library's .hip files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "nt_common.hpp"
+
+struct nt_plan {
+    int32_t device;
+    int32_t ntensors;
+    nt_mt_layout layout;
+    uint64_t numel;
+    int64_t chunk;               // elements per workgroup task
+    int64_t ntasks;
+    int32_t prepass_grid;        // workgroups of the grad pre-pass (partials slots)
+    uint32_t max_slot;           // largest coefficient slot any tensor selects
+    nt::DevTensor *d_tensors;    // [ntensors]
+    nt::Task *d_tasks;           // [ntasks]
+    nt::Partial *d_partials;     // [prepass_grid]
+    double *d_pow_partials;      // [prepass_grid] (general p-norm)
+    void *h_staging;             // pinned host copy of the tables (async upload source)
+};
+
+namespace nt {
+
+// Record `msg` as this thread's last error and return `code`.
+int32_t fail(int32_t code, const std::string &msg);
+// Convert a HIP status into NT_ERR_HIP with context; NT_OK on success.
+int32_t hip_check(hipError_t err, const char *what);
+// Clear this thread's last error.
+void clear_error();
+
+// Scoped switch to `device` (restores the caller's current device).
+class DeviceGuard {
+  public:
+    explicit DeviceGuard(int32_t device);
+    ~DeviceGuard();
+    bool ok() const { return ok_; }
+    hipError_t error() const { return err_; }
+
+  private:
+    int prev_ = -1;
+    bool ok_ = true;
+    hipError_t err_ = hipSuccess;
+};
+
+// Device-side transform parameters from a host nt_grad_xform (ctrl ignored).
+Xform make_xform(const nt_grad_xform *x);
+
+// Validate a plan pointer.
+int32_t check_plan(const nt_plan *plan);
+
+}  // namespace nt
+
+#define NT_HIP_TRY(expr, what)                                   \
+    do {                                                         \
+        int32_t nt_rc_ = nt::hip_check((expr), (what));          \
+        if (nt_rc_ != NT_OK) return nt_rc_;                      \
+    } while (0)
+
+#define NT_LAUNCH_CHECK(what) NT_HIP_TRY(hipGetLastError(), what)

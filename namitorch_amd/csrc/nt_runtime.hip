@@ -1,0 +1,264 @@
+// nt_runtime.hip — error reporting, device helpers and multi-tensor plans.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "nt_internal.hpp"
+
+namespace nt {
+
+static thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int32_t hip_check(hipError_t err, const char *what) {
+    if (err == hipSuccess) return NT_OK;
+    return fail(NT_ERR_HIP, std::string(what) + ": " + hipGetErrorName(err) + " (" +
+                                hipGetErrorString(err) + ")");
+}
+
+DeviceGuard::DeviceGuard(int32_t device) {
+    err_ = hipGetDevice(&prev_);
+    if (err_ != hipSuccess) {
+        ok_ = false;
+        prev_ = -1;
+        return;
+    }
+    if (prev_ != device) {
+        err_ = hipSetDevice(device);
+        ok_ = (err_ == hipSuccess);
+    }
+}
+
+DeviceGuard::~DeviceGuard() {
+    int cur = -1;
+    if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+}
+
+Xform make_xform(const nt_grad_xform *x) {
+    Xform r{};
+    r.scale = 1.0f;
+    r.inv_scale = 1.0f;
+    r.clip_coef = 1.0;
+    if (x == nullptr) return r;
+    r.scale = x->scale;
+    if (x->unscale) {
+        // Dividing by a power of two equals multiplying by its exact inverse
+        // (both round the same real number once), so use the multiply then.
+        int e = 0;
+        float m = frexpf(x->scale, &e);
+        float inv = ldexpf(1.0f, 1 - e);
+        bool pow2 = (m == 0.5f) && inv != 0.0f && (double)inv * (double)x->scale == 1.0;
+        r.unscale = pow2 ? 2 : 1;
+        r.inv_scale = pow2 ? inv : 1.0f;
+    }
+    r.clip = x->clip ? 1 : 0;
+    r.clip_coef = x->clip_coef;
+    return r;
+}
+
+int32_t check_plan(const nt_plan *plan) {
+    if (plan == nullptr) return fail(NT_ERR_VALUE, "multi-tensor plan is NULL");
+    return NT_OK;
+}
+
+static bool valid_dtype(int32_t d, bool allow_none) {
+    return (allow_none && d == NT_DTYPE_NONE) || d == NT_F32 || d == NT_F16 || d == NT_BF16 || d == NT_F64;
+}
+
+static size_t dtype_size(int32_t d) {
+    switch (d) {
+        case NT_F32: return 4;
+        case NT_F16:
+        case NT_BF16: return 2;
+        case NT_F64: return 8;
+        default: return 0;
+    }
+}
+
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+const char *nt_last_error(void) { return g_last_error.c_str(); }
+
+int32_t nt_abi_version(void) { return 1; }
+
+int32_t nt_device_count(int32_t *count) {
+    clear_error();
+    if (count == nullptr) return fail(NT_ERR_VALUE, "count is NULL");
+    int c = 0;
+    hipError_t err = hipGetDeviceCount(&c);
+    if (err == hipErrorNoDevice) c = 0;
+    else NT_HIP_TRY(err, "hipGetDeviceCount");
+    *count = c;
+    return NT_OK;
+}
+
+int32_t nt_device_arch(int32_t device, char *buf, int32_t len) {
+    clear_error();
+    if (buf == nullptr || len <= 0) return fail(NT_ERR_VALUE, "arch buffer is empty");
+    hipDeviceProp_t prop;
+    NT_HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    std::strncpy(buf, prop.gcnArchName, (size_t)len - 1);
+    buf[len - 1] = '\0';
+    return NT_OK;
+}
+
+int32_t nt_stream_synchronize(void *stream) {
+    clear_error();
+    NT_HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    return NT_OK;
+}
+
+int32_t nt_memcpy_d2h(void *dst, const void *src, uint64_t bytes, void *stream) {
+    clear_error();
+    if (bytes == 0) return NT_OK;
+    if (dst == nullptr || src == nullptr) return fail(NT_ERR_VALUE, "memcpy with NULL pointer");
+    NT_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream), "hipMemcpyAsync(D2H)");
+    NT_HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    return NT_OK;
+}
+
+int32_t nt_memcpy_h2d(void *dst, const void *src, uint64_t bytes, void *stream) {
+    clear_error();
+    if (bytes == 0) return NT_OK;
+    if (dst == nullptr || src == nullptr) return fail(NT_ERR_VALUE, "memcpy with NULL pointer");
+    NT_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream), "hipMemcpyAsync(H2D)");
+    NT_HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    return NT_OK;
+}
+
+int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
+                       const nt_mt_layout *layout, int64_t chunk, void *stream, nt_plan **out) {
+    clear_error();
+    if (out == nullptr) return fail(NT_ERR_VALUE, "plan output pointer is NULL");
+    *out = nullptr;
+    if (layout == nullptr) return fail(NT_ERR_VALUE, "plan layout is NULL");
+    if (n < 0 || (n > 0 && tensors == nullptr)) return fail(NT_ERR_VALUE, "plan tensor table is invalid");
+    if (!valid_dtype(layout->param_dtype, true) || !valid_dtype(layout->grad_dtype, false) ||
+        !valid_dtype(layout->state_dtype, true) || !valid_dtype(layout->copy_dtype, true))
+        return fail(NT_ERR_TYPE, "plan layout names an unsupported dtype code");
+    if (chunk == 0) chunk = 16384;
+    const int64_t quantum = (int64_t)kBlock * kVec;
+    if (chunk < quantum || chunk % quantum != 0 || chunk > (int64_t)1 << 30)
+        return fail(NT_ERR_VALUE, "plan chunk must be a positive multiple of 2048 elements, at most 2**30");
+
+    std::vector<DevTensor> host(n > 0 ? (size_t)n : 1);
+    std::vector<Task> tasks;
+    uint64_t total = 0;
+    uint32_t max_slot = 0;
+    const size_t gsz = dtype_size(layout->grad_dtype);
+    const size_t psz = dtype_size(layout->param_dtype);
+    const size_t ssz = dtype_size(layout->state_dtype);
+    const size_t csz = dtype_size(layout->copy_dtype);
+    for (int32_t t = 0; t < n; ++t) {
+        const nt_mt_tensor &s = tensors[t];
+        if (s.grad == nullptr && s.numel > 0) return fail(NT_ERR_VALUE, "plan tensor " + std::to_string(t) + " has no gradient");
+        if (s.slot >= NT_MAX_SLOTS) return fail(NT_ERR_VALUE, "plan tensor " + std::to_string(t) + " selects a coefficient slot >= 16");
+        DevTensor d{};
+        d.param = s.param;
+        d.grad = s.grad;
+        d.exp_avg = s.exp_avg;
+        d.exp_avg_sq = s.exp_avg_sq;
+        d.model_copy = s.model_copy;
+        d.numel = s.numel;
+        d.slot = s.slot;
+        if (s.slot > max_slot) max_slot = s.slot;
+        bool aligned = true;
+        const void *ptrs[5] = {s.param, s.grad, s.exp_avg, s.exp_avg_sq, s.model_copy};
+        const size_t sizes[5] = {psz, gsz, ssz, ssz, csz};
+        for (int r = 0; r < 5; ++r) {
+            if (ptrs[r] == nullptr) continue;
+            uintptr_t p = (uintptr_t)ptrs[r];
+            if (p % 16 != 0) aligned = false;
+            if (sizes[r] != 0 && p % sizes[r] != 0)
+                return fail(NT_ERR_VALUE, "plan tensor " + std::to_string(t) + " has a pointer not aligned to its dtype");
+        }
+        d.flags = aligned ? kAligned16 : 0u;
+        host[t] = d;
+        total += s.numel;
+        uint64_t nchunks = (s.numel + (uint64_t)chunk - 1) / (uint64_t)chunk;
+        if (nchunks > 0xffffffffull) return fail(NT_ERR_VALUE, "tensor too large for the task map");
+        for (uint64_t c = 0; c < nchunks; ++c) tasks.push_back(Task{(uint32_t)t, (uint32_t)c});
+    }
+    if (tasks.size() > 0x7fffffffull) return fail(NT_ERR_VALUE, "too many workgroup tasks");
+
+    DeviceGuard guard(device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+
+    nt_plan *plan = new nt_plan{};
+    plan->device = device;
+    plan->ntensors = n;
+    plan->layout = *layout;
+    plan->numel = total;
+    plan->chunk = chunk;
+    plan->ntasks = (int64_t)tasks.size();
+    plan->max_slot = max_slot;
+    int64_t grid = plan->ntasks < 2048 ? plan->ntasks : 2048;
+    plan->prepass_grid = (int32_t)(grid > 0 ? grid : 1);
+
+    auto cleanup = [&](int32_t rc) {
+        if (plan->d_tensors) (void)hipFree(plan->d_tensors);
+        if (plan->d_tasks) (void)hipFree(plan->d_tasks);
+        if (plan->d_partials) (void)hipFree(plan->d_partials);
+        if (plan->d_pow_partials) (void)hipFree(plan->d_pow_partials);
+        if (plan->h_staging) (void)hipHostFree(plan->h_staging);
+        delete plan;
+        return rc;
+    };
+    const size_t tensor_bytes = host.size() * sizeof(DevTensor);
+    const size_t task_bytes = (tasks.empty() ? 1 : tasks.size()) * sizeof(Task);
+    int32_t rc;
+    if ((rc = hip_check(hipMalloc((void **)&plan->d_tensors, tensor_bytes), "hipMalloc(plan tensors)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipMalloc((void **)&plan->d_tasks, task_bytes), "hipMalloc(plan tasks)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipMalloc((void **)&plan->d_partials, (size_t)plan->prepass_grid * sizeof(Partial)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipMalloc((void **)&plan->d_pow_partials, (size_t)plan->prepass_grid * sizeof(double)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipHostMalloc(&plan->h_staging, tensor_bytes + task_bytes, hipHostMallocDefault), "hipHostMalloc(plan staging)")) != NT_OK) return cleanup(rc);
+    char *staging = static_cast<char *>(plan->h_staging);
+    std::memcpy(staging, host.data(), tensor_bytes);
+    if (!tasks.empty()) std::memcpy(staging + tensor_bytes, tasks.data(), tasks.size() * sizeof(Task));
+    hipStream_t s = (hipStream_t)stream;
+    if ((rc = hip_check(hipMemcpyAsync(plan->d_tensors, staging, tensor_bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync(plan tensors)")) != NT_OK) return cleanup(rc);
+    if (!tasks.empty() &&
+        (rc = hip_check(hipMemcpyAsync(plan->d_tasks, staging + tensor_bytes, tasks.size() * sizeof(Task), hipMemcpyHostToDevice, s), "hipMemcpyAsync(plan tasks)")) != NT_OK)
+        return cleanup(rc);
+    *out = plan;
+    return NT_OK;
+}
+
+int32_t nt_plan_destroy(nt_plan *plan) {
+    clear_error();
+    if (plan == nullptr) return NT_OK;
+    DeviceGuard guard(plan->device);
+    // Kernels queued with this plan may still read its tables.
+    (void)hipDeviceSynchronize();
+    (void)hipFree(plan->d_tensors);
+    (void)hipFree(plan->d_tasks);
+    (void)hipFree(plan->d_partials);
+    (void)hipFree(plan->d_pow_partials);
+    (void)hipHostFree(plan->h_staging);
+    delete plan;
+    return NT_OK;
+}
+
+int32_t nt_plan_info(const nt_plan *plan, uint64_t *numel, int32_t *tensors, int64_t *tasks) {
+    clear_error();
+    int32_t rc = check_plan(plan);
+    if (rc != NT_OK) return rc;
+    if (numel) *numel = plan->numel;
+    if (tensors) *tensors = plan->ntensors;
+    if (tasks) *tasks = plan->ntasks;
+    return NT_OK;
+}
+
+}  // extern "C"

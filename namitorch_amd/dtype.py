@@ -1,0 +1,143 @@
+"""Data types of the optimizer-step path.
+
+Mirrors ``namitorch/dtype.py:16-25`` (float16/32/64, int8/16/32/64, uint8,
+bool) and adds ``bfloat16``, which the reference does not have: it is needed
+for the low-precision model copies, moments and gradients of mixed-precision
+training.  Each dtype knows its NumPy dtype (bfloat16 has none; its host
+form is float32 values or uint16 bit patterns), its torch storage dtype and
+its code in the C ABI.
+"""
+
+from __future__ import annotations
+
+from enum import Enum
+
+import numpy as np
+import torch
+
+from . import _native
+
+
+class UnsupportedDTypeError(TypeError):
+    def __init__(self, value: object):
+        supported = ", ".join(dtype.value for dtype in DType)
+        super().__init__(f"Unsupported NamiTorch dtype: {value!r}. Supported: {supported}.")
+
+
+class DType(Enum):
+    float16 = "float16"
+    float32 = "float32"
+    float64 = "float64"
+    bfloat16 = "bfloat16"
+    int8 = "int8"
+    int16 = "int16"
+    int32 = "int32"
+    int64 = "int64"
+    uint8 = "uint8"
+    bool = "bool"
+
+    @classmethod
+    def _missing_(cls, value: object) -> "DType":
+        raise UnsupportedDTypeError(value)
+
+    def __repr__(self) -> str:
+        return f"namitorch.{self.value}"
+
+    def __str__(self) -> str:
+        return repr(self)
+
+    @property
+    def itemsize(self) -> int:
+        return _ITEMSIZE[self]
+
+    @property
+    def bits(self) -> int:
+        return self.itemsize * 8
+
+    @property
+    def numpy_dtype(self) -> np.dtype:
+        if self is DType.bfloat16:
+            raise TypeError("bfloat16 has no NumPy dtype; use float32 values or uint16 bit patterns.")
+        return np.dtype(self.value)
+
+    @property
+    def torch_dtype(self) -> torch.dtype:
+        return _TORCH[self]
+
+    @property
+    def code(self) -> int:
+        """C-ABI storage code (NT_F32 ...); NT_DTYPE_NONE for non-floating types."""
+        return _CODES.get(self, _native.NT_DTYPE_NONE)
+
+    @property
+    def is_floating_point(self) -> bool:
+        return self in (DType.float16, DType.float32, DType.float64, DType.bfloat16)
+
+    @property
+    def is_integer(self) -> bool:
+        return self in (DType.int8, DType.int16, DType.int32, DType.int64, DType.uint8)
+
+    @property
+    def can_require_grad(self) -> bool:
+        return self.is_floating_point
+
+    @property
+    def finfo_max(self) -> float:
+        if self is DType.bfloat16:
+            return float.fromhex("0x1.fep127")
+        return float(np.finfo(self.numpy_dtype).max)
+
+
+float16 = DType.float16
+float32 = DType.float32
+float64 = DType.float64
+bfloat16 = DType.bfloat16
+int8 = DType.int8
+int16 = DType.int16
+int32 = DType.int32
+int64 = DType.int64
+uint8 = DType.uint8
+bool_ = DType.bool
+
+_ITEMSIZE = {float16: 2, float32: 4, float64: 8, bfloat16: 2, int8: 1, int16: 2, int32: 4, int64: 8, uint8: 1, bool_: 1}
+_TORCH = {
+    float16: torch.float16, float32: torch.float32, float64: torch.float64, bfloat16: torch.bfloat16,
+    int8: torch.int8, int16: torch.int16, int32: torch.int32, int64: torch.int64, uint8: torch.uint8, bool_: torch.bool,
+}
+_FROM_TORCH = {value: key for key, value in _TORCH.items()}
+_CODES = {float32: _native.NT_F32, float16: _native.NT_F16, bfloat16: _native.NT_BF16, float64: _native.NT_F64}
+
+
+def normalize_dtype(value: object) -> DType:
+    if isinstance(value, DType):
+        return value
+    if isinstance(value, torch.dtype):
+        if value not in _FROM_TORCH:
+            raise UnsupportedDTypeError(value)
+        return _FROM_TORCH[value]
+    if isinstance(value, str):
+        return DType("bool" if value == "bool_" else value)
+    try:
+        return from_numpy_dtype(np.dtype(value))
+    except TypeError:
+        raise UnsupportedDTypeError(value) from None
+
+
+def from_numpy_dtype(value: np.dtype) -> DType:
+    name = np.dtype(value).name
+    try:
+        return DType(name)
+    except UnsupportedDTypeError:
+        raise
+    except ValueError:
+        raise UnsupportedDTypeError(value) from None
+
+
+def from_torch_dtype(value: torch.dtype) -> DType:
+    if value not in _FROM_TORCH:
+        raise UnsupportedDTypeError(value)
+    return _FROM_TORCH[value]
+
+
+__all__ = ["DType", "UnsupportedDTypeError", "normalize_dtype", "from_numpy_dtype", "from_torch_dtype",
+           "float16", "float32", "float64", "bfloat16"]

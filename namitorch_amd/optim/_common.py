@@ -1,0 +1,215 @@
+"""First-order optimizer machinery (namitorch/optim/_common.py).
+
+Option validation (``_real_option``/``_bool_option``, _common.py:16-36), the
+rounding of host scalars to the parameter dtype (``_scalar``, 39-47) and the
+step orchestration of ``_FirstOrderOptimizer.step`` (133-167) keep the
+reference's checks, order and messages.  What changes is the update: the
+reference loops over parameters in Python and launches one kernel each
+(165-166); here every parameter of a step is handed to
+``_update_many``, which groups them by device and storage layout and
+launches one multi-tensor kernel per group.
+
+Per-step validation is memoized where its inputs cannot have changed:
+``_scalar`` checks depend only on (dtype, option values), and the
+"exp_avg_sq is nonnegative" state check (a full read of the buffer in the
+reference) is skipped for buffers whose version counter shows that only this
+optimizer's kernels wrote them since the last check — those kernels cannot
+produce a negative value.
+"""
+
+from __future__ import annotations
+
+import math
+from numbers import Real
+
+import numpy as np
+import torch
+
+from ..backends import ensure_same_device, get_backend
+from ..dtype import DType, float32, from_numpy_dtype, from_torch_dtype
+from ..tensor import Tensor, enable_grad, no_grad
+from .optimizer import Optimizer
+
+
+def _real_option(options: dict, name: str, positive: bool = False, unit_interval: bool = False) -> float:
+    if name not in options:
+        raise ValueError(f"Missing optimizer option {name!r}.")
+    value = options[name]
+    if isinstance(value, (bool, np.bool_)) or not isinstance(value, Real):
+        raise TypeError(f"Optimizer {name} must be a real scalar.")
+    try:
+        value = float(value)
+    except OverflowError:
+        raise ValueError(f"Optimizer {name} must be finite.") from None
+    if not math.isfinite(value) or value < 0 or (positive and value == 0) or (unit_interval and value >= 1):
+        constraint = "in [0, 1)" if unit_interval else "positive" if positive else "nonnegative"
+        raise ValueError(f"Optimizer {name} must be finite and {constraint}.")
+    options[name] = value
+    return value
+
+
+def _bool_option(options: dict, name: str) -> bool:
+    if name not in options or type(options[name]) is not bool:
+        raise TypeError(f"Optimizer {name} must be a Python bool.")
+    return options[name]
+
+
+def _round_scalar(dtype: DType, value: float, name: str = "coefficient") -> float:
+    """Round a host float to `dtype` once (RNE), as ``dtype.type(value)``."""
+    if not math.isfinite(value) or abs(value) > dtype.finfo_max:
+        raise ValueError(f"Optimizer {name} must be representable in {dtype.name}.")
+    if dtype is DType.float64:
+        result = float(value)
+    elif dtype is DType.bfloat16:
+        from ..tensor import _bf16_bits_from_f64
+        bits = int(_bf16_bits_from_f64(np.asarray([value]))[0])
+        result = float(np.array([bits << 16], dtype=np.uint32).view(np.float32)[0])
+    else:
+        with np.errstate(under="ignore"):
+            result = float(dtype.numpy_dtype.type(value))
+    if name == "eps" and result == 0:
+        raise ValueError(f"Optimizer eps must remain positive in {dtype.name}.")
+    return result
+
+
+def _scalar(parameter: Tensor, value: float, name: str = "coefficient"):
+    """The reference's ``_scalar``: `value` rounded to the parameter dtype."""
+    return _round_scalar(parameter.dtype, value, name)
+
+
+class _FirstOrderOptimizer(Optimizer):
+    _state_buffers = ()
+    _required_buffers = ()
+    _has_step = False
+    _nonnegative_buffers = ()
+    _decoupled_weight_decay = False
+
+    def _prepare_options(self, options: dict, path: str) -> dict:
+        prepared = super()._prepare_options(options, path)
+        _real_option(prepared, "lr")
+        _real_option(prepared, "weight_decay")
+        _bool_option(prepared, "maximize")
+        return prepared
+
+    # ---- state ------------------------------------------------------------------------
+    def _state_dtype(self, parameter: Tensor, name: str) -> DType:
+        """dtype every state buffer must have (the parameter's by default)."""
+        return parameter.dtype
+
+    def _allowed_state(self) -> tuple[set, set]:
+        allowed = set(self._state_buffers) | ({"step"} if self._has_step else set())
+        required = set(self._required_buffers) | ({"step"} if self._has_step else set())
+        return allowed, required
+
+    def _check_state(self, values: dict, parameter: Tensor, path: str, runtime: bool = False) -> None:
+        if not isinstance(values, dict):
+            raise TypeError(f"{path} must be a dictionary.")
+        if not values:
+            return
+        allowed, required = self._allowed_state()
+        if not set(values) <= allowed or not required <= values.keys():
+            raise ValueError(f"{path} has invalid state fields for {type(self).__name__}.")
+        if self._has_step and (type(values["step"]) is not int or values["step"] < 0):
+            raise ValueError(f"{path} step must be a nonnegative Python integer.")
+        for name in self._state_buffers:
+            if name not in values:
+                continue
+            value = values[name]
+            if not isinstance(value, (Tensor, np.ndarray, torch.Tensor)):
+                raise TypeError(f"{path}[{name!r}] must be a floating Tensor or NumPy array.")
+            if isinstance(value, Tensor):
+                dtype = value.dtype
+            elif isinstance(value, torch.Tensor):
+                dtype = from_torch_dtype(value.dtype)
+            else:
+                dtype = from_numpy_dtype(value.dtype)
+            if not dtype.is_floating_point:
+                raise TypeError(f"{path}[{name!r}] must have a floating dtype.")
+            if tuple(value.shape) != parameter.shape:
+                raise ValueError(f"{path}[{name!r}] shape {tuple(value.shape)} must equal parameter shape {parameter.shape}.")
+            if name in self._nonnegative_buffers and self._has_negative(value):
+                raise ValueError(f"{path}[{name!r}] must be nonnegative.")
+            if runtime:
+                ensure_same_device(parameter, value)
+                expected = self._state_dtype(parameter, name)
+                if not isinstance(value, Tensor) or dtype is not expected:
+                    raise TypeError(f"{path}[{name!r}] must be a Tensor with parameter dtype {expected.name}.")
+                if value.requires_grad or not value._writable:
+                    raise RuntimeError(f"{path}[{name!r}] must be writable and detached from autograd.")
+
+    @staticmethod
+    def _has_negative(value) -> bool:
+        if isinstance(value, Tensor):
+            if value._clean_version is not None and value._clean_version == value._version:
+                return False      # written only by this optimizer's kernels since the last check
+            if value.device.type == "cpu":
+                result = bool((value._data.to(torch.float32) < 0).any())
+            else:
+                result = get_backend(value).any_negative(value._data, value.dtype.code)
+            if not result:
+                value._clean_version = value._version
+            return result
+        if isinstance(value, torch.Tensor):
+            return bool((value.to(torch.float32) < 0).any())
+        return bool(np.any(np.less(value, 0)))
+
+    def _prepare_state(self, values: dict, parameter: Tensor, path: str) -> dict:
+        copied = super()._prepare_state(values, parameter, path)
+        self._check_state(copied, parameter, path)
+        if copied and not parameter.dtype.is_floating_point:
+            raise TypeError("Nonfloating parameters cannot have optimizer accumulation buffers.")
+        for name in self._state_buffers:
+            if name in copied:
+                copied[name] = Tensor(copied[name], dtype=self._state_dtype(parameter, name), device=parameter.device)
+        return copied
+
+    # ---- step ----------------------------------------------------------------------------
+    def _validate_entry(self, parameter: Tensor, prepared: dict, checked: set) -> None:
+        key = (parameter.dtype, id(prepared))
+        if key in checked:
+            return
+        for name, value in prepared.items():
+            if type(value) is float:
+                _scalar(parameter, value, name)
+        if self._decoupled_weight_decay:
+            _scalar(parameter, 1 - prepared["lr"] * prepared["weight_decay"], "decay factor")
+        checked.add(key)
+
+    def step(self, closure=None):
+        if closure is not None and not callable(closure):
+            raise TypeError("Optimizer closure must be callable or None.")
+        loss = None
+        if closure is not None:
+            with enable_grad():
+                loss = closure()
+        entries = list(self._parameters_with_grad())
+        options = {
+            id(group): self._prepare_options({key: value for key, value in group.items() if key != "params"}, "param_group")
+            for group in self.param_groups
+        }
+        checked: set = set()
+        validate_update = getattr(self, "_validate_update", None)
+        for group, parameter, gradient in entries:
+            if not parameter.dtype.is_floating_point:
+                raise TypeError("Optimizer updates require floating parameters.")
+            if not parameter._writable:
+                raise RuntimeError("Optimizer cannot update read-only parameter storage.")
+            prepared = options[id(group)]
+            self._validate_entry(parameter, prepared, checked)
+            self._check_state(self.state.get(id(parameter), {}), parameter, "parameter state", runtime=True)
+            if validate_update is not None:
+                validate_update(parameter, gradient, prepared)
+        with no_grad():
+            self._update_many([(parameter, gradient, options[id(group)]) for group, parameter, gradient in entries])
+        return loss
+
+    def _update_many(self, items) -> None:
+        """Apply the update to every (parameter, gradient, options) of a step."""
+        update = getattr(self, "_update_parameter", None)
+        if not callable(update):
+            raise RuntimeError("Optimizer subclass must implement parameter updates.")
+        for parameter, gradient, prepared in items:
+            update(parameter, gradient, prepared)
+
+
+__all__ = ["_FirstOrderOptimizer", "_real_option", "_bool_option", "_scalar", "_round_scalar"]

@@ -1,0 +1,256 @@
+"""Gradient norm and clipping (namitorch/optim/clip_grad.py) on the MI355X.
+
+``clip_grad_norm_``/``get_grad_norm`` keep the reference's argument checks,
+errors and return value (a 0-d float64 Tensor on the gradients' device).
+The norm follows ``_total_norm`` (clip_grad.py:63-79): a non-finite or zero
+max-abs prescale is itself the result (and the result for norm_type=inf);
+otherwise the p-norm in float64.  For p = 2 the device reduces sum(g*g) in
+float64 in one pass (no max-abs prescale is needed: float64 cannot
+overflow or underflow on squares of float32/16 values), so the norm agrees
+with NumPy's to a few float64 ulps rather than bit for bit; other p use the
+prescaled form with a second pass.  The reduction order is fixed, so the
+result is deterministic.
+
+Clipping multiplies each gradient by ``max_norm / (norm + 1e-6)`` in
+float64 and rounds once to the gradient dtype (clip_grad.py:106-111).  The
+rewrite is recorded on the gradients (see ``GradTransform``) and fused into
+the next kernel that reads them.
+"""
+
+from __future__ import annotations
+
+import math
+from numbers import Real
+
+import numpy as np
+import torch
+
+from ..backends import ensure_same_device, get_backend
+from ..dtype import float64
+from ..tensor import GradTransform, Tensor, no_grad
+
+_NORM_EPS = 1e-6
+
+
+def _nonnegative(value: object, name: str) -> float:
+    if isinstance(value, (bool, np.bool_)) or not isinstance(value, Real):
+        raise TypeError(f"{name} must be a finite nonnegative real scalar.")
+    try:
+        value = float(value)
+    except OverflowError:
+        raise ValueError(f"{name} must be finite.") from None
+    if not math.isfinite(value) or value < 0:
+        raise ValueError(f"{name} must be finite and nonnegative.")
+    return value
+
+
+def _norm_type(value: object) -> float:
+    if isinstance(value, (bool, np.bool_)) or not isinstance(value, Real):
+        raise TypeError("norm_type must be a positive real scalar or positive infinity.")
+    try:
+        value = float(value)
+    except OverflowError:
+        raise ValueError("norm_type is outside the supported range.") from None
+    if math.isnan(value) or value <= 0:
+        raise ValueError("norm_type must be positive or positive infinity.")
+    return value
+
+
+def _gradients(parameters) -> list[Tensor]:
+    if isinstance(parameters, Tensor):
+        parameters = (parameters,)
+    if isinstance(parameters, (dict, str, bytes, set, frozenset)):
+        raise TypeError("parameters must be a Tensor or an ordered iterable of Tensors.")
+    try:
+        parameters = iter(parameters)
+    except TypeError:
+        raise TypeError("parameters must be a Tensor or an ordered iterable of Tensors.") from None
+    gradients = []
+    seen = set()
+    for parameter in parameters:
+        if not isinstance(parameter, Tensor):
+            raise TypeError("parameters must contain only NamiTorch Tensors.")
+        gradient = parameter.grad
+        if gradient is None or id(gradient) in seen:
+            continue
+        if not isinstance(gradient, Tensor) or not gradient.dtype.is_floating_point:
+            raise TypeError("Gradients must be floating NamiTorch Tensors.")
+        if gradient.shape != parameter.shape:
+            raise ValueError(f"Gradient shape {gradient.shape} does not match parameter shape {parameter.shape}.")
+        ensure_same_device(parameter, gradient)
+        seen.add(id(gradient))
+        gradients.append(gradient)
+    return gradients
+
+
+class GradStats:
+    """float64 sum of squares, max |g| and non-finite flags of a gradient set."""
+
+    __slots__ = ("sumsq", "amax", "has_nan", "has_inf")
+
+    def __init__(self, sumsq=0.0, amax=0.0, has_nan=False, has_inf=False):
+        self.sumsq, self.amax, self.has_nan, self.has_inf = sumsq, amax, has_nan, has_inf
+
+    def merge(self, other: "GradStats") -> None:
+        self.sumsq += other.sumsq
+        self.amax = max(self.amax, other.amax)
+        self.has_nan |= other.has_nan
+        self.has_inf |= other.has_inf
+
+    @property
+    def finite(self) -> bool:
+        return not (self.has_nan or self.has_inf)
+
+    def prescale(self) -> float:
+        """The reference's max-abs prescale including NaN/inf propagation."""
+        if self.has_nan:
+            return math.nan
+        if self.has_inf:
+            return math.inf
+        return self.amax
+
+
+# Statistics of the last device pre-pass, reused by clip_grad_norm_ when it
+# sees the same gradients at the same versions with the same pending transform.
+_last_stats: dict = {}
+
+
+def _stats_key(gradients) -> frozenset:
+    return frozenset((id(gradient), gradient._version, gradient._pending) for gradient in gradients)
+
+
+def _remember_stats(gradients, stats: GradStats) -> None:
+    _last_stats.clear()
+    _last_stats[_stats_key(gradients)] = (list(gradients), stats)
+
+
+def _device_groups(gradients) -> dict:
+    groups: dict = {}
+    for gradient in gradients:
+        groups.setdefault((get_backend(gradient), gradient.dtype), []).append(gradient)
+    return groups
+
+
+def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tuple[GradStats, dict]:
+    """Run the device pre-pass over `gradients` (with their pending unscale)
+    and return the merged statistics; also the per-group control blocks."""
+    stats = GradStats()
+    blocks = {}
+    for (backend, dtype), members in _device_groups(gradients).items():
+        if backend.adamw is None:
+            backend._unsupported("Gradient norms")
+        transforms = {gradient._pending for gradient in members}
+        if len(transforms) > 1 or any(t is not None and t.clip is not None for t in transforms):
+            for gradient in members:
+                gradient._materialize()
+            scale = None
+        else:
+            transform = next(iter(transforms))
+            scale = None if transform is None else transform.scale
+        layout = (-1, dtype.code, -1, -1)
+        plan = backend.plan(backend.grad_rows(members), layout)
+        block = backend.new_ctrl()
+        backend.grad_prepass(plan, scale)
+        backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0)
+        ctrl = backend.read_ctrl(block)
+        stats.merge(GradStats(ctrl.sumsq, ctrl.amax, bool(ctrl.has_nan), bool(ctrl.found_inf and not ctrl.has_nan)))
+        blocks[(backend, dtype)] = (plan, block, scale)
+    if remember:
+        _remember_stats(gradients, stats)
+    return stats, blocks
+
+
+def _pow_total(blocks, amax: float, order: float) -> float:
+    """Sum over gradients of (|g|/amax)^p in float64 (clip_grad.py:73-76)."""
+    total = 0.0
+    for (backend, _), (plan, block, scale) in blocks.items():
+        ctrl = backend.read_ctrl(block)
+        ctrl.amax = amax
+        import ctypes
+        from .. import _native
+        with backend.context():
+            _native.call("nt_memcpy_h2d", block.data_ptr(), ctypes.addressof(ctrl), ctypes.sizeof(ctrl), backend.stream())
+        backend.grad_norm_pow(plan, block.data_ptr(), order, -1.0, scale)
+        total += backend.read_ctrl(block).sumsq
+    return total
+
+
+def _total_norm(gradients: list[Tensor], norm_type: float) -> float:
+    if not gradients:
+        return 0.0
+    key = _stats_key(gradients)
+    cached = _last_stats.get(key)
+    if cached is not None and (norm_type == 2 or math.isinf(norm_type)):
+        stats, blocks = cached[1], None
+    else:
+        stats, blocks = grad_stats(gradients)
+    scale = stats.prescale()
+    if not math.isfinite(scale) or scale == 0 or math.isinf(norm_type):
+        return scale
+    if norm_type == 2:
+        return math.sqrt(stats.sumsq)
+    if blocks is None:
+        stats, blocks = grad_stats(gradients)
+    total = _pow_total(blocks, scale, norm_type)
+    with np.errstate(over="ignore", divide="ignore", invalid="ignore", under="ignore"):
+        result = float(np.float64(scale) * np.power(np.float64(total), 1 / norm_type))
+        if not math.isfinite(result):
+            result = float(np.exp(np.log(np.float64(scale)) + np.log(np.float64(total)) / norm_type))
+    return result
+
+
+def _norm_tensor(norm: float, gradients) -> Tensor:
+    device = gradients[0].device if gradients else None
+    storage = torch.tensor(norm, dtype=torch.float64, device=None if device is None else device.torch)
+    return Tensor._from_storage(storage, False)
+
+
+def get_grad_norm(parameters, norm_type: float = 2) -> Tensor:
+    order = _norm_type(norm_type)
+    gradients = _gradients(parameters)
+    return _norm_tensor(_total_norm(gradients, order), gradients)
+
+
+def _require_writable(gradients: list[Tensor]) -> None:
+    if any(not gradient._writable for gradient in gradients):
+        raise RuntimeError("Cannot clip read-only gradient storage.")
+
+
+def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_nonfinite: bool = False) -> Tensor:
+    maximum = _nonnegative(max_norm, "max_norm")
+    order = _norm_type(norm_type)
+    if type(error_if_nonfinite) is not bool:
+        raise TypeError("error_if_nonfinite must be a Python bool.")
+    gradients = _gradients(parameters)
+    norm = _total_norm(gradients, order)
+    if error_if_nonfinite and not math.isfinite(norm):
+        raise RuntimeError(f"Cannot clip gradients with nonfinite total norm {np.asarray(norm, dtype=np.float64)}.")
+    with np.errstate(invalid="ignore", divide="ignore"):
+        coefficient = float(np.divide(np.float64(maximum), np.add(np.float64(norm), _NORM_EPS)))
+    if coefficient < 1:
+        _require_writable(gradients)
+        with no_grad():
+            for gradient in gradients:
+                gradient._ensure_inplace_allowed()
+                pending = gradient._pending
+                if pending is not None and pending.clip is not None:
+                    gradient._materialize()
+                    pending = None
+                keep_finite = gradient._finite_version is not None and gradient._finite_version == gradient._version
+                gradient._pending = (pending or GradTransform()).then_clip(coefficient)
+                gradient._version_counter.increment()
+                if keep_finite:
+                    gradient._finite_version = gradient._version
+    return _norm_tensor(norm, gradients)
+
+
+def clip_grad_value_(parameters, clip_value: float) -> None:
+    bound = _nonnegative(clip_value, "clip_value")
+    gradients = _gradients(parameters)
+    _require_writable(gradients)
+    raise NotImplementedError(
+        f"clip_grad_value_ (bound {bound}) is outside the optimizer-step path this package accelerates."
+    )
+
+
+__all__ = ["get_grad_norm", "clip_grad_norm_", "clip_grad_value_", "grad_stats", "GradStats"]

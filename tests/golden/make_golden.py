@@ -1,0 +1,257 @@
+"""Write golden fixtures from the reference's own NumPy-backend code.
+
+Run in the build container only (the reference tree is not on the GPU box):
+
+    python tests/golden/make_golden.py /root/reference
+
+It imports ``namitorch`` from the given reference checkout, runs small,
+seeded cases of the optimizer-step path on the CPU (NumPy) backend and
+stores inputs and outputs as ``tests/golden/*.npz`` plus
+``tests/golden/golden.json`` (scalar sequences and exception texts).  The
+fixtures are data; nothing of the reference is copied.  These pin the
+oracle where closed forms cannot: the bit-level operation order of
+Adam/AdamW through ``Tensor.copy_``, the float16 array path, the
+GradScaler sequence and clip_grad_norm_'s rounding.
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+SEED = 1337
+STEPS = 10
+
+
+def _grads(n, steps, sigma, dtype, seed_base=SEED + 1000):
+    return [(np.random.Generator(np.random.PCG64(seed_base + k)).standard_normal(n, dtype=np.float32) * np.float32(sigma)).astype(dtype)
+            for k in range(steps)]
+
+
+def _params(n, dtype, seed=SEED, sigma=0.02):
+    return (np.random.Generator(np.random.PCG64(seed)).standard_normal(n, dtype=np.float32) * np.float32(sigma)).astype(dtype)
+
+
+def run_adam(nt, cls, p0, grads, **options):
+    param = nt.nn.Parameter(p0.copy())
+    optimizer = cls([param], **options)
+    for grad in grads:
+        param._grad = nt.Tensor(grad.copy())
+        optimizer.step()
+    state = optimizer.state[id(param)]
+    return (param._data.copy(), state["exp_avg"]._data.copy(), state["exp_avg_sq"]._data.copy(), state["step"])
+
+
+def adam_cases(nt):
+    cases = {}
+    n = 4099
+    p0 = _params(n, np.float32)
+    grads = _grads(n, STEPS, 1e-3, np.float32)
+    base = dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    variants = {
+        "adamw_f32": (nt.optim.AdamW, base),
+        "adamw_f32_maximize": (nt.optim.AdamW, dict(base, maximize=True)),
+        "adamw_f32_lr0": (nt.optim.AdamW, dict(base, lr=0.0)),
+        "adamw_f32_wd0": (nt.optim.AdamW, dict(base, weight_decay=0.0)),
+        "adamw_f32_defaults": (nt.optim.AdamW, {}),
+        "adam_f32_coupled": (nt.optim.Adam, base),
+    }
+    for name, (cls, options) in variants.items():
+        p, m, v, step = run_adam(nt, cls, p0, grads, **options)
+        cases[name] = dict(p0=p0, grads=np.stack(grads), p=p, m=m, v=v, step=np.int64(step),
+                           options=json.dumps({k: list(v) if isinstance(v, tuple) else v for k, v in options.items()}))
+    # bfloat16-valued float32 gradients: pins the master-weight extension.
+    bf = [(g.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32) for g in grads]
+    p, m, v, step = run_adam(nt, nt.optim.AdamW, p0, bf, **base)
+    cases["adamw_f32_bfgrads"] = dict(p0=p0, grads=np.stack(bf), p=p, m=m, v=v, step=np.int64(step),
+                                      options=json.dumps({k: list(v) if isinstance(v, tuple) else v for k, v in base.items()}))
+    # Special values: zeros, subnormals, huge, inf and NaN gradients.
+    m0 = 64
+    sp = _params(m0, np.float32, seed=7)
+    g = _grads(m0, 3, 1e-3, np.float32, seed_base=77)
+    g[0][:8] = [0.0, -0.0, 1e-40, -1e-42, 3e38, -3e38, np.float32(1e-45), 5e-39]
+    g[1][8:12] = [np.inf, -np.inf, np.nan, 0.0]
+    p, m, v, step = run_adam(nt, nt.optim.AdamW, sp, g, **base)
+    cases["adamw_f32_special"] = dict(p0=sp, grads=np.stack(g), p=p, m=m, v=v, step=np.int64(step),
+                                      options=json.dumps({k: list(v) if isinstance(v, tuple) else v for k, v in base.items()}))
+    # float16 parameters: the NumPy float16 array path.
+    h0 = _params(1000, np.float16, seed=11, sigma=0.5)
+    hg = _grads(1000, STEPS, 1e-2, np.float16, seed_base=111)
+    hopt = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-4, weight_decay=0.1)
+    p, m, v, step = run_adam(nt, nt.optim.AdamW, h0, hg, **hopt)
+    cases["adamw_f16"] = dict(p0=h0, grads=np.stack(hg), p=p, m=m, v=v, step=np.int64(step),
+                              options=json.dumps({k: list(v) if isinstance(v, tuple) else v for k, v in hopt.items()}))
+    # float64 parameters.
+    d0 = _params(513, np.float64, seed=13)
+    dg = _grads(513, 4, 1e-3, np.float64, seed_base=131)
+    p, m, v, step = run_adam(nt, nt.optim.AdamW, d0, dg, **base)
+    cases["adamw_f64"] = dict(p0=d0, grads=np.stack(dg), p=p, m=m, v=v, step=np.int64(step),
+                              options=json.dumps({k: list(v) if isinstance(v, tuple) else v for k, v in base.items()}))
+    for name, arrays in cases.items():
+        np.savez(HERE / f"{name}.npz", **arrays)
+    return sorted(cases)
+
+
+def clip_cases(nt):
+    rng = np.random.Generator(np.random.PCG64(21))
+    shapes = [(37,), (8, 16), (1000,), (3, 5, 7)]
+    out = {}
+    records = []
+    for dtype in (np.float32, np.float16):
+        for norm_type in (2.0, 1.0, 3.0, float("inf"), 0.5):
+            for max_norm, sigma in ((1.0, 0.5), (1e6, 0.5)):
+                grads = [(rng.standard_normal(s) * sigma).astype(dtype) for s in shapes]
+                params = [nt.nn.Parameter(np.zeros(s, dtype=dtype)) for s in shapes]
+                for param, grad in zip(params, grads):
+                    param._grad = nt.Tensor(grad.copy())
+                norm = nt.optim.clip_grad_norm_(params, max_norm, norm_type=norm_type)
+                key = f"clip_{np.dtype(dtype).name}_{norm_type}_{max_norm:g}"
+                for index, (grad, param) in enumerate(zip(grads, params)):
+                    out[f"{key}_in{index}"] = grad
+                    out[f"{key}_out{index}"] = param.grad._data.copy()
+                records.append(dict(key=key, dtype=np.dtype(dtype).name, norm_type=norm_type, max_norm=max_norm,
+                                    norm=float(norm._data), count=len(shapes)))
+    # Non-finite gradients (no error requested): inf -> coefficient 0 -> NaN/0 grads.
+    for label, poison in (("inf", np.inf), ("nan", np.nan)):
+        grads = [(rng.standard_normal(s) * 0.5).astype(np.float32) for s in shapes]
+        grads[2][5] = poison
+        params = [nt.nn.Parameter(np.zeros(s, dtype=np.float32)) for s in shapes]
+        for param, grad in zip(params, grads):
+            param._grad = nt.Tensor(grad.copy())
+        norm = nt.optim.clip_grad_norm_(params, 1.0)
+        key = f"clip_nonfinite_{label}"
+        for index, (grad, param) in enumerate(zip(grads, params)):
+            out[f"{key}_in{index}"] = grad
+            out[f"{key}_out{index}"] = param.grad._data.copy()
+        records.append(dict(key=key, dtype="float32", norm_type=2.0, max_norm=1.0, norm=float(norm._data), count=len(shapes)))
+    # All-zero gradients.
+    params = [nt.nn.Parameter(np.zeros(s, dtype=np.float32)) for s in shapes]
+    for param in params:
+        param._grad = nt.Tensor(np.zeros(param.shape, dtype=np.float32))
+    records.append(dict(key="clip_zero", dtype="float32", norm_type=2.0, max_norm=1.0,
+                        norm=float(nt.optim.clip_grad_norm_(params, 1.0)._data), count=0))
+    np.savez(HERE / "clip.npz", **out)
+    return records
+
+
+def scaler_cases(nt):
+    """The runner's AMP sequence (training/runner.py:234-254) on float32 and
+    float16 parameters, with an inf at step 4 and a NaN at step 7."""
+    results = {}
+    arrays = {}
+    for dtype, eps, sigma in ((np.float32, 1e-8, 1e-3), (np.float16, 1e-4, 1e-3)):
+        n = 777
+        p0 = _params(n, dtype, seed=31, sigma=0.5 if dtype == np.float16 else 0.02)
+        raw = _grads(n, STEPS, sigma, np.float32, seed_base=3100)
+        param = nt.nn.Parameter(p0.copy())
+        optimizer = nt.optim.AdamW([param], lr=1e-3, betas=(0.9, 0.999), eps=eps, weight_decay=0.1)
+        scaler = nt.amp.GradScaler(init_scale=65536.0, growth_interval=3)
+        finite_seq, updated_seq, scale_seq, norm_seq = [], [], [], []
+        grads_in = []
+        for k in range(STEPS):
+            loss = nt.Tensor(np.float32(1.0))
+            scaler.scale(loss)
+            scaled = (raw[k].astype(np.float64) * scaler.get_scale()).astype(dtype)
+            if k == 4:
+                scaled[10] = np.inf
+            if k == 7:
+                scaled[20] = np.nan
+            grads_in.append(scaled.copy())
+            param._grad = nt.Tensor(scaled)
+            finite = scaler.unscale_(optimizer)
+            norm = nt.optim.clip_grad_norm_([param], 1.0, error_if_nonfinite=True).item() if finite else None
+            updated = scaler.step(optimizer)
+            scaler.update()
+            finite_seq.append(bool(finite))
+            updated_seq.append(bool(updated))
+            scale_seq.append(scaler.get_scale())
+            norm_seq.append(norm)
+        name = f"scaler_{np.dtype(dtype).name}"
+        arrays[f"{name}_p0"] = p0
+        arrays[f"{name}_grads"] = np.stack(grads_in)
+        arrays[f"{name}_p"] = param._data.copy()
+        state = optimizer.state[id(param)]
+        arrays[f"{name}_m"] = state["exp_avg"]._data.copy()
+        arrays[f"{name}_v"] = state["exp_avg_sq"]._data.copy()
+        results[name] = dict(finite=finite_seq, updated=updated_seq, scale=scale_seq, norm=norm_seq,
+                             step=state["step"], eps=eps)
+    # Scale sequence under repeated overflow and growth (no optimizer arithmetic involved).
+    param = nt.nn.Parameter(np.zeros(4, dtype=np.float32))
+    optimizer = nt.optim.AdamW([param], lr=0.0)
+    scaler = nt.amp.GradScaler(init_scale=2.0 ** 120, growth_factor=4.0, backoff_factor=0.25, growth_interval=2)
+    pattern = [False, False, False, False, True, False, False, True, True, False, False, False]
+    sequence = []
+    for overflow in pattern:
+        scaler.scale(nt.Tensor(np.float32(1.0)))
+        grad = np.ones(4, dtype=np.float32)
+        if overflow:
+            grad[0] = np.inf
+        param._grad = nt.Tensor(grad)
+        scaler.step(optimizer)
+        scaler.update()
+        sequence.append(scaler.get_scale())
+    results["scale_sequence"] = dict(pattern=pattern, scale=sequence, init=2.0 ** 120, growth=4.0, backoff=0.25, interval=2)
+    np.savez(HERE / "scaler.npz", **arrays)
+    return results
+
+
+def error_texts(nt):
+    texts = {}
+    half = nt.nn.Parameter(np.zeros(3, dtype=np.float16))
+    half._grad = nt.Tensor(np.zeros(3, dtype=np.float16))
+    try:
+        nt.optim.AdamW([half], eps=1e-8).step()
+    except ValueError as error:
+        texts["eps_float16"] = str(error)
+    p = nt.nn.Parameter(np.zeros(3, dtype=np.float32))
+    p._grad = nt.Tensor(np.zeros(3, dtype=np.float32))
+    try:
+        nt.optim.AdamW([p], fused=True).step()
+    except RuntimeError as error:
+        texts["fused_true_unsupported"] = str(error)
+    try:
+        nt.optim.AdamW([p], fused=1)
+    except TypeError as error:
+        texts["fused_type"] = str(error)
+    try:
+        nt.optim.AdamW([p], betas=(0.9, 1.0))
+    except ValueError as error:
+        texts["beta_range"] = str(error)
+    scaler = nt.amp.GradScaler()
+    try:
+        scaler.unscale_(nt.optim.AdamW([p]))
+    except RuntimeError as error:
+        texts["unscale_before_scale"] = str(error)
+    try:
+        nt.optim.clip_grad_norm_([p], -1.0)
+    except ValueError as error:
+        texts["max_norm_negative"] = str(error)
+    bad = nt.nn.Parameter(np.zeros(3, dtype=np.float32))
+    bad._grad = nt.Tensor(np.array([1.0, np.inf, 0.0], dtype=np.float32))
+    try:
+        nt.optim.clip_grad_norm_([bad], 1.0, error_if_nonfinite=True)
+    except RuntimeError as error:
+        texts["nonfinite_norm"] = str(error)
+    return texts
+
+
+def main(reference: str) -> None:
+    sys.path.insert(0, reference)
+    import namitorch as nt  # the reference, on its NumPy (CPU) backend
+    golden = {
+        "source": "renderityai/NamiTorch NumPy backend (optim/adam.py, optim/clip_grad.py, amp.py)",
+        "numpy": np.__version__,
+        "adam_cases": adam_cases(nt),
+        "clip": clip_cases(nt),
+        "scaler": scaler_cases(nt),
+        "errors": error_texts(nt),
+    }
+    (HERE / "golden.json").write_text(json.dumps(golden, indent=1, sort_keys=True) + "\n")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,350 @@
+"""GPU parity: the gfx950 kernels against the oracle and the reference's
+golden fixtures.  Every test here needs an MI355X and the built library;
+nothing falls back to the CPU.
+
+Bars: bit-identical for float32/float16/float64 AdamW, unscale, found_inf,
+skip decisions and the loss-scale sequence; clipped gradients bit-identical
+(the clip coefficient comes from a float64 norm whose summation order
+differs from NumPy's, so the test allows the norm 1e-12 relative);
+model copies and bfloat16 moments bit-identical to RNE of the float32
+values.
+"""
+
+import json
+import math
+
+import numpy as np
+import pytest
+
+import namitorch_amd as nt
+from namitorch_amd import _native
+from oracle import adam as oadam
+from oracle import clip as oclip
+from oracle import lowp
+from oracle import scaler as oscaler
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+NORM_RTOL = 1e-12   # float64 norm: fixed device order vs NumPy pairwise order
+
+
+def _same(a, b):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype, (a.shape, b.shape, a.dtype, b.dtype)
+    nan = np.isnan(a.astype(np.float64)) & np.isnan(b.astype(np.float64))
+    same = (a.view(f"u{a.itemsize}") == b.view(f"u{b.itemsize}")) | nan
+    return bool(np.all(same)), int(np.count_nonzero(~same))
+
+
+def _rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def test_library_is_native_gfx950():
+    lib = _native.load()
+    count = _native.c_int32()
+    _native.check(lib.nt_device_count(_native.ctypes.byref(count)))
+    assert count.value >= 1
+    buf = _native.ctypes.create_string_buffer(64)
+    _native.check(lib.nt_device_arch(0, buf, 64))
+    assert buf.value.decode().startswith("gfx950"), buf.value
+    assert type(nt.get_backend(DEV)).__name__ == "HIPBackend"
+
+
+GOLDEN_ADAM = ["adamw_f32", "adamw_f32_maximize", "adamw_f32_lr0", "adamw_f32_wd0", "adamw_f32_defaults",
+               "adam_f32_coupled", "adamw_f32_special", "adamw_f16", "adamw_f64"]
+
+
+@pytest.mark.parametrize("name", GOLDEN_ADAM)
+@pytest.mark.parametrize("fused", [None, False])
+def test_adam_api_matches_reference_golden(golden_dir, name, fused):
+    data = np.load(golden_dir / f"{name}.npz")
+    options = json.loads(str(data["options"]))
+    if "betas" in options:
+        options["betas"] = tuple(options["betas"])
+    param = nt.Parameter(data["p0"], device=DEV)
+    if name.startswith("adam_"):
+        optimizer = nt.optim.Adam([param], **options)
+    else:
+        optimizer = nt.optim.AdamW([param], fused=fused, **options)
+    for grad in data["grads"]:
+        param.grad = nt.Tensor(grad, device=DEV)
+        optimizer.step()
+    state = optimizer.state[id(param)]
+    for label, got, want in (("p", param.numpy(), data["p"]), ("m", state["exp_avg"].numpy(), data["m"]),
+                             ("v", state["exp_avg_sq"].numpy(), data["v"])):
+        ok, bad = _same(got, want)
+        assert ok, f"{name} {label}: {bad} elements differ"
+    assert state["step"] == int(data["step"])
+
+
+def test_per_tensor_hook_matches_reference_golden(golden_dir):
+    """The reference's backend.adamw.run protocol (nt_adamw_f32)."""
+    import torch
+    data = np.load(golden_dir / "adamw_f32.npz")
+    backend = nt.get_backend(DEV)
+    p = torch.from_numpy(data["p0"].copy()).to(DEV)
+    m = torch.zeros_like(p)
+    v = torch.zeros_like(p)
+    assert backend.adamw.supports(p, p.clone(), m, v)
+    assert not backend.adamw.supports(p, p, m, v)          # overlapping
+    assert not backend.adamw.supports(p.double(), p.double())
+    for step, grad in enumerate(data["grads"], start=1):
+        g = torch.from_numpy(grad).to(DEV)
+        coefficients = oadam.coefficients(np.float32, 3e-4, (0.9, 0.999), 1e-8, 0.1, step)
+        assert backend.adamw.run(p, g, m, v, coefficients=coefficients, maximize=False, update_parameter=True)
+    assert _same(p.cpu().numpy(), data["p"])[0]
+    assert _same(m.cpu().numpy(), data["m"])[0]
+    assert _same(v.cpu().numpy(), data["v"])[0]
+    empty = torch.empty(0, device=DEV)
+    assert backend.adamw.run(empty, empty.clone(), empty.clone(), empty.clone(), coefficients=coefficients,
+                             maximize=False, update_parameter=True) is False
+
+
+def _small_gpt_shapes():
+    from namitorch_amd.param_lists import gpt2_shapes
+    return gpt2_shapes(vocab=1001, ctx=67, d=72, layers=2)
+
+
+def _make_params(shapes, dtype, seed=1337, sigma=0.02):
+    rng = _rng(seed)
+    return [(rng.standard_normal(int(np.prod(s)), dtype=np.float32) * np.float32(sigma)).reshape(s).astype(dtype)
+            for s in shapes]
+
+
+def _make_grads(shapes, step, sigma=1e-3, dtype=np.float32):
+    rng = _rng(1337 + 1000 + step)
+    return [(rng.standard_normal(int(np.prod(s)), dtype=np.float32) * np.float32(sigma)).reshape(s).astype(dtype)
+            for s in shapes]
+
+
+def _groups(params):
+    decay = [p for p in params if p.ndim >= 2]
+    rest = [p for p in params if p.ndim < 2]
+    return [{"params": decay, "weight_decay": 0.1}, {"params": rest, "weight_decay": 0.0}]
+
+
+def test_multi_tensor_fp32_gpt_layout_ten_steps():
+    """C2 layout at reduced width: 28 tensors, 2 decay groups, odd sizes."""
+    shapes = _small_gpt_shapes()
+    host = _make_params(shapes, np.float32)
+    params = [nt.Parameter(h, device=DEV) for h in host]
+    optimizer = nt.optim.AdamW(_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8)
+    ref_p = [h.copy() for h in host]
+    ref_m = [np.zeros_like(h) for h in host]
+    ref_v = [np.zeros_like(h) for h in host]
+    for step in range(1, 11):
+        grads = _make_grads(shapes, step)
+        for param, grad in zip(params, grads):
+            param.grad = nt.Tensor(grad, device=DEV)
+        optimizer.step()
+        for i, grad in enumerate(grads):
+            wd = 0.1 if len(shapes[i]) >= 2 else 0.0
+            oadam.adam_step(ref_p[i], grad, ref_m[i], ref_v[i], step, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+    for i, param in enumerate(params):
+        state = optimizer.state[id(param)]
+        assert _same(param.numpy(), ref_p[i])[0], shapes[i]
+        assert _same(state["exp_avg"].numpy(), ref_m[i])[0]
+        assert _same(state["exp_avg_sq"].numpy(), ref_v[i])[0]
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 8, 9, 2047, 2048, 2049, 16383, 16384, 16385, 40000])
+def test_adamw_sizes_and_tails(n):
+    rng = _rng(n + 5)
+    p0 = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    param = nt.Parameter(p0, device=DEV)
+    optimizer = nt.optim.AdamW([param], lr=1e-3, weight_decay=0.1)
+    rp, rm, rv = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    for step in range(1, 4):
+        g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+        param.grad = nt.Tensor(g, device=DEV)
+        optimizer.step()
+        oadam.adam_step(rp, g, rm, rv, step, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    assert _same(param.numpy(), rp)[0]
+    assert optimizer.state[id(param)]["step"] == 3
+    # fused semantics: no version bump for empty tensors
+    assert param._version == (0 if n == 0 else 3)
+
+
+def test_adamw_unaligned_storage_scalar_path():
+    import torch
+    base = torch.zeros(4099 + 1, dtype=torch.float32, device=DEV)
+    rng = _rng(3)
+    p0 = (rng.standard_normal(4099) * 0.1).astype(np.float32)
+    view = base[1:]
+    view.copy_(torch.from_numpy(p0))
+    param = nt.Parameter.__new__(nt.Parameter)
+    nt.Tensor._initialize(param, view, True)
+    assert param._ptr % 16 != 0
+    g = (rng.standard_normal(4099) * 1e-2).astype(np.float32)
+    param.grad = nt.Tensor(g, device=DEV)
+    optimizer = nt.optim.AdamW([param], lr=1e-3)
+    optimizer.step()
+    rp, rm, rv = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    oadam.adam_step(rp, g, rm, rv, 1, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
+    assert _same(param.numpy(), rp)[0]
+
+
+def test_more_than_sixteen_coefficient_slots():
+    """17 parameter groups with distinct lr in one step -> two launches."""
+    rng = _rng(17)
+    hosts = [(rng.standard_normal(100 + i) * 0.1).astype(np.float32) for i in range(17)]
+    params = [nt.Parameter(h, device=DEV) for h in hosts]
+    groups = [{"params": [p], "lr": 1e-3 * (i + 1)} for i, p in enumerate(params)]
+    optimizer = nt.optim.AdamW(groups)
+    grads = [(rng.standard_normal(h.size) * 1e-2).astype(np.float32) for h in hosts]
+    for p, g in zip(params, grads):
+        p.grad = nt.Tensor(g, device=DEV)
+    optimizer.step()
+    for i, (p, h, g) in enumerate(zip(params, hosts, grads)):
+        rp, rm, rv = h.copy(), np.zeros_like(h), np.zeros_like(h)
+        oadam.adam_step(rp, g, rm, rv, 1, lr=1e-3 * (i + 1), betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
+        assert _same(p.numpy(), rp)[0], i
+
+
+def test_per_parameter_step_counts_differ():
+    """Params whose step counts diverge (one had no grad) use their own bias corrections."""
+    rng = _rng(23)
+    a0 = (rng.standard_normal(300) * 0.1).astype(np.float32)
+    b0 = (rng.standard_normal(301) * 0.1).astype(np.float32)
+    a, b = nt.Parameter(a0, device=DEV), nt.Parameter(b0, device=DEV)
+    optimizer = nt.optim.AdamW([a, b], lr=1e-3)
+    ra, rb = [a0.copy(), np.zeros_like(a0), np.zeros_like(a0)], [b0.copy(), np.zeros_like(b0), np.zeros_like(b0)]
+    steps = {"a": 0, "b": 0}
+    for k in range(5):
+        ga = (rng.standard_normal(300) * 1e-2).astype(np.float32)
+        gb = (rng.standard_normal(301) * 1e-2).astype(np.float32)
+        a.grad = nt.Tensor(ga, device=DEV)
+        b.grad = None if k in (1, 2) else nt.Tensor(gb, device=DEV)
+        optimizer.step()
+        steps["a"] += 1
+        oadam.adam_step(*ra[:1], ga, *ra[1:], steps["a"], lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
+        if b.grad is not None:
+            steps["b"] += 1
+            oadam.adam_step(*rb[:1], gb, *rb[1:], steps["b"], lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
+    assert _same(a.numpy(), ra[0])[0] and _same(b.numpy(), rb[0])[0]
+    assert optimizer.state[id(b)]["step"] == 3
+
+
+# ---- master weights / low precision --------------------------------------------------------
+@pytest.mark.parametrize("param_dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("grad_dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("state_dtype", [None, "bfloat16"])
+def test_master_weights_match_oracle(param_dtype, grad_dtype, state_dtype):
+    shapes = [(67, 33), (33,), (1000,), (5, 7, 9)]
+    rng = _rng(99)
+    host = [(rng.standard_normal(s) * 0.05).astype(np.float32) for s in shapes]
+    host_lp = [lowp.round_bf16(h) if param_dtype == "bfloat16" else h.astype(param_dtype).astype(np.float32) for h in host]
+    params = [nt.Parameter(h, dtype=param_dtype, device=DEV) for h in host_lp]
+    optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.1, master_weights=True, state_dtype=state_dtype)
+    masters = [h.copy() for h in host_lp]
+    ms = [np.zeros_like(h) for h in host_lp]
+    vs = [np.zeros_like(h) for h in host_lp]
+    for step in range(1, 6):
+        for i, (p, s) in enumerate(zip(params, shapes)):
+            g32 = (rng.standard_normal(s) * 1e-3).astype(np.float32)
+            g = lowp.round_bf16(g32) if grad_dtype == "bfloat16" else g32.astype(grad_dtype).astype(np.float32)
+            p.grad = nt.Tensor(g, dtype=grad_dtype, device=DEV)
+            oadam.master_step(masters[i], g, ms[i], vs[i], step, lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+                              weight_decay=0.1, state_bf16=state_dtype == "bfloat16")
+        optimizer.step()
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        assert _same(state["master"].numpy(), masters[i])[0]
+        assert _same(state["exp_avg"].numpy(), ms[i])[0]
+        assert _same(state["exp_avg_sq"].numpy(), vs[i])[0]
+        copy = oadam.copy_out(masters[i], param_dtype)   # float16 array, or float32 values for bf16/fp32
+        assert _same(p.numpy(), copy)[0]
+
+
+# ---- GradScaler / clip -----------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_grad_scaler_sequence_matches_reference_golden(golden_dir, dtype):
+    golden = json.loads((golden_dir / "golden.json").read_text())["scaler"][f"scaler_{dtype}"]
+    arrays = np.load(golden_dir / "scaler.npz")
+    name = f"scaler_{dtype}"
+    param = nt.Parameter(arrays[f"{name}_p0"], device=DEV)
+    optimizer = nt.optim.AdamW([param], lr=1e-3, betas=(0.9, 0.999), eps=golden["eps"], weight_decay=0.1)
+    scaler = nt.GradScaler(init_scale=65536.0, growth_interval=3)
+    for k, grad in enumerate(arrays[f"{name}_grads"]):
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        param.grad = nt.Tensor(grad, device=DEV)
+        finite = scaler.unscale_(optimizer)
+        norm = nt.optim.clip_grad_norm_([param], 1.0, error_if_nonfinite=True).item() if finite else None
+        updated = scaler.step(optimizer)
+        scaler.update()
+        assert finite == golden["finite"][k] and updated == golden["updated"][k]
+        assert scaler.get_scale() == golden["scale"][k]
+        if norm is not None:
+            assert abs(norm - golden["norm"][k]) <= NORM_RTOL * golden["norm"][k]
+    state = optimizer.state[id(param)]
+    assert state["step"] == golden["step"]
+    assert _same(param.numpy(), arrays[f"{name}_p"])[0]
+    assert _same(state["exp_avg"].numpy(), arrays[f"{name}_m"])[0]
+    assert _same(state["exp_avg_sq"].numpy(), arrays[f"{name}_v"])[0]
+
+
+def test_unscaled_grads_visible_in_place():
+    rng = _rng(41)
+    g = (rng.standard_normal(5001) * 70).astype(np.float16)
+    param = nt.Parameter(np.zeros(5001, dtype=np.float16), device=DEV)
+    optimizer = nt.optim.AdamW([param], eps=1e-4)
+    scaler = nt.GradScaler(init_scale=3000.0)
+    scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+    param.grad = nt.Tensor(g, device=DEV)
+    version = param.grad._version
+    assert scaler.unscale_(optimizer)
+    assert param.grad._version == version + 1
+    assert _same(param.grad.numpy(), oscaler.unscale(g, 3000.0))[0]
+
+
+def test_unscale_overflow_to_inf_in_grad_dtype():
+    """scale < 1: finite float16 grads overflow after division -> found_inf."""
+    param = nt.Parameter(np.zeros(10, dtype=np.float16), device=DEV)
+    optimizer = nt.optim.AdamW([param], eps=1e-4)
+    scaler = nt.GradScaler(init_scale=0.5)
+    scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+    g = np.full(10, 1.0, dtype=np.float16)
+    g[3] = 60000.0
+    param.grad = nt.Tensor(g, device=DEV)
+    assert scaler.unscale_(optimizer) is False
+    assert scaler.step(optimizer) is False
+    scaler.update()
+    assert scaler.get_scale() == 0.25
+    assert np.array_equal(param.numpy(), np.zeros(10, dtype=np.float16))
+
+
+def test_clip_matches_reference_golden(golden_dir):
+    data = np.load(golden_dir / "clip.npz")
+    records = json.loads((golden_dir / "golden.json").read_text())["clip"]
+    for record in records:
+        key = record["key"]
+        if record["count"] == 0:
+            continue
+        grads = [data[f"{key}_in{i}"] for i in range(record["count"])]
+        params = [nt.Parameter(np.zeros(g.shape, dtype=g.dtype), device=DEV) for g in grads]
+        for p, g in zip(params, grads):
+            p.grad = nt.Tensor(g, device=DEV)
+        norm = nt.optim.clip_grad_norm_(params, record["max_norm"], norm_type=record["norm_type"]).item()
+        want = record["norm"]
+        assert (math.isnan(norm) and math.isnan(want)) or norm == want or abs(norm - want) <= NORM_RTOL * abs(want), key
+        for i, p in enumerate(params):
+            ok, bad = _same(p.grad.numpy(), data[f"{key}_out{i}"])
+            assert ok, f"{key}[{i}]: {bad} differ"
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_clip_single_rounding_from_float64(dtype):
+    rng = _rng(57)
+    g32 = (rng.standard_normal(20001) * 3).astype(np.float32)
+    g = lowp.round_bf16(g32) if dtype == "bfloat16" else g32.astype(dtype).astype(np.float32)
+    param = nt.Parameter(np.zeros(g.shape, dtype=np.float32), dtype=dtype, device=DEV)
+    param.grad = nt.Tensor(g, dtype=dtype, device=DEV)
+    norm = nt.optim.clip_grad_norm_([param], 1.0).item()
+    want = oclip.total_norm([g.astype(np.float64)])
+    assert abs(norm - want) <= NORM_RTOL * want
+    coefficient = oclip.clip_coefficient(1.0, norm)
+    expected = oclip.clip_apply(g.astype(np.float64), coefficient, dtype)
+    got = param.grad.numpy()      # float16 array, or float32 values for bf16/fp32
+    assert _same(got, expected)[0]

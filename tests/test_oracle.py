@@ -1,0 +1,259 @@
+"""Pins of the CPU oracle (no GPU).
+
+Each oracle function is checked against something other than itself:
+golden fixtures written by the reference's own code (tests/golden), closed
+forms, invariants, library routines (torch's RNE bfloat16 conversion,
+math.fsum) or exact rational arithmetic.
+"""
+
+import json
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import adam, clip, lowp, scaler
+
+GOLDEN_CASES = ["adamw_f32", "adamw_f32_maximize", "adamw_f32_lr0", "adamw_f32_wd0", "adamw_f32_defaults",
+                "adam_f32_coupled", "adamw_f32_bfgrads", "adamw_f32_special", "adamw_f16", "adamw_f64"]
+
+
+def _load(golden_dir, name):
+    data = np.load(golden_dir / f"{name}.npz")
+    options = json.loads(str(data["options"]))
+    return data, options
+
+
+def run_oracle(data, options, decoupled=True):
+    p = data["p0"].copy()
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    full = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2, maximize=False)
+    full.update(options)
+    full["betas"] = tuple(full["betas"])
+    for step, grad in enumerate(data["grads"], start=1):
+        adam.adam_step(p, grad, m, v, step, decoupled=decoupled, **full)
+    return p, m, v
+
+
+def _same(a, b):
+    """Bit-identical up to NaN payloads."""
+    a = np.asarray(a)
+    b = np.asarray(b)
+    nan = np.isnan(a.astype(np.float64)) & np.isnan(b.astype(np.float64))
+    return bool(np.all((a.view(f"u{a.itemsize}") == b.view(f"u{b.itemsize}")) | nan))
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_adam_oracle_matches_reference_golden(golden_dir, name):
+    data, options = _load(golden_dir, name)
+    p, m, v = run_oracle(data, options, decoupled=not name.startswith("adam_"))
+    assert _same(p, data["p"]) and _same(m, data["m"]) and _same(v, data["v"])
+    assert int(data["step"]) == len(data["grads"])
+
+
+def test_adam_oracle_step1_closed_form():
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(10000) * 1e-3).astype(np.float32)
+    p = np.zeros_like(g)
+    m = np.zeros_like(g)
+    v = np.zeros_like(g)
+    adam.adam_step(p, g, m, v, 1, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0)
+    expected = -1e-3 * g.astype(np.float64) / (np.abs(g.astype(np.float64)) + 1e-8)
+    assert np.allclose(p, expected, rtol=2e-6, atol=0)
+    assert np.allclose(m, 0.1 * g.astype(np.float64), rtol=1e-6)
+    assert np.allclose(v, 0.001 * g.astype(np.float64) ** 2, rtol=1e-6)
+
+
+def test_adam_oracle_zero_gradient_leaves_params_and_decays_moments():
+    p = np.linspace(-1, 1, 257, dtype=np.float32)
+    m = np.full_like(p, 0.5)
+    v = np.full_like(p, 0.25)
+    before = p.copy()
+    adam.adam_step(p, np.zeros_like(p), m, v, 3, lr=1e-2, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0)
+    # m/bc1 and sqrt(v/bc2) are nonzero, so the update is not zero; check the moments exactly
+    assert np.all(m == np.float32(0.9) * np.float32(0.5))
+    assert np.all(v == np.float32(0.999) * np.float32(0.25))
+    p2 = before.copy()
+    m2 = np.zeros_like(p2)
+    v2 = np.zeros_like(p2)
+    adam.adam_step(p2, np.zeros_like(p2), m2, v2, 1, lr=1e-2, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0)
+    assert np.array_equal(p2, before)
+
+
+def test_adam_oracle_within_float64_bound_over_ten_steps():
+    rng = np.random.default_rng(9)
+    p0 = (rng.standard_normal(5000) * 0.02).astype(np.float32)
+    grads = [(rng.standard_normal(5000) * 1e-3).astype(np.float32) for _ in range(10)]
+    p = p0.copy()
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for step, grad in enumerate(grads, start=1):
+        adam.adam_step(p, grad, m, v, step, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    p64, m64, v64 = adam.adam_f64_reference(p0, grads, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    # float32 rounding of p (|p| < 0.1, three rounded operations per step)
+    # bounds the drift from the exact recurrence by ~1e-8 over 10 steps; a
+    # dropped or wrong term moves p by O(lr) = 3e-4.
+    assert np.max(np.abs(p - p64)) < 1e-7
+    assert np.max(np.abs(m - m64)) < 1e-9
+
+
+def test_adam_oracle_op_order_is_observable():
+    """A transposed operand order changes float32 bits, so the golden match
+    above really pins the order: (c2*g)*g differs from c2*(g*g) here."""
+    g = np.float32(1.1920929e-07) * np.arange(1, 2000, dtype=np.float32) + np.float32(0.3)
+    c2 = np.float32(1 - 0.999)
+    assert np.any((c2 * g) * g != c2 * (g * g))
+
+
+def test_bf16_rne_matches_torch():
+    rng = np.random.default_rng(1)
+    values = np.concatenate([
+        rng.standard_normal(100000).astype(np.float32) * np.float32(3.0),
+        (np.arange(0, 65536, dtype=np.uint32) << 16 | 0x8000).view(np.float32),   # exact ties
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, -3.4e38, 1e-40, -1e-44], dtype=np.float32),
+    ])
+    finite = np.isfinite(values)
+    ours = lowp.f32_to_bf16(values)
+    ref = torch.from_numpy(values.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours[finite], ref[finite])
+
+
+def test_bf16_roundtrip_all_patterns():
+    bits = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    values = lowp.bf16_to_f32(bits)
+    back = lowp.f32_to_bf16(values)
+    keep = ~np.isnan(values)
+    assert np.array_equal(back[keep], bits[keep])
+    assert np.all(np.isnan(lowp.bf16_to_f32(back[~keep])))
+
+
+def _exact_bf16(value: float) -> int:
+    """Nearest bfloat16 by exact rational comparison (ties to even)."""
+    target = Fraction(value)
+    best = None
+    sign = 0x8000 if value < 0 else 0
+    magnitude = abs(target)
+    lo_bits = int(np.array([abs(value)], dtype=np.float32).view(np.uint32)[0]) >> 16
+    candidates = [c for c in range(max(0, lo_bits - 2), min(0x7F80, lo_bits + 3))]
+    for bits in candidates:
+        candidate = Fraction(float(lowp.bf16_to_f32(np.array([bits], dtype=np.uint16))[0]))
+        distance = abs(candidate - magnitude)
+        key = (distance, bits % 2)
+        if best is None or key < best[0]:
+            best = (key, bits)
+    return sign | best[1]
+
+
+def test_f64_to_bf16_single_rounding_exact():
+    rng = np.random.default_rng(3)
+    values = rng.standard_normal(3000) * np.exp(rng.uniform(-60, 60, 3000))
+    # ties at float64 precision: midpoints of neighbouring bf16 values
+    bits = np.arange(0x3F00, 0x3F40, dtype=np.uint16)
+    lo = lowp.bf16_to_f32(bits).astype(np.float64)
+    hi = lowp.bf16_to_f32(bits + 1).astype(np.float64)
+    ties = (lo + hi) / 2
+    values = np.concatenate([values, ties, -ties])
+    ours = lowp.f64_to_bf16(values)
+    for value, got in zip(values, ours):
+        assert got == _exact_bf16(float(value)), value
+
+
+def test_f64_to_bf16_differs_from_double_rounding():
+    """Values where f64->f32->bf16 double rounding is wrong (pins the single rounding)."""
+    one = 1.0
+    ulp_bf16 = 2.0 ** -7
+    value = one + ulp_bf16 / 2 + 2.0 ** -40   # just above a tie; f32 rounding lands on the tie
+    assert float(np.float32(value)) == one + ulp_bf16 / 2
+    bits = lowp.f64_to_bf16(np.array([value]))[0]
+    assert lowp.bf16_to_f32(np.array([bits], dtype=np.uint16))[0] == np.float32(one + ulp_bf16)
+
+
+def test_clip_oracle_matches_reference_golden(golden_dir):
+    data = np.load(golden_dir / "clip.npz")
+    records = json.loads((golden_dir / "golden.json").read_text())["clip"]
+    for record in records:
+        if record["count"] == 0:
+            continue
+        key = record["key"]
+        grads = [data[f"{key}_in{i}"] for i in range(record["count"])]
+        norm, clipped = clip.clip_grad_norm(grads, record["max_norm"], record["norm_type"])
+        assert (math.isnan(norm) and math.isnan(record["norm"])) or norm == record["norm"], key
+        for index, out in enumerate(clipped):
+            assert _same(out, data[f"{key}_out{index}"]), (key, index)
+
+
+def test_clip_oracle_l2_norm_against_fsum():
+    rng = np.random.default_rng(4)
+    grads = [rng.standard_normal(n).astype(np.float32) for n in (1, 17, 1000, 4096)]
+    exact = math.sqrt(math.fsum(float(x) ** 2 for g in grads for x in g.astype(np.float64)))
+    assert abs(clip.total_norm(grads, 2.0) - exact) <= 1e-13 * exact
+    assert clip.total_norm(grads, float("inf")) == max(float(np.max(np.abs(g))) for g in grads)
+    one = math.fsum(abs(float(x)) for g in grads for x in g)
+    assert abs(clip.total_norm(grads, 1.0) - one) <= 1e-12 * one
+
+
+def test_clip_oracle_special_cases():
+    zeros = [np.zeros(5, dtype=np.float32)]
+    assert clip.total_norm(zeros) == 0.0
+    assert clip.total_norm([np.array([1.0, np.inf], dtype=np.float32)]) == math.inf
+    assert math.isnan(clip.total_norm([np.array([np.inf, np.nan], dtype=np.float32)]))
+    grads = [np.array([0.1, -0.2], dtype=np.float32)]
+    norm, out = clip.clip_grad_norm(grads, 10.0)
+    assert _same(out[0], grads[0])
+
+
+def test_scaler_oracle_matches_reference_golden(golden_dir):
+    golden = json.loads((golden_dir / "golden.json").read_text())["scaler"]
+    arrays = np.load(golden_dir / "scaler.npz")
+    for dtype in ("float32", "float16"):
+        name = f"scaler_{dtype}"
+        record = golden[name]
+        sc = scaler.Scaler(65536.0, growth_interval=3)
+        p = arrays[f"{name}_p0"].copy()
+        m = np.zeros_like(p)
+        v = np.zeros_like(p)
+        step = 0
+        for k, scaled in enumerate(arrays[f"{name}_grads"]):
+            assert sc.scale == (65536.0 if k == 0 else record["scale"][k - 1])
+            g = scaler.unscale(scaled, sc.scale)
+            finite = scaler.finite([g])
+            assert finite == record["finite"][k]
+            if finite:
+                norm, (g,) = clip.clip_grad_norm([g], 1.0)
+                assert norm == record["norm"][k]
+                step += 1
+                adam.adam_step(p, g, m, v, step, lr=1e-3, betas=(0.9, 0.999), eps=record["eps"], weight_decay=0.1)
+            sc.update(not finite)
+            assert sc.scale == record["scale"][k]
+        assert step == record["step"]
+        assert _same(p, arrays[f"{name}_p"]) and _same(m, arrays[f"{name}_m"]) and _same(v, arrays[f"{name}_v"])
+
+
+def test_scaler_oracle_sequence_closed_form(golden_dir):
+    record = json.loads((golden_dir / "golden.json").read_text())["scaler"]["scale_sequence"]
+    sc = scaler.Scaler(record["init"], record["growth"], record["backoff"], record["interval"])
+    expected, s, tracker = [], record["init"], 0
+    for overflow in record["pattern"]:
+        sc.update(overflow)
+        if overflow:
+            s, tracker = max(s * record["backoff"], float(np.finfo(np.float32).tiny)), 0
+        else:
+            tracker += 1
+            if tracker == record["interval"]:
+                s, tracker = min(s * record["growth"], float(np.finfo(np.float32).max)), 0
+        expected.append(float(np.float32(s)))
+        assert sc.scale == expected[-1]
+    assert expected == record["scale"]
+
+
+def test_unscale_oracle_exactness():
+    rng = np.random.default_rng(8)
+    g = (rng.standard_normal(10000) * 60).astype(np.float16)
+    assert np.array_equal(scaler.unscale(g, 65536.0), (g.astype(np.float32) * np.float32(2.0 ** -16)).astype(np.float16))
+    odd = 3000.0
+    q = scaler.unscale(g.astype(np.float32), odd)
+    exact = np.array([float(np.float32(float(x) / odd)) for x in g.astype(np.float32)], dtype=np.float32)
+    assert np.array_equal(q, exact)
