@@ -62,37 +62,52 @@ __device__ __forceinline__ void adamw_elem64(double &p, double g, double &m, dou
 }
 
 // ---- per-tensor kernel: the reference kernel's ABI ------------------------------
-// 8 elements per thread per iteration with 128-bit accesses when all four
-// pointers are 16-byte aligned; grid-stride over the tensor.
+// One workgroup per kChunk elements; each thread handles kUnroll groups of 4
+// elements per iteration (each group contiguous across the workgroup) with
+// 128-bit global accesses when all four pointers are 16-byte aligned.
+constexpr uint64_t kChunk = 4096;
+
 __global__ __launch_bounds__(kBlock) void adamw_f32_kernel(
     float *__restrict__ param, const float *__restrict__ grad, float *__restrict__ m1,
     float *__restrict__ m2, nt_adamw_coefs c, uint64_t count, int vectorized) {
-    const uint64_t tid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-    const uint64_t nthreads = (uint64_t)gridDim.x * kBlock;
-    uint64_t scalar_from = 0;
+    const uint64_t start = (uint64_t)blockIdx.x * kChunk;
+    const uint64_t end = min(start + kChunk, count);
+    const bool update = c.update_parameter != 0;
+    uint64_t scalar_from = start;
     if (vectorized) {
-        const uint64_t nvec = count / kVec;
-        for (uint64_t v = tid; v < nvec; v += nthreads) {
-            const uint64_t i = v * kVec;
-            float p[kVec], g[kVec], a[kVec], b[kVec];
-            Vec8IO<TF32, true>::load(grad, i, g);
-            Vec8IO<TF32, true>::load(m1, i, a);
-            Vec8IO<TF32, true>::load(m2, i, b);
-            if (c.update_parameter) Vec8IO<TF32, true>::load(param, i, p);
+        const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
+        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTile) {
+            float p[kUnroll][kVec], g[kUnroll][kVec], a[kUnroll][kVec], b[kUnroll][kVec];
 #pragma unroll
-            for (int k = 0; k < kVec; ++k) adamw_elem<RoundF32>(p[k], g[k], a[k], b[k], c);
-            Vec8IO<TF32, true>::store(m1, i, a);
-            Vec8IO<TF32, true>::store(m2, i, b);
-            if (c.update_parameter) Vec8IO<TF32, true>::store(param, i, p);
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                if (i < vend) {
+                    Vec4IO<TF32, true>::load(grad, i, g[u]);
+                    Vec4IO<TF32, true>::load(m1, i, a[u]);
+                    Vec4IO<TF32, true>::load(m2, i, b[u]);
+                    if (update) Vec4IO<TF32, true>::load(param, i, p[u]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                if (i < vend) {
+#pragma unroll
+                    for (int k = 0; k < kVec; ++k) adamw_elem<RoundF32>(p[u][k], g[u][k], a[u][k], b[u][k], c);
+                    Vec4IO<TF32, true>::store(m1, i, a[u]);
+                    Vec4IO<TF32, true>::store(m2, i, b[u]);
+                    if (update) Vec4IO<TF32, true>::store(param, i, p[u]);
+                }
+            }
         }
-        scalar_from = nvec * kVec;
+        scalar_from = vend;
     }
-    for (uint64_t i = scalar_from + tid; i < count; i += nthreads) {
-        float p = c.update_parameter ? param[i] : 0.0f, a = m1[i], b = m2[i];
+    for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock) {
+        float p = update ? param[i] : 0.0f, a = m1[i], b = m2[i];
         adamw_elem<RoundF32>(p, grad[i], a, b, c);
         m1[i] = a;
         m2[i] = b;
-        if (c.update_parameter) param[i] = p;
+        if (update) param[i] = p;
     }
 }
 
@@ -155,30 +170,34 @@ __global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__res
 
     uint64_t scalar_from = start;
     if (d.flags & kAligned16) {
-        const uint64_t vend = start + ((end - start) / kVec) * kVec;
-        for (uint64_t i = start + (uint64_t)threadIdx.x * kVec; i < vend; i += (uint64_t)kBlock * kVec) {
-            float p[kVec], g[kVec], a[kVec], b[kVec];
-            Vec8IO<G, true>::load(gp, i, g);
-            Vec8IO<S, true>::load(ap, i, a);
-            Vec8IO<S, true>::load(bp, i, b);
-            if (read_param) Vec8IO<P, true>::load(pp, i, p);
+        const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
+        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTile) {
+            float p[kUnroll][kVec], g[kUnroll][kVec], a[kUnroll][kVec], b[kUnroll][kVec];
 #pragma unroll
-            for (int k = 0; k < kVec; ++k) {
-                float gk = clip_one<G>(unscale_one<G>(g[k], xf), xf);
-                adamw_elem<R>(p[k], gk, a[k], b[k], c);
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                if (i < vend) {
+                    Vec4IO<G, true>::load(gp, i, g[u]);
+                    Vec4IO<S, true>::load(ap, i, a[u]);
+                    Vec4IO<S, true>::load(bp, i, b[u]);
+                    if (read_param) Vec4IO<P, true>::load(pp, i, p[u]);
+                }
             }
-            if constexpr (S::code != NT_F32) {
 #pragma unroll
-                for (int k = 0; k < kVec; ++k) { a[k] = S::round_f32(a[k]); b[k] = S::round_f32(b[k]); }
-            }
-            Vec8IO<S, true>::store(ap, i, a);
-            Vec8IO<S, true>::store(bp, i, b);
-            if (update) {
-                Vec8IO<P, true>::store(pp, i, p);
-                if constexpr (HAS_COPY) {
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                if (i < vend) {
 #pragma unroll
-                    for (int k = 0; k < kVec; ++k) p[k] = C::round_f32(p[k]);
-                    Vec8IO<C, true>::store(cp, i, p);
+                    for (int k = 0; k < kVec; ++k) {
+                        const float gk = clip_one<G>(unscale_one<G>(g[u][k], xf), xf);
+                        adamw_elem<R>(p[u][k], gk, a[u][k], b[u][k], c);
+                    }
+                    Vec4IO<S, true>::store(ap, i, a[u]);    // rounds to S (bf16 moments)
+                    Vec4IO<S, true>::store(bp, i, b[u]);
+                    if (update) {
+                        Vec4IO<P, true>::store(pp, i, p[u]);
+                        if constexpr (HAS_COPY) Vec4IO<C, true>::store(cp, i, p[u]);   // RNE model copy
+                    }
                 }
             }
         }
@@ -279,10 +298,8 @@ int32_t nt_adamw_f32(float *parameter, const float *gradient, float *exp_avg, fl
                      correction1, correction2, maximize ? 1 : 0, update_parameter ? 1 : 0, 0, 0};
     const int vectorized = ((((uintptr_t)parameter | (uintptr_t)gradient | (uintptr_t)exp_avg |
                                (uintptr_t)exp_avg_sq) & 15u) == 0) ? 1 : 0;
-    // Enough workgroups to fill 256 CUs several times over, capped by the work.
-    const uint64_t per_block = (uint64_t)kBlock * kVec;
-    uint64_t blocks = (count + per_block - 1) / per_block;
-    if (blocks > 8192) blocks = 8192;
+    const uint64_t blocks = (count + kChunk - 1) / kChunk;
+    if (blocks > 0x7fffffffull) return fail(NT_ERR_VALUE, "nt_adamw_f32: tensor too large");
     adamw_f32_kernel<<<dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream>>>(
         parameter, gradient, exp_avg, exp_avg_sq, c, count, vectorized);
     NT_LAUNCH_CHECK("adamw_f32_kernel launch");

@@ -101,12 +101,22 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
         const auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
         uint64_t scalar_from = start;
         if (d.flags & kAligned16) {
-            const uint64_t vend = start + ((end - start) / kVec) * kVec;
-            for (uint64_t i = start + (uint64_t)threadIdx.x * kVec; i < vend; i += (uint64_t)kBlock * kVec) {
-                float g[kVec];
-                Vec8IO<G, false>::load(gp, i, g);
+            const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
+            for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTile) {
+                float g[kUnroll][kVec];
 #pragma unroll
-                for (int k = 0; k < kVec; ++k) acc.add(unscale_one<G>(g[k], xf));
+                for (int u = 0; u < kUnroll; ++u) {
+                    const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                    if (i < vend) Vec4IO<G, false>::load(gp, i, g[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < kUnroll; ++u) {
+                    const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                    if (i < vend) {
+#pragma unroll
+                        for (int k = 0; k < kVec; ++k) acc.add(unscale_one<G>(g[u][k], xf));
+                    }
+                }
             }
             scalar_from = vend;
         }
@@ -286,13 +296,23 @@ __global__ __launch_bounds__(kBlock) void grad_apply_kernel(const DevTensor *__r
     auto *gp = reinterpret_cast<typename G::raw *>(d.grad);
     uint64_t scalar_from = start;
     if (d.flags & kAligned16) {
-        const uint64_t vend = start + ((end - start) / kVec) * kVec;
-        for (uint64_t i = start + (uint64_t)threadIdx.x * kVec; i < vend; i += (uint64_t)kBlock * kVec) {
-            float g[kVec];
-            Vec8IO<G, true>::load(gp, i, g);
+        const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
+        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTile) {
+            float g[kUnroll][kVec];
 #pragma unroll
-            for (int k = 0; k < kVec; ++k) g[k] = clip_one<G>(unscale_one<G>(g[k], xf), xf);
-            Vec8IO<G, true>::store(gp, i, g);
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                if (i < vend) Vec4IO<G, true>::load(gp, i, g[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                if (i < vend) {
+#pragma unroll
+                    for (int k = 0; k < kVec; ++k) g[u][k] = clip_one<G>(unscale_one<G>(g[u][k], xf), xf);
+                    Vec4IO<G, true>::store(gp, i, g[u]);
+                }
+            }
         }
         scalar_from = vend;
     }

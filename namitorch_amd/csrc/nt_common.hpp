@@ -14,7 +14,9 @@
 namespace nt {
 
 constexpr int kBlock = 256;        // threads per workgroup (4 wave64s)
-constexpr int kVec = 8;            // elements per thread per iteration
+constexpr int kVec = 4;            // elements per vector access
+constexpr int kUnroll = 2;         // independent vector groups per thread per iteration
+constexpr int kTile = kBlock * kVec * kUnroll;   // elements per workgroup iteration
 
 // ---- bit casts ---------------------------------------------------------------
 __device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
@@ -85,64 +87,59 @@ struct TBF16 {
     __device__ static raw from_f64(double x) { return f32_to_bf16(f64_to_f32_odd(x)); }
 };
 
-// ---- 8-element vector I/O ------------------------------------------------------
-// Loads/stores of 8 consecutive elements at a 8-element-aligned index: two
-// dwordx4 for fp32, one dwordx4 for 16-bit types.  Streams touched once per
-// step use nontemporal accesses so they do not evict each other from L2/MALL.
-template <bool NT, class V>
-__device__ __forceinline__ V ld(const V *p) {
-    if constexpr (NT) return __builtin_nontemporal_load(p);
-    else return *p;
-}
-template <bool NT, class V>
-__device__ __forceinline__ void st(V *p, V v) {
-    if constexpr (NT) __builtin_nontemporal_store(v, p);
-    else *p = v;
-}
-
+// ---- 4-element vector I/O ------------------------------------------------------
+// Loads/stores of 4 consecutive elements at a 4-element-aligned index: one
+// dwordx4 for fp32, one dwordx2 for 16-bit types.  A wave's instruction
+// covers 64 consecutive groups, i.e. whole cache lines.  Pointers are cast
+// to the global address space (global_load/global_store instead of flat),
+// and streams touched once per step use nontemporal accesses.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) f32x4 gf32x4;
+typedef __attribute__((address_space(1))) u32x2 gu32x2;
 
-template <class T, bool NT> struct Vec8IO;
+template <bool NT, class V, class G>
+__device__ __forceinline__ V gload(const void *p) {
+    const G *q = (const G *)(p);
+    if constexpr (NT) return __builtin_nontemporal_load(q);
+    else return *q;
+}
+template <bool NT, class V, class G>
+__device__ __forceinline__ void gstore(void *p, V v) {
+    G *q = (G *)(p);
+    if constexpr (NT) __builtin_nontemporal_store(v, q);
+    else *q = v;
+}
 
-template <bool NT> struct Vec8IO<TF32, NT> {
-    __device__ static void load(const float *base, uint64_t i, float (&out)[kVec]) {
-        const f32x4 *p = reinterpret_cast<const f32x4 *>(base + i);
-        f32x4 a = ld<NT>(p), b = ld<NT>(p + 1);
+template <class T, bool NT> struct Vec4IO;
+
+template <bool NT> struct Vec4IO<TF32, NT> {
+    __device__ static void load(const float *base, uint64_t i, float (&out)[4]) {
+        f32x4 a = gload<NT, f32x4, gf32x4>(base + i);
         out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
     }
-    __device__ static void store(float *base, uint64_t i, const float (&in)[kVec]) {
-        f32x4 *p = reinterpret_cast<f32x4 *>(base + i);
-        f32x4 a = {in[0], in[1], in[2], in[3]};
-        f32x4 b = {in[4], in[5], in[6], in[7]};
-        st<NT>(p, a);
-        st<NT>(p + 1, b);
+    __device__ static void store(float *base, uint64_t i, const float (&in)[4]) {
+        gstore<NT, f32x4, gf32x4>(base + i, f32x4{in[0], in[1], in[2], in[3]});
     }
 };
 
-template <class T, bool NT> struct Vec8IO16 {
-    __device__ static void load(const uint16_t *base, uint64_t i, float (&out)[kVec]) {
-        u32x4 w = ld<NT>(reinterpret_cast<const u32x4 *>(base + i));
-        uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            out[2 * k] = T::to_f32((uint16_t)(ws[k] & 0xffffu));
-            out[2 * k + 1] = T::to_f32((uint16_t)(ws[k] >> 16));
-        }
+template <class T, bool NT> struct Vec4IO16 {
+    __device__ static void load(const uint16_t *base, uint64_t i, float (&out)[4]) {
+        u32x2 w = gload<NT, u32x2, gu32x2>(base + i);
+        out[0] = T::to_f32((uint16_t)(w.x & 0xffffu));
+        out[1] = T::to_f32((uint16_t)(w.x >> 16));
+        out[2] = T::to_f32((uint16_t)(w.y & 0xffffu));
+        out[3] = T::to_f32((uint16_t)(w.y >> 16));
     }
-    // `in` must already hold values exactly representable in T.
-    __device__ static void store(uint16_t *base, uint64_t i, const float (&in)[kVec]) {
-        uint32_t ws[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            ws[k] = (uint32_t)T::from_f32(in[2 * k]) | ((uint32_t)T::from_f32(in[2 * k + 1]) << 16);
-        u32x4 w = {ws[0], ws[1], ws[2], ws[3]};
-        st<NT>(reinterpret_cast<u32x4 *>(base + i), w);
+    // Rounds each float to T (values already representable store exactly).
+    __device__ static void store(uint16_t *base, uint64_t i, const float (&in)[4]) {
+        u32x2 w = {(uint32_t)T::from_f32(in[0]) | ((uint32_t)T::from_f32(in[1]) << 16),
+                   (uint32_t)T::from_f32(in[2]) | ((uint32_t)T::from_f32(in[3]) << 16)};
+        gstore<NT, u32x2, gu32x2>(base + i, w);
     }
 };
-template <bool NT> struct Vec8IO<TF16, NT> : Vec8IO16<TF16, NT> {};
-template <bool NT> struct Vec8IO<TBF16, NT> : Vec8IO16<TBF16, NT> {};
+template <bool NT> struct Vec4IO<TF16, NT> : Vec4IO16<TF16, NT> {};
+template <bool NT> struct Vec4IO<TBF16, NT> : Vec4IO16<TBF16, NT> {};
 
 // Scalar element access for tails and unaligned tensors.
 template <class T>

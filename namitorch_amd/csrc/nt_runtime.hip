@@ -148,8 +148,8 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     if (!valid_dtype(layout->param_dtype, true) || !valid_dtype(layout->grad_dtype, false) ||
         !valid_dtype(layout->state_dtype, true) || !valid_dtype(layout->copy_dtype, true))
         return fail(NT_ERR_TYPE, "plan layout names an unsupported dtype code");
-    if (chunk == 0) chunk = 16384;
-    const int64_t quantum = (int64_t)kBlock * kVec;
+    if (chunk == 0) chunk = 4096;
+    const int64_t quantum = (int64_t)kTile;
     if (chunk < quantum || chunk % quantum != 0 || chunk > (int64_t)1 << 30)
         return fail(NT_ERR_VALUE, "plan chunk must be a positive multiple of 2048 elements, at most 2**30");
 
@@ -204,7 +204,7 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     plan->chunk = chunk;
     plan->ntasks = (int64_t)tasks.size();
     plan->max_slot = max_slot;
-    int64_t grid = plan->ntasks < 2048 ? plan->ntasks : 2048;
+    int64_t grid = plan->ntasks < 4096 ? plan->ntasks : 4096;
     plan->prepass_grid = (int32_t)(grid > 0 ? grid : 1);
 
     auto cleanup = [&](int32_t rc) {

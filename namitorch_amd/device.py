@@ -10,7 +10,7 @@ from numbers import Integral
 
 
 class Device:
-    __slots__ = ("type", "index")
+    __slots__ = ("type", "index", "_hash")
 
     def __init__(self, value="cpu", index=None):
         if isinstance(value, Device):
@@ -40,15 +40,16 @@ class Device:
             raise TypeError("Device expects a device string or another Device.")
         object.__setattr__(self, "type", kind)
         object.__setattr__(self, "index", ordinal)
+        object.__setattr__(self, "_hash", hash((kind, ordinal)))
 
     def __setattr__(self, name, value):
         raise AttributeError("Device is immutable.")
 
     def __eq__(self, other):
-        return isinstance(other, Device) and self.type == other.type and self.index == other.index
+        return self is other or (isinstance(other, Device) and self.type == other.type and self.index == other.index)
 
     def __hash__(self):
-        return hash((self.type, self.index))
+        return self._hash
 
     def __str__(self):
         return self.type if self.index is None else f"{self.type}:{self.index}"

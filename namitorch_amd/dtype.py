@@ -36,6 +36,10 @@ class DType(Enum):
     uint8 = "uint8"
     bool = "bool"
 
+    # Members are singletons compared by identity: hash them by identity too
+    # (C-level), since dtypes key dictionaries in the per-tensor step loop.
+    __hash__ = object.__hash__
+
     @classmethod
     def _missing_(cls, value: object) -> "DType":
         raise UnsupportedDTypeError(value)
@@ -67,11 +71,11 @@ class DType(Enum):
     @property
     def code(self) -> int:
         """C-ABI storage code (NT_F32 ...); NT_DTYPE_NONE for non-floating types."""
-        return _CODES.get(self, _native.NT_DTYPE_NONE)
+        return self._code
 
     @property
     def is_floating_point(self) -> bool:
-        return self in (DType.float16, DType.float32, DType.float64, DType.bfloat16)
+        return self._floating
 
     @property
     def is_integer(self) -> bool:
@@ -106,6 +110,11 @@ _TORCH = {
 }
 _FROM_TORCH = {value: key for key, value in _TORCH.items()}
 _CODES = {float32: _native.NT_F32, float16: _native.NT_F16, bfloat16: _native.NT_BF16, float64: _native.NT_F64}
+for _member in DType:
+    # Plain attributes (not enum lookups) because the step loop reads them per tensor.
+    _member._code = _CODES.get(_member, _native.NT_DTYPE_NONE)
+    _member._floating = _member in _CODES
+del _member
 
 
 def normalize_dtype(value: object) -> DType:

@@ -20,6 +20,7 @@ produce a negative value.
 from __future__ import annotations
 
 import math
+import struct
 from numbers import Real
 
 import numpy as np
@@ -54,19 +55,31 @@ def _bool_option(options: dict, name: str) -> bool:
     return options[name]
 
 
+_PACK = {DType.float32: struct.Struct("<f"), DType.float16: struct.Struct("<e")}
+_FINFO_MAX = {dtype: dtype.finfo_max for dtype in (DType.float16, DType.float32, DType.float64, DType.bfloat16)}
+
+
 def _round_scalar(dtype: DType, value: float, name: str = "coefficient") -> float:
-    """Round a host float to `dtype` once (RNE), as ``dtype.type(value)``."""
-    if not math.isfinite(value) or abs(value) > dtype.finfo_max:
+    """Round a host float to `dtype` once (RNE), as ``dtype.type(value)``.
+
+    float32/float16 use the C conversion of ``struct`` packing, the same
+    single IEEE rounding NumPy's scalar constructors perform.
+    """
+    if not math.isfinite(value) or abs(value) > _FINFO_MAX[dtype]:
         raise ValueError(f"Optimizer {name} must be representable in {dtype.name}.")
-    if dtype is DType.float64:
+    packer = _PACK.get(dtype)
+    if packer is not None:
+        try:
+            result = packer.unpack(packer.pack(value))[0]
+        except OverflowError:
+            # |value| within finfo.max but rounding up past it: NumPy gives inf.
+            result = math.copysign(math.inf, value)
+    elif dtype is DType.float64:
         result = float(value)
-    elif dtype is DType.bfloat16:
+    else:
         from ..tensor import _bf16_bits_from_f64
         bits = int(_bf16_bits_from_f64(np.asarray([value]))[0])
         result = float(np.array([bits << 16], dtype=np.uint32).view(np.float32)[0])
-    else:
-        with np.errstate(under="ignore"):
-            result = float(dtype.numpy_dtype.type(value))
     if name == "eps" and result == 0:
         raise ValueError(f"Optimizer eps must remain positive in {dtype.name}.")
     return result
@@ -100,6 +113,34 @@ class _FirstOrderOptimizer(Optimizer):
         allowed = set(self._state_buffers) | ({"step"} if self._has_step else set())
         required = set(self._required_buffers) | ({"step"} if self._has_step else set())
         return allowed, required
+
+    def _check_state_cached(self, values: dict, parameter: Tensor) -> None:
+        """``_check_state(..., runtime=True)`` for the step loop.
+
+        Passing the check depends on which buffer objects the state holds
+        (their dtype/shape/device never change), on ``step`` being a
+        nonnegative int and on the nonnegative buffers having no negative
+        element; the last is re-checked whenever a buffer's version shows a
+        write by something other than this optimizer's kernels.
+        """
+        if not values:
+            return
+        cache = self.__dict__.setdefault("_state_checked", {})
+        seen = cache.get(id(parameter))
+        if seen is not None and seen[0] is values and len(values) == seen[1]:
+            step = values.get("step", 0)
+            unchanged = type(step) is int and step >= 0
+            if unchanged:
+                for name, buffer, nonnegative in seen[2]:
+                    if (values.get(name) is not buffer or buffer._requires_grad or not buffer._writable
+                            or (nonnegative and buffer._clean_version != buffer._version_counter.value)):
+                        unchanged = False
+                        break
+            if unchanged:
+                return
+        self._check_state(values, parameter, "parameter state", runtime=True)
+        cache[id(parameter)] = (values, len(values), tuple(
+            (name, values[name], name in self._nonnegative_buffers) for name in self._state_buffers if name in values))
 
     def _check_state(self, values: dict, parameter: Tensor, path: str, runtime: bool = False) -> None:
         if not isinstance(values, dict):
@@ -164,15 +205,20 @@ class _FirstOrderOptimizer(Optimizer):
         return copied
 
     # ---- step ----------------------------------------------------------------------------
+    def _compute_dtype(self, parameter: Tensor) -> DType:
+        """dtype the update arithmetic (and its scalars) uses: the parameter's."""
+        return parameter.dtype
+
     def _validate_entry(self, parameter: Tensor, prepared: dict, checked: set) -> None:
         key = (parameter.dtype, id(prepared))
         if key in checked:
             return
+        dtype = self._compute_dtype(parameter)
         for name, value in prepared.items():
             if type(value) is float:
-                _scalar(parameter, value, name)
+                _round_scalar(dtype, value, name)
         if self._decoupled_weight_decay:
-            _scalar(parameter, 1 - prepared["lr"] * prepared["weight_decay"], "decay factor")
+            _round_scalar(dtype, 1 - prepared["lr"] * prepared["weight_decay"], "decay factor")
         checked.add(key)
 
     def step(self, closure=None):
@@ -189,18 +235,39 @@ class _FirstOrderOptimizer(Optimizer):
         }
         checked: set = set()
         validate_update = getattr(self, "_validate_update", None)
+        states = self.state
+        state_cache = self.__dict__.setdefault("_state_checked", {})
+        items = []
         for group, parameter, gradient in entries:
-            if not parameter.dtype.is_floating_point:
+            dtype = parameter._dtype
+            if not dtype._floating:
                 raise TypeError("Optimizer updates require floating parameters.")
             if not parameter._writable:
                 raise RuntimeError("Optimizer cannot update read-only parameter storage.")
             prepared = options[id(group)]
-            self._validate_entry(parameter, prepared, checked)
-            self._check_state(self.state.get(id(parameter), {}), parameter, "parameter state", runtime=True)
+            if (dtype, id(prepared)) not in checked:
+                self._validate_entry(parameter, prepared, checked)
+            values = states.get(id(parameter))
+            if values:
+                # Inline fast path of _check_state_cached (per tensor, per step).
+                seen = state_cache.get(id(parameter))
+                unchanged = seen is not None and seen[0] is values and len(values) == seen[1]
+                if unchanged:
+                    step = values.get("step", 0)
+                    unchanged = type(step) is int and step >= 0
+                    if unchanged:
+                        for name, buffer, nonnegative in seen[2]:
+                            if (values.get(name) is not buffer or buffer._requires_grad or not buffer._writable
+                                    or (nonnegative and buffer._clean_version != buffer._version_counter.value)):
+                                unchanged = False
+                                break
+                if not unchanged:
+                    self._check_state_cached(values, parameter)
             if validate_update is not None:
                 validate_update(parameter, gradient, prepared)
+            items.append((parameter, gradient, prepared))
         with no_grad():
-            self._update_many([(parameter, gradient, options[id(group)]) for group, parameter, gradient in entries])
+            self._update_many(items)
         return loss
 
     def _update_many(self, items) -> None:

@@ -24,7 +24,7 @@ unrounded float32 values).
 
 from __future__ import annotations
 
-import ctypes
+import weakref
 
 from .. import _native
 from ..backends import get_backend
@@ -111,37 +111,59 @@ class Adam(_FirstOrderOptimizer):
     def _update_many(self, items) -> None:
         if not items:
             return
+        layouts: dict = {}
         groups: dict = {}
-        for parameter, gradient, options in items:
-            compute = self._compute_dtype(parameter)
-            if compute is bfloat16:
-                raise TypeError("bfloat16 parameters require AdamW(master_weights=True).")
-            backend = get_backend(parameter)
+        for member in items:
+            parameter, gradient = member[0], member[1]
+            key = (parameter._dtype, gradient._dtype)
+            layout = layouts.get(key)
+            if layout is None:
+                compute = self._compute_dtype(parameter)
+                if compute is bfloat16:
+                    raise TypeError("bfloat16 parameters require AdamW(master_weights=True).")
+                state_dtype = self._state_dtype(parameter, "exp_avg")
+                copy = parameter._dtype.code if self._master_weights else _native.NT_DTYPE_NONE
+                layout = layouts[key] = (compute.code, gradient._dtype.code, state_dtype.code, copy)
+            groups.setdefault((parameter._device, layout), []).append(member)
+        for (device, layout), members in groups.items():
+            backend = get_backend(device)
             if backend.adamw is None:
                 backend._unsupported("Optimizer steps")
-            state_dtype = self._state_dtype(parameter, "exp_avg")
-            copy = parameter.dtype.code if self._master_weights else _native.NT_DTYPE_NONE
-            layout = (compute.code, gradient.dtype.code, state_dtype.code, copy)
-            groups.setdefault((backend, layout), []).append((parameter, gradient, options))
-        for (backend, layout), members in groups.items():
             self._launch_group(backend, layout, members)
 
     def _launch_group(self, backend, layout, members) -> None:
         # A launch carries at most NT_MAX_SLOTS coefficient sets; split if the
         # (param group, step) combinations of this step exceed it.
+        states = self.state
+        keys = {(id(options), states[id(parameter)].get("step", 0) + 1) for parameter, _, options in members}
+        if len(keys) <= _native.NT_MAX_SLOTS:
+            self._launch_batch(backend, layout, members)
+            return
         batch: list = []
-        slot_keys: dict = {}
+        slot_keys: set = set()
         for member in members:
             parameter, _, options = member
-            state = self.state[id(parameter)]
-            key = (id(options), state.get("step", 0) + 1)
+            key = (id(options), states[id(parameter)].get("step", 0) + 1)
             if key not in slot_keys and len(slot_keys) == _native.NT_MAX_SLOTS:
                 self._launch_batch(backend, layout, batch)
-                batch, slot_keys = [], {}
-            slot_keys.setdefault(key, len(slot_keys))
+                batch, slot_keys = [], set()
+            slot_keys.add(key)
             batch.append(member)
         if batch:
             self._launch_batch(backend, layout, batch)
+
+    def _fused_decision(self, parameter: Tensor, gradient: Tensor, options: dict, first, second) -> bool:
+        """``_use_fused``, memoized on the objects it depends on."""
+        fused_option = options.get("fused")
+        cache = self.__dict__.setdefault("_fused_checked", {})
+        seen = cache.get(id(parameter))
+        if (seen is not None and seen[0] is parameter and seen[1]() is gradient and seen[2] is first
+                and seen[3] is second and seen[4] is fused_option and seen[5] == fused_kernels_enabled()):
+            return seen[6]
+        decision = self._use_fused(parameter, gradient, options)
+        cache[id(parameter)] = (parameter, weakref.ref(gradient), first, second, fused_option,
+                                fused_kernels_enabled(), decision)
+        return decision
 
     def _launch_batch(self, backend, layout, members) -> None:
         compute = {_native.NT_F32: float32, _native.NT_F16: float16, _native.NT_F64: float64}[layout[0]]
@@ -149,42 +171,55 @@ class Adam(_FirstOrderOptimizer):
         records: list = []
         rows: list = []
         bookkeeping: list = []
-        pending = [gradient._pending for _, gradient, _ in members]
-        if any(transform != pending[0] for transform in pending):
-            for _, gradient, _ in members:
-                gradient._materialize()
-            transform = None
-        else:
-            transform = pending[0]
+        transform = members[0][1]._pending
+        for _, gradient, _ in members:
+            if gradient._pending != transform:
+                for _, other, _ in members:
+                    other._materialize()
+                transform = None
+                break
+        states = self.state
+        master_mode = self._master_weights
+        fused_cache = self.__dict__.setdefault("_fused_checked", {})
+        enabled = fused_kernels_enabled()
         for parameter, gradient, options in members:
-            state = self.state[id(parameter)]
-            first, second, master = self._buffers(parameter, state)
+            state = states[id(parameter)]
+            first = state.get("exp_avg")
+            second = state.get("exp_avg_sq")
+            master = state.get("master") if master_mode else None
+            if first is None or second is None or (master_mode and master is None):
+                first, second, master = self._buffers(parameter, state)
             step = state.get("step", 0) + 1
-            fused = self._use_fused(parameter, gradient, options)
+            seen = fused_cache.get(id(parameter))
+            if (seen is not None and seen[0] is parameter and seen[1]() is gradient and seen[2] is first
+                    and seen[3] is second and seen[4] is options.get("fused") and seen[5] is enabled):
+                fused = seen[6]
+            else:
+                fused = self._fused_decision(parameter, gradient, options, first, second)
             key = (id(options), step)
             slot = slot_of.get(key)
             if slot is None:
                 slot = slot_of[key] = len(records)
                 records.append(self._coefficients(compute, options, step, fused))
-            target = master if master is not None else parameter
-            copy = parameter._ptr if master is not None else 0
-            rows.append((target._ptr, gradient._ptr, first._ptr, second._ptr, copy, parameter.size, slot))
+            if master is not None:
+                rows.append((master._ptr, gradient._ptr, first._ptr, second._ptr, parameter._ptr, parameter._numel, slot))
+            else:
+                rows.append((parameter._ptr, gradient._ptr, first._ptr, second._ptr, 0, parameter._numel, slot))
             bookkeeping.append((parameter, state, first, second, master, step, fused, options["lr"] != 0))
         slots = ((_native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs) * len(records))(*records)
         plan = backend.plan(rows, layout)
         backend.adamw_multi(plan, slots, None if transform is None else make_xform(transform))
         for parameter, state, first, second, master, step, fused, moves in bookkeeping:
-            if parameter.size or not fused:
-                first._version_counter.increment()
-                second._version_counter.increment()
-                first._clean_version = first._version
-                second._clean_version = second._version
+            if not fused or parameter._numel:
+                first._version_counter.value += 1
+                second._version_counter.value += 1
+                first._clean_version = first._version_counter.value
+                second._clean_version = second._version_counter.value
                 if moves:
-                    parameter._version_counter.increment()
+                    parameter._version_counter.value += 1
                     if master is not None:
-                        master._version_counter.increment()
+                        master._version_counter.value += 1
             state["step"] = step
-            self.state[id(parameter)] = state
 
 
 class AdamW(Adam):
@@ -234,14 +269,26 @@ class AdamW(Adam):
         return backend.adamw.supports(*arrays)
 
     def _validate_update(self, parameter, gradient, options):
-        if options["fused"] is True and not self._fused_supported(parameter, gradient):
+        if options["fused"] is True and not self._fused_decision_supported(parameter, gradient):
             raise RuntimeError("fused=True requires non-overlapping contiguous float32 CUDA parameters, gradients and states on the same device.")
+
+    def _fused_decision_supported(self, parameter: Tensor, gradient: Tensor) -> bool:
+        """``_fused_supported`` memoized on the parameter/gradient/state objects."""
+        state = self.state.get(id(parameter), {})
+        first, second = state.get("exp_avg"), state.get("exp_avg_sq")
+        cache = self.__dict__.setdefault("_support_checked", {})
+        seen = cache.get(id(parameter))
+        if seen is not None and seen[0] is parameter and seen[1]() is gradient and seen[2] is first and seen[3] is second:
+            return seen[4]
+        supported = self._fused_supported(parameter, gradient)
+        cache[id(parameter)] = (parameter, weakref.ref(gradient), first, second, supported)
+        return supported
 
     def _use_fused(self, parameter: Tensor, gradient: Tensor, options: dict) -> bool:
         fused = options["fused"]
         if fused is False or (fused is None and not fused_kernels_enabled()):
             return False
-        supported = self._fused_supported(parameter, gradient)
+        supported = self._fused_decision_supported(parameter, gradient)
         if fused is True and not supported:
             raise RuntimeError("The parameter, gradient or optimizer state does not support fused AdamW.")
         return supported

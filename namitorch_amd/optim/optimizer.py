@@ -8,6 +8,7 @@ groups, the gradient iterator and its checks (181-195), ``zero_grad``
 
 from __future__ import annotations
 
+import weakref
 from collections import defaultdict
 
 import numpy as np
@@ -155,6 +156,19 @@ class Optimizer:
     def _registered_parameters(self) -> list:
         if not self.param_groups:
             raise ValueError("Optimizer must contain at least one parameter group.")
+        # The structure check below is a pure function of which objects the
+        # groups hold; skip it when that is unchanged since the last call.
+        try:
+            fingerprint = tuple(
+                (id(group), id(group["params"]), tuple(map(id, group["params"])))
+                if type(group) is dict and type(group.get("params")) is list else None
+                for group in self.param_groups
+            )
+        except TypeError:
+            fingerprint = None
+        cached = self.__dict__.get("_registered_cache")
+        if fingerprint is not None and cached is not None and cached[0] == fingerprint:
+            return list(cached[1])
         parameters = []
         identities = set()
         for index, group in enumerate(self.param_groups):
@@ -168,6 +182,8 @@ class Optimizer:
                     raise ValueError("A Parameter object cannot belong to more than one parameter group.")
                 identities.add(id(parameter))
             parameters.extend(current)
+        if fingerprint is not None and None not in fingerprint:
+            self._registered_cache = (fingerprint, tuple(parameters))
         return parameters
 
     def add_param_group(self, param_group: dict) -> None:
@@ -191,11 +207,21 @@ class Optimizer:
 
     def _parameters_with_grad(self):
         self._registered_parameters()
+        # A (parameter, gradient) pair that passed the checks once passes them
+        # again: device, shape and dtype of a Tensor never change.  Gradients
+        # are held weakly so the cache keeps no old gradient alive.
+        checked = self.__dict__.setdefault("_checked_grads", {})
         for group in self.param_groups:
             for parameter in group["params"]:
-                if not parameter.requires_grad or parameter.grad is None:
+                if not parameter._requires_grad:
                     continue
-                gradient = parameter.grad
+                gradient = parameter._grad
+                if gradient is None:
+                    continue
+                seen = checked.get(id(parameter))
+                if seen is not None and seen[0] is parameter and seen[1]() is gradient:
+                    yield group, parameter, gradient
+                    continue
                 if not isinstance(gradient, Tensor):
                     raise TypeError("Parameter gradients must be NamiTorch Tensors.")
                 ensure_same_device(parameter, gradient)
@@ -203,6 +229,7 @@ class Optimizer:
                     raise ValueError(f"Gradient shape {gradient.shape} does not match parameter shape {parameter.shape}.")
                 if not self._gradient_dtype_ok(parameter, gradient):
                     raise TypeError(f"Gradient dtype {gradient.dtype} does not match parameter dtype {parameter.dtype}.")
+                checked[id(parameter)] = (parameter, weakref.ref(gradient))
                 yield group, parameter, gradient
 
     def zero_grad(self, set_to_none: bool = True) -> None:

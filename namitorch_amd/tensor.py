@@ -175,7 +175,7 @@ def _make_storage(data: object, dtype: DType, device: Device) -> torch.Tensor:
 class Tensor:
     __slots__ = (
         "_storage", "_dtype", "_device", "_requires_grad", "_grad", "_version_counter",
-        "_writable", "_pending", "_is_leaf", "_ptr", "_clean_version", "_finite_version", "__weakref__",
+        "_writable", "_pending", "_is_leaf", "_ptr", "_numel", "_clean_version", "_finite_version", "__weakref__",
     )
 
     def __init__(self, data: object, dtype: object = None, requires_grad: builtins.bool = False, *, device=None):
@@ -206,6 +206,7 @@ class Tensor:
         self._pending = None
         self._is_leaf = True
         self._ptr = storage.data_ptr() if storage.device.type != "cpu" else None
+        self._numel = storage.numel()
         self._clean_version = None      # version at which a state buffer was last known nonnegative
         self._finite_version = None     # version at which GradScaler last knew the gradient's finiteness
 
@@ -245,10 +246,10 @@ class Tensor:
 
     @property
     def size(self) -> int:
-        return self._storage.numel()
+        return self._numel
 
     def numel(self) -> int:
-        return self._storage.numel()
+        return self._numel
 
     @property
     def dtype(self) -> DType:
