@@ -38,7 +38,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "AdamW step params/sec + achieved HBM GB/s (% of peak), GPT-2 124M & 1.3B"
 HBM_PEAK_GBPS = 8000.0
-PROFILE_PMC = ROOT / "profiles" / "adamw_mt_f32_gpt2-124m_pmc.json"
+PROFILE_PMC = ROOT / "profiles" / "adamw_mt_f32_gpt2-124m.md"
 
 
 def log(message: str) -> None:
@@ -53,6 +53,8 @@ def parse_args():
     parser.add_argument("--configs", default="c2,c1,c3,c4,c5")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-only", action="store_true", help="only the C2 kernel loop (for profilers)")
+    parser.add_argument("--calibrate", action="store_true",
+                        help="with --kernel-only: also run 3 plain 1 GiB device copies (known bytes, for PMC scaling)")
     return parser.parse_args()
 
 
@@ -265,13 +267,15 @@ def cpu_baseline(sample_params=12_000_000, steps=4):
 
 
 def pmc_traffic():
-    if not PROFILE_PMC.exists():
-        return None
+    """HBM bytes per launch of the C2 AdamW kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE/WRITE_SIZE scaled by a 1 GiB copy), or None."""
     try:
-        data = json.loads(PROFILE_PMC.read_text())
-        return data.get("hbm_bytes_per_launch")
+        for line in PROFILE_PMC.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
     except (OSError, ValueError):
         return None
+    return None
 
 
 def main():
@@ -291,6 +295,13 @@ def main():
     c2 = bench_c2(nt, torch, args.steps, args.warmup)
     log(f"C2: {c2['ms_per_step']:.3f} ms/step, kernel {c2['kernel_ms']:.3f} ms")
     if args.kernel_only:
+        if args.calibrate:
+            source = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+            target = torch.empty_like(source)
+            for _ in range(3):
+                target.copy_(source)
+            torch.cuda.synchronize()
+            c2["calibration_copy_bytes"] = {"read": source.numel() * 4, "write": target.numel() * 4, "launches": 3}
         print(json.dumps(c2))
         return
     from namitorch_amd.param_lists import gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes
