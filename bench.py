@@ -172,57 +172,67 @@ def bench_c1(nt, torch, steps, warmup):
 
 
 # ---- C3 / C4 / C5: mixed precision through the public API -------------------------------------------
-def amp_step(nt, scaler, optimizer, params, max_norm):
-    scaler.scale(nt.Tensor._from_storage(__import__("torch").ones((), device="cuda")))
-    finite = scaler.unscale_(optimizer)
-    if finite and max_norm is not None:
-        nt.optim.clip_grad_norm_(params, max_norm)
-    scaler.step(optimizer)
-    scaler.update()
+def fresh_gradients(grads):
+    """What a new backward writing into the existing gradient buffers leaves:
+    no pending unscale/clip and a bumped version (Tensor.copy_ semantics).
+    The stored (scaled) values stay the same every step."""
+    for gradient in grads:
+        gradient._pending = None
+        gradient._version_counter.value += 1
 
 
 def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype, amp, max_norm, bytes_per_param,
-                steps, warmup):
+                steps, warmup, modes=("fused", "api")):
     from namitorch_amd.param_lists import total_params
     n = total_params(shapes)
     params = make_params(nt, torch, shapes, param_dtype)
     attach_grads(nt, torch, params, grad_dtype, scale=65536.0 if amp else 1.0)
-    optimizer = nt.optim.AdamW(decay_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8,
-                               master_weights=True, state_dtype=state_dtype)
-    scaler = nt.GradScaler(init_scale=65536.0) if amp else None
     grads = [p.grad for p in params]
-    storages = [g._storage for g in grads]
+    loss = nt.Tensor._from_storage(torch.ones((), device="cuda"))
+    result = dict(params=n, tensors=len(shapes), bytes_per_param=bytes_per_param)
+    for mode in modes:
+        optimizer = nt.optim.AdamW(decay_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8,
+                                   master_weights=True, state_dtype=state_dtype)
+        scaler = nt.GradScaler(init_scale=65536.0) if amp else None
 
-    def one_step():
-        # The pending unscale/clip of the previous step is dropped by giving
-        # the gradients fresh Tensor handles over the same storage (as a new
-        # backward would), so every step reads the same scaled values.
-        for param, storage in zip(params, storages):
-            param.grad = nt.Tensor._from_storage(storage)
-        if amp:
-            amp_step(nt, scaler, optimizer, params, max_norm)
-        else:
-            if max_norm is not None:
-                nt.optim.clip_grad_norm_(params, max_norm)
-            optimizer.step()
+        def one_step():
+            fresh_gradients(grads)
+            if mode == "fused":
+                if amp:
+                    scaler.scale(loss)
+                nt.amp.fused_step(optimizer, scaler, max_norm=max_norm)
+            elif amp:
+                scaler.scale(loss)
+                finite = scaler.unscale_(optimizer)
+                if finite and max_norm is not None:
+                    nt.optim.clip_grad_norm_(params, max_norm)
+                scaler.step(optimizer)
+                scaler.update()
+            else:
+                if max_norm is not None:
+                    nt.optim.clip_grad_norm_(params, max_norm)
+                optimizer.step()
 
-    for _ in range(warmup):
-        one_step()
-    torch.cuda.synchronize()
-    start_wall = time.perf_counter()
-    start, stop = event_pair(torch)
-    start.record()
-    for _ in range(steps):
-        one_step()
-    stop.record()
-    stop.synchronize()
-    wall_ms = (time.perf_counter() - start_wall) * 1e3 / steps
-    gpu_ms = start.elapsed_time(stop) / steps
-    result = dict(params=n, tensors=len(shapes), bytes_per_param=bytes_per_param, ms_per_step=wall_ms,
-                  params_per_s=n / (wall_ms / 1e3), GBps=bytes_per_param * n / wall_ms / 1e6,
-                  pct_hbm_peak=100 * bytes_per_param * n / wall_ms / 1e6 / HBM_PEAK_GBPS,
-                  scale=None if scaler is None else scaler.get_scale())
-    del optimizer, params, grads, storages, scaler
+        for _ in range(warmup):
+            one_step()
+        torch.cuda.synchronize()
+        start_wall = time.perf_counter()
+        for _ in range(steps):
+            one_step()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - start_wall) * 1e3 / steps
+        result[mode] = dict(ms_per_step=wall_ms, params_per_s=n / (wall_ms / 1e3),
+                            GBps=bytes_per_param * n / wall_ms / 1e6,
+                            pct_hbm_peak=100 * bytes_per_param * n / wall_ms / 1e6 / HBM_PEAK_GBPS,
+                            scale=None if scaler is None else scaler.get_scale())
+        log(f"{name} {mode}: {wall_ms:.3f} ms/step")
+        for p in params:
+            p._grad = None
+        del optimizer, scaler
+        for p, g in zip(params, grads):
+            p.grad = g
+        torch.cuda.empty_cache()
+    del params, grads
     torch.cuda.empty_cache()
     return result
 

@@ -37,6 +37,10 @@ extern "C" {
 #define NT_BF16 2
 #define NT_F64 3
 
+/* ---- nt_amp_finalize flags --------------------------------------------- */
+#define NT_FINALIZE_SCALER_UPDATE 1   /* advance scale/growth tracker (amp.py:225-233) */
+#define NT_FINALIZE_CLIP_IF_FINITE 2  /* clip only when no grad is non-finite (runner.py:249) */
+
 /* ---- multi-tensor plan limits ------------------------------------------ */
 #define NT_MAX_SLOTS 16     /* coefficient sets per nt_adamw_mt launch */
 
@@ -219,13 +223,15 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale,
  * into `ctrl` (device memory).  norm_type 2 or +inf; other norm types call
  * nt_grad_norm_pow afterwards.  With `max_norm >= 0` also computes
  * clip_coef = max_norm / (norm + 1e-6) and clip = clip_coef < 1
- * (optim/clip_grad.py:106-107).  Always sets skip = found_inf and
- * scale_used = scale.  With `scaler_update` the GradScaler state machine
- * of amp.py:225-233 then runs on the device, advancing ctrl->scale and
- * ctrl->growth_tracker.
+ * (optim/clip_grad.py:106-107); with NT_FINALIZE_CLIP_IF_FINITE the clip
+ * is also withheld when any grad is non-finite, as the reference training
+ * loop only clips after a finite unscale_ (training/runner.py:249).  Always
+ * sets skip = found_inf and scale_used = scale.  With
+ * NT_FINALIZE_SCALER_UPDATE the GradScaler state machine of amp.py:225-233
+ * then runs on the device, advancing ctrl->scale and ctrl->growth_tracker.
  */
 int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type,
-                        double max_norm, int32_t scaler_update,
+                        double max_norm, int32_t flags,
                         double growth_factor, double backoff_factor,
                         int32_t growth_interval, void *stream);
 
@@ -252,6 +258,11 @@ int32_t nt_grad_apply(nt_plan *plan, const nt_grad_xform *xform,
  * not a memset, so the call can be captured in a HIP graph). */
 int32_t nt_ctrl_reset(nt_amp_ctrl *ctrl, float scale, int32_t growth_tracker,
                       void *stream);
+
+/* Start a new iteration's block: dst takes src's scaler state (scale,
+ * growth_tracker, iterations, skipped); every per-iteration field of dst is
+ * cleared.  dst and src may not alias. */
+int32_t nt_ctrl_carry(nt_amp_ctrl *dst, const nt_amp_ctrl *src, void *stream);
 
 /* ---- small single-array kernels ---------------------------------------- */
 

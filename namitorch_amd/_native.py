@@ -26,6 +26,8 @@ NT_BF16 = 2
 NT_F64 = 3
 
 NT_MAX_SLOTS = 16
+NT_FINALIZE_SCALER_UPDATE = 1
+NT_FINALIZE_CLIP_IF_FINITE = 2
 ABI_VERSION = 1
 
 c_void_p = ctypes.c_void_p
@@ -131,6 +133,7 @@ SIGNATURES = {
     "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_void_p]),
     "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
     "nt_ctrl_reset": (c_int32, [c_void_p, c_float, c_int32, c_void_p]),
+    "nt_ctrl_carry": (c_int32, [c_void_p, c_void_p, c_void_p]),
     "nt_scale_array": (c_int32, [c_void_p, c_void_p, c_int32, c_double, c_void_p, c_uint64, c_void_p]),
     "nt_any_negative": (c_int32, [c_void_p, c_int32, c_uint64, c_void_p, c_void_p]),
 }

@@ -15,15 +15,115 @@ unscale/clip in the same kernel that reads the gradients.
 
 from __future__ import annotations
 
+import ctypes
 import math
 import operator
 from numbers import Real
 
 import numpy as np
 
+from . import _native
 from .backends import get_backend
-from .optim.clip_grad import grad_stats
+from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
 from .tensor import GradTransform
+
+
+class DeviceStep:
+    """One iteration whose unscale/finite/clip/skip/scale decisions were taken
+    on the device: its control block, an asynchronous host snapshot of that
+    block, and the host-side bookkeeping to undo if the step was skipped."""
+
+    def __init__(self, backend, block, unscale: bool, honor_skip: bool, clip_bumps: list):
+        import torch
+        self.backend = backend
+        self.block = block
+        self.unscale = unscale
+        self.honor_skip = honor_skip
+        self.records: list = []
+        self.optimizers: set = set()
+        self.clip_bumps = clip_bumps          # (gradient, version after the optimistic clip bump)
+        self.snapshot = torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, pin_memory=True)
+        self.event = torch.cuda.Event()
+        self._ctrl = None
+        self._reconciled = False
+
+    def capture(self) -> None:
+        """Queue the copy of the control block to pinned host memory."""
+        with self.backend.context():
+            self.snapshot.copy_(self.block, non_blocking=True)
+            self.event.record()
+
+    def ctrl(self) -> _native.AmpCtrl:
+        if self._ctrl is None:
+            self.event.synchronize()
+            self._ctrl = _native.AmpCtrl.from_buffer_copy(self.snapshot.numpy().tobytes())
+        return self._ctrl
+
+    def reconcile(self) -> None:
+        if self._reconciled:
+            return
+        ctrl = self.ctrl()
+        if self.honor_skip and ctrl.skip:
+            # The AdamW pass left everything untouched: undo the host bookkeeping.
+            for parameter, state, first, second, master, step, bumped, moved in self.records:
+                if state.get("step") == step:
+                    state["step"] = step - 1
+                if bumped:
+                    for buffer in (first, second):
+                        buffer._version_counter.value -= 1
+                        buffer._clean_version = buffer._version_counter.value
+                    if moved:
+                        parameter._version_counter.value -= 1
+                        if master is not None:
+                            master._version_counter.value -= 1
+        if not ctrl.clip:
+            for gradient, version in self.clip_bumps:
+                if gradient._version_counter.value == version:
+                    gradient._version_counter.value -= 1
+                    if gradient._finite_version == version:
+                        gradient._finite_version = version - 1
+        self.records.clear()
+        self._reconciled = True
+
+
+class StepResult:
+    """Outcome of ``fused_step``; reading a field waits for that step's
+    finalize kernel (not for the AdamW pass)."""
+
+    def __init__(self, device_step: DeviceStep | None = None, *, finite=None, updated=None, norm=None, scale=None):
+        self._device_step = device_step
+        self._eager = (finite, updated, norm, scale)
+
+    @property
+    def finite(self) -> bool:
+        if self._device_step is None:
+            return self._eager[0]
+        return not self._device_step.ctrl().found_inf
+
+    @property
+    def updated(self) -> bool:
+        if self._device_step is None:
+            return self._eager[1]
+        return not (self._device_step.honor_skip and self._device_step.ctrl().skip)
+
+    @property
+    def norm(self):
+        """Global grad norm (float), or None when no norm was requested."""
+        if self._device_step is None:
+            return self._eager[2]
+        return self._device_step.ctrl().norm if self._device_step.clip_requested else None
+
+    @property
+    def scale(self) -> float:
+        """Loss scale for the next iteration."""
+        if self._device_step is None:
+            return self._eager[3]
+        return float(self._device_step.ctrl().scale)
+
+    def synchronize(self) -> "StepResult":
+        if self._device_step is not None:
+            self._device_step.reconcile()
+        return self
 
 
 class GradScaler:
@@ -49,6 +149,8 @@ class GradScaler:
         self._growth_tracker = 0
         self._optimizer_states: dict = {}
         self._scale_used = False
+        self._device_blocks: dict = {}       # backend -> latest control block (scale lives there)
+        self._device_steps: list = []        # fused steps not yet reflected in the host mirror
 
     @staticmethod
     def _real(value, name):
@@ -72,7 +174,20 @@ class GradScaler:
     def is_enabled(self):
         return self._enabled
 
+    def _reconcile(self) -> None:
+        """Bring the host mirror (scale, growth tracker) up to date with the
+        device after fused steps; waits for their finalize kernels only."""
+        if not self._device_steps:
+            return
+        for device_step in self._device_steps:
+            device_step.reconcile()
+        last = self._device_steps[-1].ctrl()
+        self._scale = float(last.scale)
+        self._growth_tracker = int(last.growth_tracker)
+        self._device_steps.clear()
+
     def get_scale(self):
+        self._reconcile()
         return self._scale if self._enabled else 1.0
 
     def scale(self, loss):
@@ -84,7 +199,13 @@ class GradScaler:
             return loss
         if self._optimizer_states:
             raise RuntimeError("Call update() before scaling another loss after unscale_ or step.")
-        result = loss * self._scale
+        backend = get_backend(loss)
+        block = self._device_blocks.get(backend) if self._device_steps else None
+        if block is not None:
+            # The current scale lives on the device after a fused step.
+            result = backend.scale_tensor(loss, 1.0, ctrl=block)
+        else:
+            result = loss * self._scale
         self._scale_used = True
         return result
 
@@ -107,6 +228,7 @@ class GradScaler:
     def unscale_(self, optimizer):
         if not self._enabled:
             return True
+        self._reconcile()
         if not self._scale_used:
             raise RuntimeError("Call scale(loss) and backward before unscale_.")
         identity = id(optimizer)
@@ -165,6 +287,7 @@ class GradScaler:
     def update(self):
         if not self._enabled:
             return
+        self._reconcile()
         if not self._optimizer_states or any(state["stage"] != "stepped" for state in self._optimizer_states.values()):
             raise RuntimeError("Call step() for every unscaled optimizer before update().")
         if any(not state["finite"] for state in self._optimizer_states.values()):
@@ -178,7 +301,14 @@ class GradScaler:
         self._optimizer_states.clear()
         self._scale_used = False
 
+    def fused_step(self, optimizer, max_norm=None, norm_type=2.0) -> StepResult:
+        """``unscale_`` → ``clip_grad_norm_`` (only when finite) → ``step`` →
+        ``update`` — the reference training loop's sequence
+        (training/runner.py:248-251) — with every decision on the device."""
+        return fused_step(optimizer, self, max_norm=max_norm, norm_type=norm_type)
+
     def _ensure_idle(self):
+        self._reconcile()
         if self._optimizer_states or self._scale_used:
             raise RuntimeError("GradScaler state can be saved or loaded only between iterations, after update().")
 
@@ -205,4 +335,98 @@ class GradScaler:
         self.__dict__.update(prepared.__dict__)
 
 
-__all__ = ["GradScaler"]
+def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, norm_type=2.0) -> StepResult:
+    """One optimizer step with the reference training loop's AMP/clip
+    semantics and no host synchronization.
+
+    With an enabled ``scaler``: gradients are unscaled by the current loss
+    scale; if every unscaled gradient is finite they are clipped to
+    ``max_norm`` (when given) and the optimizer steps, otherwise the step is
+    skipped; then the scale is updated — exactly ``unscale_``,
+    ``clip_grad_norm_`` (if finite), ``step`` and ``update`` of
+    training/runner.py:248-251.  Without a scaler: clip (when ``max_norm``
+    is given) and step.  One pre-pass kernel, one single-workgroup finalize
+    and the fused AdamW pass; the host learns the outcome from an
+    asynchronous snapshot of the control block and reconciles its
+    bookkeeping (``state['step']``, version counters, the scale mirror) at
+    the next step, ``get_scale``/``state_dict`` or ``StepResult`` access.
+    ``error_if_nonfinite`` has no equivalent here (it would need the host).
+    """
+    amp = scaler is not None and scaler._enabled
+    if amp:
+        if not scaler._scale_used:
+            raise RuntimeError("Call scale(loss) and backward before unscale_.")
+        if scaler._optimizer_states:
+            raise RuntimeError("fused_step cannot follow unscale_ or step in the same iteration; call update() first.")
+    maximum = None if max_norm is None else _nonnegative(max_norm, "max_norm")
+    order = _norm_type(norm_type)
+    if order != 2.0 and not math.isinf(order):
+        raise ValueError("fused_step supports norm_type 2 and inf; use clip_grad_norm_ for other norms.")
+    pairs = GradScaler._gradients(optimizer)
+    gradients = [gradient for _, gradient in pairs]
+    if not gradients:
+        raise RuntimeError("No gradients were found for this optimizer.")
+    groups = _device_groups(gradients)
+    if len(groups) != 1:
+        return _fused_step_host(optimizer, scaler, amp, maximum, order, [p for p, _ in pairs])
+    (backend, dtype), _ = next(iter(groups.items()))
+    if backend.adamw is None:
+        backend._unsupported("Optimizer steps")
+    if amp:
+        previous = scaler._device_blocks.get(backend)
+        if previous is None or not scaler._device_steps:
+            previous = backend.new_ctrl(scaler._scale, scaler._growth_tracker)
+        block = backend.carry_ctrl(previous)
+    else:
+        block = backend.new_ctrl()
+    clip_bumps: list = []
+    device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps)
+    device_step.clip_requested = maximum is not None
+    transform = GradTransform(device=device_step)
+    for gradient in gradients:
+        gradient._ensure_inplace_allowed()
+        if gradient._pending is not None:
+            gradient._materialize()
+        gradient._pending = transform
+        if amp:
+            gradient._version_counter.value += 1          # unscale_ rewrites the gradient
+        if maximum is not None:
+            gradient._version_counter.value += 1          # clip may; undone on reconcile if not
+            clip_bumps.append((gradient, gradient._version_counter.value))
+        gradient._finite_version = gradient._version_counter.value
+    layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
+    plan = backend.plan(backend.grad_rows(gradients), layout)
+    backend.grad_prepass(plan, None, block.data_ptr(), unscale=amp)
+    flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
+    growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)
+    backend.grad_finalize(plan, block.data_ptr(), order, -1.0 if maximum is None else maximum, flags,
+                          growth, backoff, interval)
+    device_step.capture()
+    if amp:
+        scaler._reconcile()                               # earlier fused steps: their finalize already ran
+        scaler._device_blocks[backend] = block
+        scaler._device_steps.append(device_step)
+        scaler._scale_used = False
+    optimizer.step()                                      # the AdamW pass reads the control block
+    optimizer.__dict__.setdefault("_device_steps", []).append(device_step)
+    return StepResult(device_step)
+
+
+def _fused_step_host(optimizer, scaler, amp, maximum, order, parameters) -> StepResult:
+    """Several devices or gradient dtypes: the same sequence through the
+    host-synchronizing API (identical results)."""
+    norm = None
+    if amp:
+        finite = scaler.unscale_(optimizer)
+        if finite and maximum is not None:
+            norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+        updated = scaler.step(optimizer)
+        scaler.update()
+        return StepResult(finite=finite, updated=updated, norm=norm, scale=scaler.get_scale())
+    if maximum is not None:
+        norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+    optimizer.step()
+    return StepResult(finite=None if norm is None else math.isfinite(norm), updated=True, norm=norm, scale=1.0)
+
+
+__all__ = ["GradScaler", "fused_step", "StepResult"]

@@ -197,9 +197,9 @@ class HIPBackend:
                          int(unscale or scale is not None), ctrl_ptr, self.stream())
 
     def grad_finalize(self, plan: Plan, ctrl_ptr: int, norm_type: float = 2.0, max_norm: float = -1.0,
-                      scaler_update: bool = False, growth: float = 2.0, backoff: float = 0.5, interval: int = 2000) -> None:
+                      flags: int = 0, growth: float = 2.0, backoff: float = 0.5, interval: int = 2000) -> None:
         with self.context():
-            _native.call("nt_amp_finalize", plan.handle, ctrl_ptr, norm_type, max_norm, int(scaler_update),
+            _native.call("nt_amp_finalize", plan.handle, ctrl_ptr, norm_type, max_norm, int(flags),
                          growth, backoff, interval, self.stream())
 
     def grad_norm_pow(self, plan: Plan, ctrl_ptr: int, norm_type: float, max_norm: float,
@@ -222,6 +222,13 @@ class HIPBackend:
     def reset_ctrl(self, block: torch.Tensor, scale: float, growth_tracker: int = 0) -> None:
         with self.context():
             _native.call("nt_ctrl_reset", block.data_ptr(), scale, growth_tracker, self.stream())
+
+    def carry_ctrl(self, previous: torch.Tensor) -> torch.Tensor:
+        """A new control block that continues `previous`'s scaler state."""
+        block = torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, device=self.device.torch)
+        with self.context():
+            _native.call("nt_ctrl_carry", block.data_ptr(), previous.data_ptr(), self.stream())
+        return block
 
     def read_ctrl(self, block: torch.Tensor) -> _native.AmpCtrl:
         out = _native.AmpCtrl()
@@ -265,6 +272,12 @@ def make_xform(transform, ctrl_ptr: int | None = None, honor_skip: bool = False)
     xform = _native.GradXform()
     xform.scale = 1.0
     xform.clip_coef = 1.0
+    device = getattr(transform, "device", None)
+    if device is not None:
+        xform.unscale = int(device.unscale)
+        xform.honor_skip = int(device.honor_skip)
+        xform.ctrl = device.block.data_ptr()
+        return xform
     if transform is not None:
         if transform.scale is not None:
             xform.scale = transform.scale

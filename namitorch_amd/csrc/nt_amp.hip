@@ -86,62 +86,263 @@ __device__ __forceinline__ float ctrl_scale_inv(float s, int &mode, float &inv) 
     return s;
 }
 
+// ---- pre-pass ------------------------------------------------------------------
+// One workgroup per kPrepassTasks consecutive tasks.  Per element g' (the
+// unscaled grad, rounded to its dtype) it keeps
+//   * the max of |g'| as fp32 bits: integer order equals magnitude order for
+//     finite values, +inf is 0x7f800000 and any NaN is above it, so one
+//     unsigned max yields amax, "some inf" and "some NaN" together;
+//   * the fp64 sum of g'^2 over finite g'.  For fp16/bf16 grads g'*g' is exact
+//     in fp32 whenever the fp32 exponent of g' lies in [-63, 62] (at most 11
+//     significant bits squared, result normal), so only the fp64 add remains;
+//     other groups take the fp64 fma path.
+struct PAcc {
+    double sumsq = 0.0;
+    uint32_t amax_bits = 0;
+};
+
+__device__ __forceinline__ void pacc_wide(PAcc &a, float g) {
+    const uint32_t b = f32_bits(g) & 0x7fffffffu;
+    a.amax_bits = b > a.amax_bits ? b : a.amax_bits;
+    if (b < 0x7f800000u) {
+        const double d = (double)g;
+        a.sumsq = __builtin_fma(d, d, a.sumsq);
+    }
+}
+
+// fp32 exponent field of g in [64, 189] (or g == 0): g*g exact and normal in fp32.
+__device__ __forceinline__ bool square_exact(float g) {
+    const uint32_t b = f32_bits(g) & 0x7fffffffu;
+    const uint32_t e = b >> 23;
+    return b == 0u || (e - 64u) <= 125u;
+}
+
+// fp16: every finite fp16 squares exactly into a normal fp32, so the fast
+// accumulation is always exact (non-finite values only set the flags).
+// bf16 (raw mode): accumulates the squares of the stored values; exactness is
+// checked per workgroup from the min/max magnitudes afterwards.
 template <class G>
-__global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__restrict__ tensors,
-                                                         const Task *__restrict__ tasks, int64_t ntasks,
-                                                         int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
-                                                         Partial *__restrict__ partials) {
-    if (ctrl != nullptr && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale, xf.unscale, xf.inv_scale);
-    Acc acc;
-    for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
-        const Task task = tasks[t];
-        const DevTensor d = tensors[task.tensor];
+__device__ __forceinline__ void pacc_fast(PAcc &a, uint32_t &mn, const float (&g)[kPrepassUnroll][kVec]) {
+#pragma unroll
+    for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) {
+            const uint32_t b = f32_bits(g[u][k]) & 0x7fffffffu;
+            a.amax_bits = b > a.amax_bits ? b : a.amax_bits;
+            if constexpr (G::code == NT_BF16) {
+                const uint32_t z = b - 1u;                // 0 wraps to the top: ignored by min
+                mn = z < mn ? z : mn;
+            }
+            a.sumsq += (double)(g[u][k] * g[u][k]);
+        }
+}
+
+__device__ __forceinline__ void pacc_fast1(PAcc &a, uint32_t &mn, float v, bool track_min) {
+    const uint32_t b = f32_bits(v) & 0x7fffffffu;
+    a.amax_bits = b > a.amax_bits ? b : a.amax_bits;
+    if (track_min) {
+        const uint32_t z = b - 1u;
+        mn = z < mn ? z : mn;
+    }
+    a.sumsq += (double)(v * v);
+}
+
+// Workgroup-uniform max/min of two u32 values (fixed order).
+__device__ void block_minmax(uint32_t &mx, uint32_t &mn) {
+    __shared__ uint32_t s_mx[kBlock / 64], s_mn[kBlock / 64];
+    __shared__ uint32_t s_out[2];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t a = (uint32_t)__shfl_xor((int)mx, off, 64);
+        const uint32_t b = (uint32_t)__shfl_xor((int)mn, off, 64);
+        mx = a > mx ? a : mx;
+        mn = b < mn ? b : mn;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        s_mx[wave] = mx;
+        s_mn[wave] = mn;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t x = 0, y = 0xffffffffu;
+        for (int w = 0; w < kBlock / 64; ++w) {
+            x = s_mx[w] > x ? s_mx[w] : x;
+            y = s_mn[w] < y ? s_mn[w] : y;
+        }
+        s_out[0] = x;
+        s_out[1] = y;
+    }
+    __syncthreads();
+    mx = s_out[0];
+    mn = s_out[1];
+}
+
+__device__ __forceinline__ double amax_from_bits(uint32_t bits) { return (double)bits_f32(bits); }
+
+// Workgroup reduction of (sumsq, amax_bits) in a fixed order; thread 0 gets it.
+__device__ PAcc block_reduce_p(PAcc a) {
+    __shared__ double s_sum[kBlock / 64];
+    __shared__ uint32_t s_max[kBlock / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    double s = wave_sum(a.sumsq);
+    uint32_t m = a.amax_bits;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)m, off, 64);
+        m = o > m ? o : m;
+    }
+    if (lane == 0) {
+        s_sum[wave] = s;
+        s_max[wave] = m;
+    }
+    __syncthreads();
+    PAcc r;
+    if (threadIdx.x == 0) {
+        for (int w = 0; w < kBlock / 64; ++w) {
+            r.sumsq += s_sum[w];
+            r.amax_bits = s_max[w] > r.amax_bits ? s_max[w] : r.amax_bits;
+        }
+    }
+    return r;
+}
+
+// Visits the elements of this workgroup's tasks (descriptors staged in LDS):
+// vec(g) for each group of kPrepassUnroll x 4 loaded values (missing ones 0),
+// one(value) for tail/unaligned elements.
+template <class G, class Vec, class One>
+__device__ __forceinline__ void prepass_visit(const Task *s_task, const DevTensor *s_desc, int ntask, int64_t chunk,
+                                              Vec vec, One one) {
+    for (int j = 0; j < ntask; ++j) {
+        const Task task = s_task[j];
+        const DevTensor &d = s_desc[j];
         const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
         const uint64_t end = min(start + (uint64_t)chunk, d.numel);
         const auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
         uint64_t scalar_from = start;
         if (d.flags & kAligned16) {
             const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
-            for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTile) {
-                float g[kUnroll][kVec];
+            for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kPrepassTile) {
+                float g[kPrepassUnroll][kVec];
 #pragma unroll
-                for (int u = 0; u < kUnroll; ++u) {
-                    const uint64_t i = base + (uint64_t)u * kBlock * kVec;
-                    if (i < vend) Vec4IO<G, false>::load(gp, i, g[u]);
-                }
-#pragma unroll
-                for (int u = 0; u < kUnroll; ++u) {
+                for (int u = 0; u < kPrepassUnroll; ++u) {
                     const uint64_t i = base + (uint64_t)u * kBlock * kVec;
                     if (i < vend) {
+                        Vec4IO<G, true>::load(gp, i, g[u]);
+                    } else {
 #pragma unroll
-                        for (int k = 0; k < kVec; ++k) acc.add(unscale_one<G>(g[u][k], xf));
+                        for (int k = 0; k < kVec; ++k) g[u][k] = 0.0f;
                     }
                 }
+                vec(g);
             }
             scalar_from = vend;
         }
-        for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock)
-            acc.add(unscale_one<G>(load1<G>(gp, i), xf));
+        for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock) one(load1<G>(gp, i));
     }
-    Acc r = block_reduce(acc);
-    if (threadIdx.x == 0) {
-        Partial p;
-        p.sumsq = r.sumsq;
-        p.amax = r.amax;
-        p.has_nan = r.nan;
-        p.has_inf = r.inf;
-        p.pad[0] = p.pad[1] = 0;
-        partials[blockIdx.x] = p;
+}
+
+template <class G>
+__global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__restrict__ tensors,
+                                                         const Task *__restrict__ tasks, int64_t ntasks,
+                                                         int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
+                                                         Partial *__restrict__ partials) {
+    __shared__ Task s_task[kPrepassTasks];
+    __shared__ DevTensor s_desc[kPrepassTasks];
+    __shared__ int s_redo;
+    if (ctrl != nullptr && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale, xf.unscale, xf.inv_scale);
+    // Stage this workgroup's task entries and descriptors (one round trip).
+    const int64_t first = (int64_t)blockIdx.x * kPrepassTasks;
+    const int64_t left = ntasks - first;
+    const int ntask = left < (int64_t)kPrepassTasks ? (int)(left > 0 ? left : 0) : kPrepassTasks;
+    if ((int)threadIdx.x < ntask) {
+        const Task task = tasks[first + threadIdx.x];
+        s_task[threadIdx.x] = task;
+        s_desc[threadIdx.x] = tensors[task.tensor];
     }
+    __syncthreads();
+
+    PAcc acc;
+    uint32_t mn = 0xffffffffu;
+    // Raw mode (bf16): no unscale, or an exact power-of-two scale >= 1.  The
+    // squares of the stored values are summed and the sum rescaled by
+    // inv_scale^2 at the end.  That equals the sum over the unscaled values
+    // when every unscaled value stays a normal bf16 and every stored square is
+    // exact in fp32, which the workgroup checks from its magnitude range; if
+    // not, it recomputes element by element.
+    const bool raw = G::code == NT_BF16 && (xf.unscale == 0 || (xf.unscale == 2 && xf.inv_scale <= 1.0f));
+    if (raw) {
+        prepass_visit<G>(s_task, s_desc, ntask, chunk,
+                         [&](const float (&g)[kPrepassUnroll][kVec]) { pacc_fast<G>(acc, mn, g); },
+                         [&](float v) { pacc_fast1(acc, mn, v, true); });
+        uint32_t mx = acc.amax_bits;
+        block_minmax(mx, mn);
+        if (threadIdx.x == 0) {
+            // fp32 exponent field: stored square exact and normal for [64, 189];
+            // unscaled value (by 2^-k) a normal bf16 for >= k + 1.
+            const uint32_t k = xf.unscale ? 127u - ((f32_bits(xf.inv_scale) >> 23) & 0xffu) : 0u;
+            const uint32_t lo = k + 1u > 64u ? k + 1u : 64u;
+            const bool finite = mx < 0x7f800000u;
+            const bool any_nonzero = mn != 0xffffffffu;
+            const uint32_t emax = mx >> 23, emin = (mn + 1u) >> 23;
+            s_redo = finite && (emax > 189u || (any_nonzero && emin < lo)) ? 1 : 0;
+        }
+        __syncthreads();
+        const bool redo = s_redo != 0;
+        if (redo) {
+            acc = PAcc();
+            prepass_visit<G>(s_task, s_desc, ntask, chunk,
+                             [&](const float (&g)[kPrepassUnroll][kVec]) {
+#pragma unroll
+                                 for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+                                     for (int k = 0; k < kVec; ++k) pacc_wide(acc, unscale_one<G>(g[u][k], xf));
+                             },
+                             [&](float v) { pacc_wide(acc, unscale_one<G>(v, xf)); });
+        }
+        PAcc r = block_reduce_p(acc);
+        if (threadIdx.x == 0) {
+            double sumsq = r.sumsq, amax = amax_from_bits(r.amax_bits);
+            if (!redo && xf.unscale) {
+                const double inv = (double)xf.inv_scale;
+                sumsq *= inv * inv;       // exact: a power of two
+                amax *= inv;
+            }
+            partials[blockIdx.x] = Partial{sumsq, amax};
+        }
+        return;
+    }
+    // Per-element path: unscale and round each value, then accumulate.
+    prepass_visit<G>(s_task, s_desc, ntask, chunk,
+                     [&](const float (&g)[kPrepassUnroll][kVec]) {
+                         float h[kPrepassUnroll][kVec];
+#pragma unroll
+                         for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+                             for (int k = 0; k < kVec; ++k) h[u][k] = unscale_one<G>(g[u][k], xf);
+                         if constexpr (G::code == NT_F16) {
+                             pacc_fast<G>(acc, mn, h);
+                         } else {
+#pragma unroll
+                             for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+                                 for (int k = 0; k < kVec; ++k) pacc_wide(acc, h[u][k]);
+                         }
+                     },
+                     [&](float v) { pacc_wide(acc, unscale_one<G>(v, xf)); });
+    PAcc r = block_reduce_p(acc);
+    if (threadIdx.x == 0) partials[blockIdx.x] = Partial{r.sumsq, amax_from_bits(r.amax_bits)};
 }
 
 __global__ __launch_bounds__(kBlock) void prepass_f64_kernel(const DevTensor *__restrict__ tensors,
                                                              const Task *__restrict__ tasks, int64_t ntasks,
                                                              int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
                                                              Partial *__restrict__ partials) {
-    double scale = (ctrl != nullptr) ? (double)ctrl->scale : (double)xf.scale;
+    const double scale = (ctrl != nullptr) ? (double)ctrl->scale : (double)xf.scale;
     Acc acc;
-    for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
+    for (int j = 0; j < kPrepassTasks; ++j) {
+        const int64_t t = (int64_t)blockIdx.x * kPrepassTasks + j;
+        if (t >= ntasks) break;
         const Task task = tasks[t];
         const DevTensor d = tensors[task.tensor];
         const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
@@ -155,13 +356,32 @@ __global__ __launch_bounds__(kBlock) void prepass_f64_kernel(const DevTensor *__
     }
     Acc r = block_reduce(acc);
     if (threadIdx.x == 0) {
-        Partial p;
-        p.sumsq = r.sumsq;
-        p.amax = r.amax;
-        p.has_nan = r.nan;
-        p.has_inf = r.inf;
-        p.pad[0] = p.pad[1] = 0;
-        partials[blockIdx.x] = p;
+        const double amax = r.nan ? __builtin_nan("") : (r.inf ? __builtin_inf() : r.amax);
+        partials[blockIdx.x] = Partial{r.sumsq, amax};
+    }
+}
+
+// Fixed-order reduction of partials[begin, end) over one workgroup.
+__device__ Acc reduce_partials(const Partial *__restrict__ partials, int64_t begin, int64_t end) {
+    Acc acc;
+    for (int64_t i = begin + threadIdx.x; i < end; i += kBlock) {
+        const Partial p = partials[i];
+        acc.sumsq += p.sumsq;
+        if (p.amax != p.amax) acc.nan = 1;
+        else if (__builtin_isinf(p.amax)) acc.inf = 1;
+        else acc.amax = p.amax > acc.amax ? p.amax : acc.amax;
+    }
+    return block_reduce(acc);
+}
+
+__global__ __launch_bounds__(kBlock) void stage2_kernel(const Partial *__restrict__ partials, int64_t n,
+                                                        Partial *__restrict__ out) {
+    const int64_t begin = (int64_t)blockIdx.x * kStage2Span;
+    const int64_t end = min(begin + kStage2Span, n);
+    Acc r = reduce_partials(partials, begin, end);
+    if (threadIdx.x == 0) {
+        const double amax = r.nan ? __builtin_nan("") : (r.inf ? __builtin_inf() : r.amax);
+        out[blockIdx.x] = Partial{r.sumsq, amax};
     }
 }
 
@@ -184,19 +404,11 @@ __device__ __forceinline__ void scaler_update(nt_amp_ctrl *c, int found, double 
     }
 }
 
-__global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restrict__ partials, int32_t n,
+__global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restrict__ partials, int64_t n,
                                                           nt_amp_ctrl *ctrl, double norm_type, double max_norm,
-                                                          int32_t do_update, double growth, double backoff,
+                                                          int32_t flags, double growth, double backoff,
                                                           int32_t interval) {
-    Acc acc;
-    for (int32_t i = threadIdx.x; i < n; i += kBlock) {
-        const Partial p = partials[i];
-        acc.sumsq += p.sumsq;
-        acc.amax = p.amax > acc.amax ? p.amax : acc.amax;
-        acc.nan |= p.has_nan;
-        acc.inf |= p.has_inf;
-    }
-    Acc r = block_reduce(acc);
+    Acc r = reduce_partials(partials, 0, n);
     if (threadIdx.x != 0) return;
     const double nanv = __builtin_nan("");
     const double infv = __builtin_inf();
@@ -216,6 +428,7 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restr
     if (max_norm >= 0.0) {
         c.clip_coef = max_norm / (norm + 1e-6);
         c.clip = c.clip_coef < 1.0 ? 1 : 0;
+        if ((flags & NT_FINALIZE_CLIP_IF_FINITE) && c.found_inf) c.clip = 0;
     } else {
         c.clip_coef = 1.0;
         c.clip = 0;
@@ -224,7 +437,7 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restr
     c.scale_used = c.scale;
     c.iterations += 1;
     c.skipped += c.found_inf;
-    if (do_update) scaler_update(&c, c.found_inf, growth, backoff, interval);
+    if (flags & NT_FINALIZE_SCALER_UPDATE) scaler_update(&c, c.found_inf, growth, backoff, interval);
     *ctrl = c;
 }
 
@@ -343,6 +556,19 @@ __global__ __launch_bounds__(kBlock) void grad_apply_f64_kernel(const DevTensor 
     }
 }
 
+__global__ void ctrl_carry_kernel(nt_amp_ctrl *dst, const nt_amp_ctrl *src) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const nt_amp_ctrl s = *src;
+    nt_amp_ctrl c{};
+    c.scale = s.scale;
+    c.scale_used = s.scale;
+    c.growth_tracker = s.growth_tracker;
+    c.iterations = s.iterations;
+    c.skipped = s.skipped;
+    c.clip_coef = 1.0;
+    *dst = c;
+}
+
 __global__ void ctrl_reset_kernel(nt_amp_ctrl *ctrl, float scale, int32_t tracker) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     nt_amp_ctrl c{};
@@ -440,7 +666,7 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale, const nt_amp
     Xform xf = make_xform(unscale && ctrl == nullptr ? &hx : nullptr);
     if (unscale && ctrl != nullptr) xf.unscale = 1;  // scale read on the device
     hipStream_t s = (hipStream_t)stream;
-    dim3 grid((unsigned)plan->prepass_grid);
+    dim3 grid((unsigned)plan->npartials);
     if (plan->layout.grad_dtype == NT_F64) {
         prepass_f64_kernel<<<grid, dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, plan->ntasks, plan->chunk,
                                                          xf, ctrl, plan->d_partials);
@@ -451,22 +677,32 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale, const nt_amp
         if (rc != NT_OK) return rc;
     }
     NT_LAUNCH_CHECK("prepass_kernel launch");
+    if (plan->nstage2 > 0) {
+        stage2_kernel<<<dim3((unsigned)plan->nstage2), dim3(kBlock), 0, s>>>(plan->d_partials, plan->npartials,
+                                                                            plan->d_partials2);
+        NT_LAUNCH_CHECK("stage2_kernel launch");
+    }
     return NT_OK;
 }
 
-int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, double max_norm, int32_t scaler_update,
+int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, double max_norm, int32_t flags,
                         double growth_factor, double backoff_factor, int32_t growth_interval, void *stream) {
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
     if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
     if (!(norm_type > 0.0)) return fail(NT_ERR_VALUE, "norm_type must be positive or positive infinity.");
-    if (scaler_update && (growth_interval <= 0 || !(growth_factor > 1.0) || !(backoff_factor > 0.0 && backoff_factor < 1.0)))
+    if (flags & ~(NT_FINALIZE_SCALER_UPDATE | NT_FINALIZE_CLIP_IF_FINITE))
+        return fail(NT_ERR_VALUE, "nt_amp_finalize: unknown flags");
+    if ((flags & NT_FINALIZE_SCALER_UPDATE) &&
+        (growth_interval <= 0 || !(growth_factor > 1.0) || !(backoff_factor > 0.0 && backoff_factor < 1.0)))
         return fail(NT_ERR_VALUE, "invalid GradScaler growth/backoff settings");
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    const Partial *src = plan->nstage2 > 0 ? plan->d_partials2 : plan->d_partials;
+    const int64_t count = plan->nstage2 > 0 ? plan->nstage2 : plan->npartials;
     finalize_kernel<<<dim3(1), dim3(kBlock), 0, (hipStream_t)stream>>>(
-        plan->d_partials, plan->prepass_grid, ctrl, norm_type, max_norm, scaler_update, growth_factor,
+        src, count, ctrl, norm_type, max_norm, flags, growth_factor,
         backoff_factor, growth_interval);
     NT_LAUNCH_CHECK("finalize_kernel launch");
     return NT_OK;
@@ -490,13 +726,13 @@ int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, dou
     Xform xf = make_xform(unscale && !scale_from_ctrl ? &hx : nullptr);
     if (unscale && scale_from_ctrl) xf.unscale = 1;
     hipStream_t s = (hipStream_t)stream;
-    dim3 grid((unsigned)plan->prepass_grid);
+    dim3 grid((unsigned)plan->pow_grid);
     rc = grad_dispatch<NormPowL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
                                  (const Task *)plan->d_tasks, plan->ntasks, plan->chunk, xf,
                                  (const nt_amp_ctrl *)ctrl, scale_from_ctrl, norm_type, plan->d_pow_partials);
     if (rc != NT_OK) return rc;
     NT_LAUNCH_CHECK("norm_pow_kernel launch");
-    norm_pow_finalize_kernel<<<dim3(1), dim3(kBlock), 0, s>>>(plan->d_pow_partials, plan->prepass_grid, ctrl,
+    norm_pow_finalize_kernel<<<dim3(1), dim3(kBlock), 0, s>>>(plan->d_pow_partials, plan->pow_grid, ctrl,
                                                               norm_type, max_norm);
     NT_LAUNCH_CHECK("norm_pow_finalize_kernel launch");
     return NT_OK;
@@ -530,6 +766,15 @@ int32_t nt_ctrl_reset(nt_amp_ctrl *ctrl, float scale, int32_t growth_tracker, vo
     if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
     ctrl_reset_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>(ctrl, scale, growth_tracker);
     NT_LAUNCH_CHECK("ctrl_reset_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_ctrl_carry(nt_amp_ctrl *dst, const nt_amp_ctrl *src, void *stream) {
+    clear_error();
+    if (dst == nullptr || src == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
+    if (dst == src) return fail(NT_ERR_VALUE, "nt_ctrl_carry: dst and src alias");
+    ctrl_carry_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>(dst, src);
+    NT_LAUNCH_CHECK("ctrl_carry_kernel launch");
     return NT_OK;
 }
 

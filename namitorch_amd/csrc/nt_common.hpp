@@ -169,14 +169,18 @@ struct Task {
     uint32_t chunk;
 };
 
-// Per-workgroup partial of the grad pre-pass.
-struct alignas(32) Partial {
+// Per-workgroup partial of the grad pre-pass: float64 sum of squares of the
+// finite (unscaled) grads and max |g| as a double that is +inf when some
+// grad is infinite and NaN when some grad is NaN.
+struct alignas(16) Partial {
     double sumsq;
     double amax;
-    int32_t has_nan;
-    int32_t has_inf;
-    int32_t pad[2];
 };
+constexpr int kPrepassTasks = 8;        // 4096-element tasks per pre-pass workgroup
+constexpr int kPrepassUnroll = 4;       // 4-element groups in flight per lane
+constexpr int kPrepassTile = kBlock * kVec * kPrepassUnroll;
+constexpr int64_t kStage2Span = 4096;   // partials per stage-2 workgroup
+constexpr int64_t kFinalizeDirect = 4096;  // at most this many partials: no stage 2
 
 // ---- grad transform (unscale then clip), exactly as stored grads would be -------
 // g' = to_G(f32(g) / scale)           (amp.py:190-191; division or an exact

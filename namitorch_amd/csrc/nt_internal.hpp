@@ -15,12 +15,15 @@ struct nt_plan {
     uint64_t numel;
     int64_t chunk;               // elements per workgroup task
     int64_t ntasks;
-    int32_t prepass_grid;        // workgroups of the grad pre-pass (partials slots)
+    int64_t npartials;           // pre-pass workgroups = partial slots
+    int64_t nstage2;             // stage-2 workgroups (0: finalize reads the partials directly)
+    int32_t pow_grid;            // workgroups of the general p-norm pass
     uint32_t max_slot;           // largest coefficient slot any tensor selects
     nt::DevTensor *d_tensors;    // [ntensors]
     nt::Task *d_tasks;           // [ntasks]
-    nt::Partial *d_partials;     // [prepass_grid]
-    double *d_pow_partials;      // [prepass_grid] (general p-norm)
+    nt::Partial *d_partials;     // [npartials]
+    nt::Partial *d_partials2;    // [max(nstage2, 1)]
+    double *d_pow_partials;      // [pow_grid] (general p-norm)
     void *h_staging;             // pinned host copy of the tables (async upload source)
 };
 

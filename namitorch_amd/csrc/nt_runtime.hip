@@ -204,13 +204,16 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     plan->chunk = chunk;
     plan->ntasks = (int64_t)tasks.size();
     plan->max_slot = max_slot;
+    plan->npartials = plan->ntasks > 0 ? (plan->ntasks + kPrepassTasks - 1) / kPrepassTasks : 1;
+    plan->nstage2 = plan->npartials > kFinalizeDirect ? (plan->npartials + kStage2Span - 1) / kStage2Span : 0;
     int64_t grid = plan->ntasks < 4096 ? plan->ntasks : 4096;
-    plan->prepass_grid = (int32_t)(grid > 0 ? grid : 1);
+    plan->pow_grid = (int32_t)(grid > 0 ? grid : 1);
 
     auto cleanup = [&](int32_t rc) {
         if (plan->d_tensors) (void)hipFree(plan->d_tensors);
         if (plan->d_tasks) (void)hipFree(plan->d_tasks);
         if (plan->d_partials) (void)hipFree(plan->d_partials);
+        if (plan->d_partials2) (void)hipFree(plan->d_partials2);
         if (plan->d_pow_partials) (void)hipFree(plan->d_pow_partials);
         if (plan->h_staging) (void)hipHostFree(plan->h_staging);
         delete plan;
@@ -221,8 +224,9 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     int32_t rc;
     if ((rc = hip_check(hipMalloc((void **)&plan->d_tensors, tensor_bytes), "hipMalloc(plan tensors)")) != NT_OK) return cleanup(rc);
     if ((rc = hip_check(hipMalloc((void **)&plan->d_tasks, task_bytes), "hipMalloc(plan tasks)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipMalloc((void **)&plan->d_partials, (size_t)plan->prepass_grid * sizeof(Partial)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipMalloc((void **)&plan->d_pow_partials, (size_t)plan->prepass_grid * sizeof(double)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipMalloc((void **)&plan->d_partials, (size_t)plan->npartials * sizeof(Partial)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipMalloc((void **)&plan->d_partials2, (size_t)(plan->nstage2 > 0 ? plan->nstage2 : 1) * sizeof(Partial)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipMalloc((void **)&plan->d_pow_partials, (size_t)plan->pow_grid * sizeof(double)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
     if ((rc = hip_check(hipHostMalloc(&plan->h_staging, tensor_bytes + task_bytes, hipHostMallocDefault), "hipHostMalloc(plan staging)")) != NT_OK) return cleanup(rc);
     char *staging = static_cast<char *>(plan->h_staging);
     std::memcpy(staging, host.data(), tensor_bytes);
@@ -245,6 +249,7 @@ int32_t nt_plan_destroy(nt_plan *plan) {
     (void)hipFree(plan->d_tensors);
     (void)hipFree(plan->d_tasks);
     (void)hipFree(plan->d_partials);
+    (void)hipFree(plan->d_partials2);
     (void)hipFree(plan->d_pow_partials);
     (void)hipHostFree(plan->h_staging);
     delete plan;

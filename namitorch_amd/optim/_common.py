@@ -224,6 +224,7 @@ class _FirstOrderOptimizer(Optimizer):
     def step(self, closure=None):
         if closure is not None and not callable(closure):
             raise TypeError("Optimizer closure must be callable or None.")
+        self._reconcile_device_steps()
         loss = None
         if closure is not None:
             with enable_grad():

@@ -209,8 +209,10 @@ class Adam(_FirstOrderOptimizer):
         slots = ((_native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs) * len(records))(*records)
         plan = backend.plan(rows, layout)
         backend.adamw_multi(plan, slots, None if transform is None else make_xform(transform))
+        device_step = None if transform is None else transform.device
         for parameter, state, first, second, master, step, fused, moves in bookkeeping:
-            if not fused or parameter._numel:
+            bumped = not fused or parameter._numel
+            if bumped:
                 first._version_counter.value += 1
                 second._version_counter.value += 1
                 first._clean_version = first._version_counter.value
@@ -220,6 +222,12 @@ class Adam(_FirstOrderOptimizer):
                     if master is not None:
                         master._version_counter.value += 1
             state["step"] = step
+            if device_step is not None:
+                # The device decides whether this step is skipped; remember
+                # what to undo on the host if it was.
+                device_step.records.append((parameter, state, first, second, master, step, bumped, moves))
+        if device_step is not None:
+            device_step.optimizers.add(self)
 
 
 class AdamW(Adam):

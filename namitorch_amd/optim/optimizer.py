@@ -246,7 +246,17 @@ class Optimizer:
     def step(self, closure=None):
         raise RuntimeError("Optimizer subclass must implement step.")
 
+    def _reconcile_device_steps(self) -> None:
+        """Settle host state (step counts, version counters) of steps whose
+        skip decision was taken on the device (``namitorch_amd.amp.fused_step``)."""
+        pending = self.__dict__.get("_device_steps")
+        if pending:
+            for device_step in pending:
+                device_step.reconcile()
+            pending.clear()
+
     def state_dict(self) -> dict:
+        self._reconcile_device_steps()
         parameters = self._registered_parameters()
         indices = {id(parameter): index for index, parameter in enumerate(parameters)}
         state = {}

@@ -88,13 +88,17 @@ class GradTransform:
     ``scale``: divide by this fp32 loss scale and round to the grad dtype
     (``amp.py:190-191``); ``clip``: multiply by this fp64 coefficient and
     round to the grad dtype (``optim/clip_grad.py:111``).  ``None`` = absent.
+    ``device``: the scale, the clip decision and its coefficient live in the
+    control block of a device-decided step (``namitorch_amd.amp.DeviceStep``)
+    instead; compared by identity.
     """
 
     scale: float | None = None
     clip: float | None = None
+    device: object = None
 
     def then_clip(self, coefficient: float) -> "GradTransform":
-        return GradTransform(self.scale, coefficient)
+        return GradTransform(self.scale, coefficient, self.device)
 
 
 # ---- host-side conversions used when creating storage ---------------------------------

@@ -348,3 +348,104 @@ def test_clip_single_rounding_from_float64(dtype):
     expected = oclip.clip_apply(g.astype(np.float64), coefficient, dtype)
     got = param.grad.numpy()      # float16 array, or float32 values for bf16/fp32
     assert _same(got, expected)[0]
+
+
+# ---- device-decided step (fused_step) ---------------------------------------------------------
+def _run_sequence(mode, shapes, param_dtype, grad_dtype, state_dtype, amp, max_norm, inf_step, steps=6):
+    rng = _rng(71)
+    host = [(rng.standard_normal(s) * 0.05).astype(np.float32) for s in shapes]
+    params = [nt.Parameter(lowp.round_bf16(h) if param_dtype == "bfloat16" else h, dtype=param_dtype, device=DEV)
+              for h in host]
+    optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.1, master_weights=True, state_dtype=state_dtype)
+    scaler = nt.GradScaler(init_scale=65536.0, growth_interval=2) if amp else None
+    grng = _rng(72)
+    trace = []
+    for k in range(steps):
+        scale = 65536.0 if amp else 1.0
+        grads = [(grng.standard_normal(s) * 1e-3 * scale).astype(np.float32) for s in shapes]
+        if k == inf_step:
+            grads[-1].reshape(-1)[7] = np.inf
+        for p, g in zip(params, grads):
+            p.grad = nt.Tensor(g, dtype=grad_dtype, device=DEV)
+        if amp:
+            scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        if mode == "api":
+            if amp:
+                finite = scaler.unscale_(optimizer)
+                if finite and max_norm is not None:
+                    nt.optim.clip_grad_norm_(params, max_norm)
+                updated = scaler.step(optimizer)
+                scaler.update()
+            else:
+                if max_norm is not None:
+                    nt.optim.clip_grad_norm_(params, max_norm)
+                optimizer.step()
+                updated = True
+        else:
+            result = nt.amp.fused_step(optimizer, scaler, max_norm=max_norm)
+            updated = result.updated
+        trace.append((updated, scaler.get_scale() if amp else 1.0,
+                      [p.grad.numpy() for p in params], [p.grad._version for p in params]))
+    state = [optimizer.state[id(p)] for p in params]
+    final = dict(params=[p.numpy() for p in params], master=[s["master"].numpy() for s in state],
+                 m=[s["exp_avg"].numpy() for s in state], v=[s["exp_avg_sq"].numpy() for s in state],
+                 step=[s["step"] for s in state], versions=[(p._version, s["exp_avg"]._version) for p, s in zip(params, state)])
+    return trace, final
+
+
+@pytest.mark.parametrize("config", [
+    dict(param_dtype="bfloat16", grad_dtype="float16", state_dtype=None, amp=True, max_norm=None, inf_step=2),     # C3-like
+    dict(param_dtype="bfloat16", grad_dtype="bfloat16", state_dtype="bfloat16", amp=False, max_norm=0.01, inf_step=-1),  # C4-like
+    dict(param_dtype="bfloat16", grad_dtype="bfloat16", state_dtype=None, amp=True, max_norm=0.01, inf_step=3),   # C5-like
+    dict(param_dtype="float32", grad_dtype="float32", state_dtype=None, amp=True, max_norm=1e6, inf_step=1),
+])
+def test_fused_step_matches_api_sequence(config):
+    shapes = [(301, 17), (17,), (4099,)]
+    api_trace, api_final = _run_sequence("api", shapes, **config)
+    dev_trace, dev_final = _run_sequence("fused", shapes, **config)
+    for k, (a, d) in enumerate(zip(api_trace, dev_trace)):
+        assert a[0] == d[0] and a[1] == d[1], (k, a[:2], d[:2])
+        for ga, gd in zip(a[2], d[2]):
+            assert _same(ga, gd)[0], k
+        assert a[3] == d[3], (k, a[3], d[3])
+    for key in ("params", "master", "m", "v"):
+        for x, y in zip(api_final[key], dev_final[key]):
+            assert _same(x, y)[0], key
+    assert api_final["step"] == dev_final["step"]
+    assert api_final["versions"] == dev_final["versions"]
+    if config["inf_step"] >= 0:
+        assert not api_trace[config["inf_step"]][0]
+
+
+@pytest.mark.parametrize("scale", [None, 65536.0, 3.0])
+@pytest.mark.parametrize("magnitude", ["normal", "huge", "tiny", "subnormal"])
+def test_bf16_grad_norm_paths(scale, magnitude):
+    """Pre-pass exactness: the raw-square fast path, its per-workgroup range
+    check and the element-by-element fallback all give the oracle's norm and
+    found_inf on bfloat16 gradients."""
+    rng = _rng(91)
+    n = 70001
+    g32 = (rng.standard_normal(n) * 0.5).astype(np.float32)
+    if magnitude == "huge":
+        g32[::997] *= np.float32(3e25)
+    elif magnitude == "tiny":
+        g32[::991] *= np.float32(1e-25)
+    elif magnitude == "subnormal":
+        g32[5] = np.float32(1e-39)
+        g32[60000] = np.float32(-5e-40)
+    g = lowp.round_bf16(g32)
+    param = nt.Parameter(np.zeros(n, dtype=np.float32), dtype="bfloat16", device=DEV)
+    param.grad = nt.Tensor(g, dtype="bfloat16", device=DEV)
+    if scale is None:
+        norm = nt.optim.clip_grad_norm_([param], 1e30).item()
+        want = oclip.total_norm([g.astype(np.float64)])
+    else:
+        optimizer = nt.optim.AdamW([param], master_weights=True)
+        scaler = nt.GradScaler(init_scale=scale)
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        finite = scaler.unscale_(optimizer)
+        unscaled = oscaler.unscale(g, scale, "bfloat16")
+        assert finite == oscaler.finite([unscaled])
+        norm = nt.optim.clip_grad_norm_([param], 1e30).item()
+        want = oclip.total_norm([unscaled.astype(np.float64)])
+    assert abs(norm - want) <= NORM_RTOL * want, (norm, want)
