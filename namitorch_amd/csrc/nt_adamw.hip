@@ -171,12 +171,16 @@ __global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__res
     uint64_t scalar_from = start;
     if (d.flags & kAligned16) {
         const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
-        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTile) {
-            float p[kUnroll][kVec], g[kUnroll][kVec], a[kUnroll][kVec], b[kUnroll][kVec];
+        // All groups of an iteration are loaded first, then updated, then
+        // stored stream by stream (fewer read/write turnarounds per wave).
+        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kPass2Tile) {
+            float p[kPass2Unroll][kVec], g[kPass2Unroll][kVec], a[kPass2Unroll][kVec], b[kPass2Unroll][kVec];
+            bool ok[kPass2Unroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < kPass2Unroll; ++u) {
                 const uint64_t i = base + (uint64_t)u * kBlock * kVec;
-                if (i < vend) {
+                ok[u] = i < vend;
+                if (ok[u]) {
                     Vec4IO<G, true>::load(gp, i, g[u]);
                     Vec4IO<S, true>::load(ap, i, a[u]);
                     Vec4IO<S, true>::load(bp, i, b[u]);
@@ -184,20 +188,29 @@ __global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__res
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
-                if (i < vend) {
+            for (int u = 0; u < kPass2Unroll; ++u) {
+                if (ok[u]) {
 #pragma unroll
                     for (int k = 0; k < kVec; ++k) {
                         const float gk = clip_one<G>(unscale_one<G>(g[u][k], xf), xf);
                         adamw_elem<R>(p[u][k], gk, a[u][k], b[u][k], c);
                     }
-                    Vec4IO<S, true>::store(ap, i, a[u]);    // rounds to S (bf16 moments)
-                    Vec4IO<S, true>::store(bp, i, b[u]);
-                    if (update) {
-                        Vec4IO<P, true>::store(pp, i, p[u]);
-                        if constexpr (HAS_COPY) Vec4IO<C, true>::store(cp, i, p[u]);   // RNE model copy
-                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kPass2Unroll; ++u)
+                if (ok[u]) Vec4IO<S, true>::store(ap, base + (uint64_t)u * kBlock * kVec, a[u]);   // rounds to S
+#pragma unroll
+            for (int u = 0; u < kPass2Unroll; ++u)
+                if (ok[u]) Vec4IO<S, true>::store(bp, base + (uint64_t)u * kBlock * kVec, b[u]);
+            if (update) {
+#pragma unroll
+                for (int u = 0; u < kPass2Unroll; ++u)
+                    if (ok[u]) Vec4IO<P, true>::store(pp, base + (uint64_t)u * kBlock * kVec, p[u]);
+                if constexpr (HAS_COPY) {
+#pragma unroll
+                    for (int u = 0; u < kPass2Unroll; ++u)
+                        if (ok[u]) Vec4IO<C, true>::store(cp, base + (uint64_t)u * kBlock * kVec, p[u]);   // RNE copy
                 }
             }
         }

@@ -17,6 +17,8 @@ constexpr int kBlock = 256;        // threads per workgroup (4 wave64s)
 constexpr int kVec = 4;            // elements per vector access
 constexpr int kUnroll = 2;         // independent vector groups per thread per iteration
 constexpr int kTile = kBlock * kVec * kUnroll;   // elements per workgroup iteration
+constexpr int kPass2Unroll = 4;    // groups in flight per lane in the multi-tensor AdamW pass
+constexpr int kPass2Tile = kBlock * kVec * kPass2Unroll;
 
 // ---- bit casts ---------------------------------------------------------------
 __device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
