@@ -30,7 +30,6 @@ from .. import _native
 from ..device import Device
 
 PLAN_CACHE_SIZE = 16
-DEFAULT_CHUNK = 16384
 _backends_alive: "weakref.WeakSet[HIPBackend]" = weakref.WeakSet()
 _shutting_down = False
 
