@@ -147,78 +147,86 @@ __device__ __forceinline__ void pacc_fast1(PAcc &a, uint32_t &mn, float v, bool 
     a.sumsq += (double)(v * v);
 }
 
-// Workgroup-uniform max/min of two u32 values (fixed order).
-__device__ void block_minmax(uint32_t &mx, uint32_t &mn) {
-    __shared__ uint32_t s_mx[kBlock / 64], s_mn[kBlock / 64];
-    __shared__ uint32_t s_out[2];
+// Wave-uniform max/min of a u32 (every lane gets the result).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t a = (uint32_t)__shfl_xor((int)mx, off, 64);
-        const uint32_t b = (uint32_t)__shfl_xor((int)mn, off, 64);
-        mx = a > mx ? a : mx;
-        mn = b < mn ? b : mn;
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+        v = o > v ? o : v;
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
-        s_mx[wave] = mx;
-        s_mn[wave] = mn;
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+        v = o < v ? o : v;
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t x = 0, y = 0xffffffffu;
-        for (int w = 0; w < kBlock / 64; ++w) {
-            x = s_mx[w] > x ? s_mx[w] : x;
-            y = s_mn[w] < y ? s_mn[w] : y;
-        }
-        s_out[0] = x;
-        s_out[1] = y;
-    }
-    __syncthreads();
-    mx = s_out[0];
-    mn = s_out[1];
+    return v;
 }
 
 __device__ __forceinline__ double amax_from_bits(uint32_t bits) { return (double)bits_f32(bits); }
 
-// Workgroup reduction of (sumsq, amax_bits) in a fixed order; thread 0 gets it.
-__device__ PAcc block_reduce_p(PAcc a) {
-    __shared__ double s_sum[kBlock / 64];
-    __shared__ uint32_t s_max[kBlock / 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    double s = wave_sum(a.sumsq);
-    uint32_t m = a.amax_bits;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t o = (uint32_t)__shfl_xor((int)m, off, 64);
-        m = o > m ? o : m;
-    }
-    if (lane == 0) {
-        s_sum[wave] = s;
-        s_max[wave] = m;
-    }
-    __syncthreads();
-    PAcc r;
-    if (threadIdx.x == 0) {
-        for (int w = 0; w < kBlock / 64; ++w) {
-            r.sumsq += s_sum[w];
-            r.amax_bits = s_max[w] > r.amax_bits ? s_max[w] : r.amax_bits;
-        }
-    }
+// Fixed-order combination of two partials: sums add, a NaN max wins, else the
+// larger max (+inf included).
+__device__ __forceinline__ Partial merge_partial(Partial a, Partial b) {
+    Partial r;
+    r.sumsq = a.sumsq + b.sumsq;
+    r.amax = (a.amax != a.amax) ? a.amax : ((b.amax != b.amax) ? b.amax : (b.amax > a.amax ? b.amax : a.amax));
     return r;
 }
 
-// Visits the elements of this workgroup's tasks (descriptors staged in LDS):
-// vec(g) for each group of kPrepassUnroll x 4 loaded values (missing ones 0),
-// one(value) for tail/unaligned elements.
+// Per-workgroup combination of the waves' partials without a barrier: each
+// wave's lane 0 parks its partial in LDS and bumps a workgroup counter; the
+// last wave to arrive combines the slots in wave order (deterministic) and
+// writes the workgroup's partial.  Waves never wait for each other.
+struct WaveJoin {
+    Partial slot[kBlock / 64];
+    uint32_t arrived;
+};
+
+__device__ __forceinline__ void wave_join_init(WaveJoin &j) {
+    if (threadIdx.x == 0) j.arrived = 0u;
+    __syncthreads();
+}
+
+__device__ __forceinline__ void wave_join_finish(WaveJoin &j, Partial mine, Partial *out) {
+    if ((threadIdx.x & 63) != 0) return;
+    const int wave = threadIdx.x >> 6;
+    j.slot[wave] = mine;
+    const uint32_t before = __hip_atomic_fetch_add(&j.arrived, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (before != (uint32_t)(kBlock / 64 - 1)) return;
+    Partial r = j.slot[0];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; ++w) r = merge_partial(r, j.slot[w]);
+    *out = r;
+}
+
+// Visits the elements of this workgroup's tasks: vec(g) for each group of
+// kPrepassUnroll x 4 loaded values (missing ones 0), one(value) for
+// tail/unaligned elements.  Task entries and descriptors are read at
+// workgroup-uniform addresses, so they come through scalar loads with no
+// LDS staging or barrier; every wave covers its lanes' share of each task.
 template <class G, class Vec, class One>
-__device__ __forceinline__ void prepass_visit(const Task *s_task, const DevTensor *s_desc, int ntask, int64_t chunk,
-                                              Vec vec, One one) {
+__device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tensors, const Task *__restrict__ tasks,
+                                              int64_t first, int ntask, int64_t chunk, Vec vec, One one) {
     for (int j = 0; j < ntask; ++j) {
-        const Task task = s_task[j];
-        const DevTensor &d = s_desc[j];
+        const Task task = tasks[first + j];
+        const DevTensor d = tensors[task.tensor];
         const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
-        const uint64_t end = min(start + (uint64_t)chunk, d.numel);
         const auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
+        // A whole, aligned 4096-element task (all but tensor tails): straight
+        // code with the kPrepassUnroll loads issued back to back.  The branch
+        // is workgroup-uniform.
+        if (chunk == kPrepassTile && (d.flags & kAligned16) != 0u && start + (uint64_t)kPrepassTile <= d.numel) {
+            float g[kPrepassUnroll][kVec];
+#pragma unroll
+            for (int u = 0; u < kPrepassUnroll; ++u)
+                Vec4IO<G, true>::load(gp + start, (uint64_t)u * kBlock * kVec + (uint64_t)threadIdx.x * kVec, g[u]);
+            vec(g);
+            continue;
+        }
+        const uint64_t end = min(start + (uint64_t)chunk, d.numel);
         uint64_t scalar_from = start;
         if (d.flags & kAligned16) {
             const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
@@ -247,20 +255,12 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
                                                          const Task *__restrict__ tasks, int64_t ntasks,
                                                          int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
                                                          Partial *__restrict__ partials) {
-    __shared__ Task s_task[kPrepassTasks];
-    __shared__ DevTensor s_desc[kPrepassTasks];
-    __shared__ int s_redo;
+    __shared__ WaveJoin join;
+    wave_join_init(join);
     if (ctrl != nullptr && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale, xf.unscale, xf.inv_scale);
-    // Stage this workgroup's task entries and descriptors (one round trip).
     const int64_t first = (int64_t)blockIdx.x * kPrepassTasks;
     const int64_t left = ntasks - first;
     const int ntask = left < (int64_t)kPrepassTasks ? (int)(left > 0 ? left : 0) : kPrepassTasks;
-    if ((int)threadIdx.x < ntask) {
-        const Task task = tasks[first + threadIdx.x];
-        s_task[threadIdx.x] = task;
-        s_desc[threadIdx.x] = tensors[task.tensor];
-    }
-    __syncthreads();
 
     PAcc acc;
     uint32_t mn = 0xffffffffu;
@@ -268,30 +268,27 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
     // squares of the stored values are summed and the sum rescaled by
     // inv_scale^2 at the end.  That equals the sum over the unscaled values
     // when every unscaled value stays a normal bf16 and every stored square is
-    // exact in fp32, which the workgroup checks from its magnitude range; if
-    // not, it recomputes element by element.
+    // exact in fp32, which each wave checks from its own magnitude range; a
+    // wave that fails the check recomputes its elements one by one.
     const bool raw = G::code == NT_BF16 && (xf.unscale == 0 || (xf.unscale == 2 && xf.inv_scale <= 1.0f));
     if (raw) {
-        prepass_visit<G>(s_task, s_desc, ntask, chunk,
+        prepass_visit<G>(tensors, tasks, first, ntask, chunk,
                          [&](const float (&g)[kPrepassUnroll][kVec]) { pacc_fast<G>(acc, mn, g); },
                          [&](float v) { pacc_fast1(acc, mn, v, true); });
-        uint32_t mx = acc.amax_bits;
-        block_minmax(mx, mn);
-        if (threadIdx.x == 0) {
-            // fp32 exponent field: stored square exact and normal for [64, 189];
-            // unscaled value (by 2^-k) a normal bf16 for >= k + 1.
-            const uint32_t k = xf.unscale ? 127u - ((f32_bits(xf.inv_scale) >> 23) & 0xffu) : 0u;
-            const uint32_t lo = k + 1u > 64u ? k + 1u : 64u;
-            const bool finite = mx < 0x7f800000u;
-            const bool any_nonzero = mn != 0xffffffffu;
-            const uint32_t emax = mx >> 23, emin = (mn + 1u) >> 23;
-            s_redo = finite && (emax > 189u || (any_nonzero && emin < lo)) ? 1 : 0;
-        }
-        __syncthreads();
-        const bool redo = s_redo != 0;
+        const uint32_t mx = wave_max_u32(acc.amax_bits);
+        const uint32_t wmn = wave_min_u32(mn);
+        // fp32 exponent field: stored square exact and normal for [64, 189];
+        // unscaled value (by 2^-k) a normal bf16 for >= k + 1.
+        const uint32_t k = xf.unscale ? 127u - ((f32_bits(xf.inv_scale) >> 23) & 0xffu) : 0u;
+        const uint32_t lo = k + 1u > 64u ? k + 1u : 64u;
+        const bool finite = mx < 0x7f800000u;
+        const bool any_nonzero = wmn != 0xffffffffu;
+        const uint32_t emax = mx >> 23, emin = (wmn + 1u) >> 23;
+        const bool redo = finite && (emax > 189u || (any_nonzero && emin < lo));   // wave-uniform
+        Partial mine;
         if (redo) {
             acc = PAcc();
-            prepass_visit<G>(s_task, s_desc, ntask, chunk,
+            prepass_visit<G>(tensors, tasks, first, ntask, chunk,
                              [&](const float (&g)[kPrepassUnroll][kVec]) {
 #pragma unroll
                                  for (int u = 0; u < kPrepassUnroll; ++u)
@@ -299,21 +296,20 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
                                      for (int k = 0; k < kVec; ++k) pacc_wide(acc, unscale_one<G>(g[u][k], xf));
                              },
                              [&](float v) { pacc_wide(acc, unscale_one<G>(v, xf)); });
-        }
-        PAcc r = block_reduce_p(acc);
-        if (threadIdx.x == 0) {
-            double sumsq = r.sumsq, amax = amax_from_bits(r.amax_bits);
-            if (!redo && xf.unscale) {
+            mine = Partial{wave_sum(acc.sumsq), amax_from_bits(wave_max_u32(acc.amax_bits))};
+        } else {
+            mine = Partial{wave_sum(acc.sumsq), amax_from_bits(mx)};
+            if (xf.unscale) {
                 const double inv = (double)xf.inv_scale;
-                sumsq *= inv * inv;       // exact: a power of two
-                amax *= inv;
+                mine.sumsq *= inv * inv;       // exact: a power of two
+                mine.amax *= inv;
             }
-            partials[blockIdx.x] = Partial{sumsq, amax};
         }
+        wave_join_finish(join, mine, partials + blockIdx.x);
         return;
     }
     // Per-element path: unscale and round each value, then accumulate.
-    prepass_visit<G>(s_task, s_desc, ntask, chunk,
+    prepass_visit<G>(tensors, tasks, first, ntask, chunk,
                      [&](const float (&g)[kPrepassUnroll][kVec]) {
                          float h[kPrepassUnroll][kVec];
 #pragma unroll
@@ -330,14 +326,16 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
                          }
                      },
                      [&](float v) { pacc_wide(acc, unscale_one<G>(v, xf)); });
-    PAcc r = block_reduce_p(acc);
-    if (threadIdx.x == 0) partials[blockIdx.x] = Partial{r.sumsq, amax_from_bits(r.amax_bits)};
+    const Partial mine{wave_sum(acc.sumsq), amax_from_bits(wave_max_u32(acc.amax_bits))};
+    wave_join_finish(join, mine, partials + blockIdx.x);
 }
 
 __global__ __launch_bounds__(kBlock) void prepass_f64_kernel(const DevTensor *__restrict__ tensors,
                                                              const Task *__restrict__ tasks, int64_t ntasks,
                                                              int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
                                                              Partial *__restrict__ partials) {
+    __shared__ WaveJoin join;
+    wave_join_init(join);
     const double scale = (ctrl != nullptr) ? (double)ctrl->scale : (double)xf.scale;
     Acc acc;
     for (int j = 0; j < kPrepassTasks; ++j) {
@@ -354,11 +352,11 @@ __global__ __launch_bounds__(kBlock) void prepass_f64_kernel(const DevTensor *__
             acc.add64(g);
         }
     }
-    Acc r = block_reduce(acc);
-    if (threadIdx.x == 0) {
-        const double amax = r.nan ? __builtin_nan("") : (r.inf ? __builtin_inf() : r.amax);
-        partials[blockIdx.x] = Partial{r.sumsq, amax};
-    }
+    const double s = wave_sum(acc.sumsq);
+    const double m = wave_max(acc.amax);
+    const int f = wave_or(acc.nan | (acc.inf << 1));
+    const Partial mine{s, (f & 1) ? __builtin_nan("") : ((f & 2) ? __builtin_inf() : m)};
+    wave_join_finish(join, mine, partials + blockIdx.x);
 }
 
 // Fixed-order reduction of partials[begin, end) over one workgroup.
