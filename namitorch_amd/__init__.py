@@ -3,18 +3,22 @@
 AdamW.step(), GradScaler unscale_/finite check/update and clip_grad_norm_
 behind NamiTorch's Python API, computed by hand-written gfx950 HIP kernels
 (``libnamitorch_amd.so``, C ABI in ``include/namitorch_amd.h``) reached
-through ctypes.
+through ctypes.  Optimizer and scaler state read and write NamiTorch's
+``.nt`` archive and checkpoint layout (``serialization``, ``checkpoint``).
 """
 
-from . import amp, optim
+from . import amp, checkpoint, optim, serialization
 from .amp import GradScaler
+from .checkpoint import load_checkpoint, save_checkpoint
+from .serialization import SerializationError, load, save
 from .backends import enable_fused_kernels, fused_kernels_enabled, get_backend
 from .device import Device, device
 from .dtype import DType, bfloat16, float16, float32, float64
 from .tensor import Parameter, Tensor, enable_grad, is_grad_enabled, no_grad, tensor
 
 __all__ = [
-    "amp", "optim", "GradScaler", "enable_fused_kernels", "fused_kernels_enabled", "get_backend",
+    "amp", "checkpoint", "optim", "serialization", "GradScaler", "SerializationError", "save", "load",
+    "save_checkpoint", "load_checkpoint", "enable_fused_kernels", "fused_kernels_enabled", "get_backend",
     "Device", "device", "DType", "bfloat16", "float16", "float32", "float64",
     "Parameter", "Tensor", "enable_grad", "is_grad_enabled", "no_grad", "tensor",
 ]

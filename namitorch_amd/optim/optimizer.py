@@ -333,8 +333,14 @@ class Optimizer:
             restored_state[id(parameter)] = self._prepare_state(values, parameter, f"state[{index}]")
         return defaults, restored_groups, restored_state
 
+    def _install_loaded_state(self, defaults: dict, param_groups: list, state) -> None:
+        """Replace options and state with a prepared load; device-side steps
+        still in flight settle against the state they updated first."""
+        self._reconcile_device_steps()
+        self.defaults, self.param_groups, self.state = defaults, param_groups, state
+
     def load_state_dict(self, state_dict: dict) -> None:
-        self.defaults, self.param_groups, self.state = self._prepare_load_state_dict(state_dict)
+        self._install_loaded_state(*self._prepare_load_state_dict(state_dict))
 
     def to(self, device):
         target = Device(device)

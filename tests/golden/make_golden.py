@@ -199,6 +199,81 @@ def scaler_cases(nt):
     return results
 
 
+def checkpoint_case(nt):
+    """A training checkpoint written by the reference's own save_checkpoint
+    (training/checkpoint.py:80-110) after 3 AMP steps of the runner sequence on
+    a two-group AdamW, plus the parameters/moments/scaler after 2 more steps.
+    A resumed optimizer must continue bit for bit."""
+    from namitorch.training.checkpoint import save_checkpoint
+
+    class Tiny(nt.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.weight = nt.nn.Parameter(_params(40 * 48, np.float32, seed=41).reshape(40, 48))
+            self.bias = nt.nn.Parameter(_params(40, np.float32, seed=42))
+
+    model = Tiny()
+    params = [model.weight, model.bias]
+    optimizer = nt.optim.AdamW([{"params": [model.weight], "weight_decay": 0.1},
+                                {"params": [model.bias], "weight_decay": 0.0}],
+                               lr=1e-3, betas=(0.9, 0.95), eps=1e-8)
+    scaler = nt.amp.GradScaler(init_scale=1024.0, growth_interval=2)
+    raw = [_grads(p.size, 5, 1e-3, np.float32, seed_base=4100 + 10 * i) for i, p in enumerate(params)]
+    arrays = {}
+    finite_seq = []
+    for k in range(5):
+        if k == 3:
+            save_checkpoint(HERE / "checkpoint_reference.nt", model, optimizer, step=3, epoch=0,
+                            config={"case": "amp-adamw"}, cumulative_tokens=0, scaler=scaler)
+        scaler.scale(nt.Tensor(np.float32(1.0)))
+        for i, p in enumerate(params):
+            g = (raw[i][k].astype(np.float64) * scaler.get_scale()).astype(np.float32).reshape(p.shape)
+            if k == 1 and i == 1:
+                g[3] = np.inf
+            arrays[f"grad{i}_{k}"] = g.copy()
+            p._grad = nt.Tensor(g)
+        finite = scaler.unscale_(optimizer)
+        if finite:
+            nt.optim.clip_grad_norm_(params, 1.0, error_if_nonfinite=True)
+        scaler.step(optimizer)
+        scaler.update()
+        finite_seq.append(bool(finite))
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        arrays[f"p{i}"] = p._data.copy()
+        arrays[f"m{i}"] = state["exp_avg"]._data.copy()
+        arrays[f"v{i}"] = state["exp_avg_sq"]._data.copy()
+        arrays[f"step{i}"] = np.int64(state["step"])
+    np.savez(HERE / "checkpoint_resume.npz", **arrays)
+    return dict(finite=finite_seq, scale=scaler.get_scale(), scaler=scaler.state_dict(),
+                saved_at=3, steps=5, optimizer_type="namitorch.optim.adam.AdamW")
+
+
+def serialization_errors(nt, scratch: Path):
+    """Exception class names and texts of the archive writer/reader for invalid inputs."""
+    from namitorch import serialization as ser
+    texts = {}
+
+    def record(name, fn):
+        try:
+            fn()
+        except Exception as error:  # noqa: BLE001 - the class is part of the record
+            texts[name] = [type(error).__name__, str(error)]
+
+    cyclic = []
+    cyclic.append(cyclic)
+    record("save_complex", lambda: ser.save({"x": np.zeros(2, dtype=np.complex128)}, scratch / "e.nt"))
+    record("save_cycle", lambda: ser.save(cyclic, scratch / "e.nt"))
+    record("save_int_key", lambda: ser.save({1: 2}, scratch / "e.nt"))
+    record("save_object", lambda: ser.save({"x": object()}, scratch / "e.nt"))
+    (scratch / "garbage.nt").write_bytes(b"not a zip archive")
+    record("load_garbage", lambda: ser.load(scratch / "garbage.nt"))
+    ser.save({"a": np.arange(4, dtype=np.int32)}, scratch / "ok.nt")
+    record("load_max_bytes", lambda: ser.load(scratch / "ok.nt", max_array_bytes=8))
+    record("load_max_bytes_type", lambda: ser.load(scratch / "ok.nt", max_array_bytes=-1))
+    return texts
+
+
 def error_texts(nt):
     texts = {}
     half = nt.nn.Parameter(np.zeros(3, dtype=np.float16))
@@ -249,7 +324,11 @@ def main(reference: str) -> None:
         "clip": clip_cases(nt),
         "scaler": scaler_cases(nt),
         "errors": error_texts(nt),
+        "checkpoint": checkpoint_case(nt),
     }
+    import tempfile
+    with tempfile.TemporaryDirectory() as scratch:
+        golden["serialization_errors"] = serialization_errors(nt, Path(scratch))
     (HERE / "golden.json").write_text(json.dumps(golden, indent=1, sort_keys=True) + "\n")
 
 

@@ -1,0 +1,136 @@
+"""Checkpoint resume on the device.
+
+* A checkpoint written by the reference's own save_checkpoint after 3 AMP
+  steps (tests/golden/checkpoint_reference.nt) is restored into this
+  package's AdamW and GradScaler on the GPU; the next 2 steps must give the
+  reference's parameters, moments, step counts and scaler state bit for bit
+  (through the reference call sequence and through amp.fused_step).
+* Device-resident state written here (fp32 masters, bfloat16 moments, the
+  scale held on the device by fused steps) must survive save/load exactly:
+  3 steps + checkpoint + 3 steps in fresh objects equals 6 uninterrupted
+  steps, bit for bit.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import namitorch_amd as nt
+from namitorch_amd import checkpoint as ck
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _bits(tensor):
+    return tensor.bits().tobytes()
+
+
+def _tiny(device=DEV):
+    named = {"weight": nt.Parameter(np.zeros((40, 48), np.float32), device=device),
+             "bias": nt.Parameter(np.zeros(40, np.float32), device=device)}
+    optimizer = nt.optim.AdamW([{"params": [named["weight"]], "weight_decay": 0.1},
+                                {"params": [named["bias"]], "weight_decay": 0.0}],
+                               lr=1e-3, betas=(0.9, 0.95), eps=1e-8)
+    scaler = nt.GradScaler(init_scale=1024.0, growth_interval=2)
+    return named, optimizer, scaler
+
+
+@pytest.mark.parametrize("mode", ["api", "fused"])
+def test_resume_from_reference_checkpoint(mode):
+    golden = json.loads((GOLDEN / "golden.json").read_text())["checkpoint"]
+    data = np.load(GOLDEN / "checkpoint_resume.npz")
+    named, optimizer, scaler = _tiny()
+    info = ck.load_checkpoint(GOLDEN / "checkpoint_reference.nt", named, optimizer, scaler=scaler)
+    assert info["step"] == golden["saved_at"]
+    params = [named["weight"], named["bias"]]
+    for k in range(golden["saved_at"], golden["steps"]):
+        for i, p in enumerate(params):
+            p.grad = nt.Tensor(data[f"grad{i}_{k}"], device=DEV)
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        if mode == "api":
+            finite = scaler.unscale_(optimizer)
+            if finite:
+                nt.optim.clip_grad_norm_(params, 1.0, error_if_nonfinite=True)
+            scaler.step(optimizer)
+            scaler.update()
+        else:
+            finite = nt.amp.fused_step(optimizer, scaler, max_norm=1.0).finite
+        assert finite == golden["finite"][k], k
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        assert p.numpy().tobytes() == data[f"p{i}"].tobytes(), i
+        assert state["exp_avg"].numpy().tobytes() == data[f"m{i}"].tobytes(), i
+        assert state["exp_avg_sq"].numpy().tobytes() == data[f"v{i}"].tobytes(), i
+        assert state["step"] == int(data[f"step{i}"])
+    assert scaler.state_dict() == golden["scaler"]
+
+
+def _master_setup(seed):
+    rng = np.random.default_rng(seed)
+    shapes = {"embed": (1000, 64), "proj": (64, 64), "norm": (64,), "tail": (4099,)}
+    named = {}
+    for name, shape in shapes.items():
+        host = (rng.standard_normal(shape) * 0.05).astype(np.float32)
+        named[name] = nt.Parameter(host, dtype="bfloat16", device=DEV)
+    decay = [p for n, p in named.items() if n != "norm"]
+    optimizer = nt.optim.AdamW([{"params": decay, "weight_decay": 0.1},
+                                {"params": [named["norm"]], "weight_decay": 0.0}],
+                               lr=2e-3, master_weights=True, state_dtype="bfloat16")
+    scaler = nt.GradScaler(init_scale=2.0 ** 14, growth_interval=2)
+    return named, optimizer, scaler
+
+
+def _grads(named, k, scale):
+    rng = np.random.default_rng(1000 + k)
+    grads = {}
+    for name, p in named.items():
+        g = (rng.standard_normal(p.shape) * 1e-3 * scale).astype(np.float32)
+        if k == 1 and name == "tail":
+            g[17] = np.inf
+        grads[name] = g
+    return grads
+
+
+def _run(named, optimizer, scaler, steps):
+    for k in steps:
+        scale = scaler.get_scale()
+        for name, g in _grads(named, k, scale).items():
+            named[name].grad = nt.Tensor(g, dtype="bfloat16", device=DEV)
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        nt.amp.fused_step(optimizer, scaler, max_norm=0.05)
+
+
+def _snapshot(named, optimizer, scaler):
+    out = {"scaler": scaler.state_dict()}
+    for name, p in named.items():
+        state = optimizer.state[id(p)]
+        out[name] = (_bits(p), _bits(state["master"]), _bits(state["exp_avg"]), _bits(state["exp_avg_sq"]),
+                     state["step"], state["exp_avg"].dtype)
+    return out
+
+
+def test_device_state_roundtrip_is_exact(tmp_path):
+    named, optimizer, scaler = _master_setup(5)
+    _run(named, optimizer, scaler, range(6))
+    uninterrupted = _snapshot(named, optimizer, scaler)
+
+    named, optimizer, scaler = _master_setup(5)
+    _run(named, optimizer, scaler, range(3))
+    path = tmp_path / "resume.nt"
+    ck.save_checkpoint(path, named, optimizer, scaler=scaler, step=3)
+    fresh_named, fresh_optimizer, fresh_scaler = _master_setup(99)      # different weights until loaded
+    ck.load_checkpoint(path, fresh_named, fresh_optimizer, scaler=fresh_scaler)
+    assert fresh_scaler.state_dict() == scaler.state_dict()
+    _run(fresh_named, fresh_optimizer, fresh_scaler, range(3, 6))
+    resumed = _snapshot(fresh_named, fresh_optimizer, fresh_scaler)
+    assert resumed["scaler"] == uninterrupted["scaler"]
+    for name in named:
+        assert resumed[name] == uninterrupted[name], name
+    assert uninterrupted["tail"][5] is nt.bfloat16
