@@ -46,6 +46,7 @@ class DeviceStep:
         self.event = torch.cuda.Event()
         self._ctrl = None
         self._reconciled = False
+        self.scheduler = None                 # advanced at reconciliation iff the step updated
 
     def capture(self) -> None:
         """Queue the copy of the control block to pinned host memory."""
@@ -84,6 +85,8 @@ class DeviceStep:
                         gradient._finite_version = version - 1
         self.records.clear()
         self._reconciled = True
+        if self.scheduler is not None and not (self.honor_skip and ctrl.skip):
+            self.scheduler._advance()         # training/runner.py:252-253: only after an update
 
 
 class StepResult:
@@ -335,7 +338,8 @@ class GradScaler:
         self.__dict__.update(prepared.__dict__)
 
 
-def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, norm_type=2.0) -> StepResult:
+def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, norm_type=2.0,
+               scheduler=None) -> StepResult:
     """One optimizer step with the reference training loop's AMP/clip
     semantics and no host synchronization.
 
@@ -351,7 +355,20 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     bookkeeping (``state['step']``, version counters, the scale mirror) at
     the next step, ``get_scale``/``state_dict`` or ``StepResult`` access.
     ``error_if_nonfinite`` has no equivalent here (it would need the host).
+
+    ``scheduler`` (an ``optim.lr_scheduler.LRScheduler`` of ``optimizer``) is
+    stepped when this step turns out to have updated, as the training loop
+    does after ``scaler.step`` (runner.py:250-253).  The outcome is known on
+    the device first, so the scheduler advances when the step is reconciled:
+    before the next step computes its coefficients, or at the first read of
+    the schedule.
     """
+    if scheduler is not None:
+        from .optim.lr_scheduler import LRScheduler
+        if not isinstance(scheduler, LRScheduler):
+            raise TypeError("scheduler must be a NamiTorch LRScheduler or None.")
+        if scheduler.optimizer is not optimizer:
+            raise ValueError("scheduler must belong to the supplied optimizer.")
     amp = scaler is not None and scaler._enabled
     if amp:
         if not scaler._scale_used:
@@ -368,7 +385,10 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         raise RuntimeError("No gradients were found for this optimizer.")
     groups = _device_groups(gradients)
     if len(groups) != 1:
-        return _fused_step_host(optimizer, scaler, amp, maximum, order, [p for p, _ in pairs])
+        result = _fused_step_host(optimizer, scaler, amp, maximum, order, [p for p, _ in pairs])
+        if scheduler is not None and result.updated:
+            scheduler.step()
+        return result
     (backend, dtype), _ = next(iter(groups.items()))
     if backend.adamw is None:
         backend._unsupported("Optimizer steps")
@@ -382,6 +402,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     clip_bumps: list = []
     device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps)
     device_step.clip_requested = maximum is not None
+    device_step.scheduler = scheduler
     transform = GradTransform(device=device_step)
     for gradient in gradients:
         gradient._ensure_inplace_allowed()

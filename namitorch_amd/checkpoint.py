@@ -16,8 +16,8 @@ This module covers the optimizer-step side of that file:
   AdamW of this package and the reference's AdamW read each other's
   checkpoints;
 * `save_checkpoint` writes a complete checkpoint from named parameters, an
-  optimizer and a scaler (model entries are the named parameters; no
-  scheduler);
+  optimizer, a learning-rate scheduler and a scaler (model entries are the
+  named parameters);
 * `load_checkpoint` reads one, checks it like checkpoint.py:113-174 does for
   the parts it restores, and restores parameters, optimizer and scaler state
   with nothing changed unless every check passes.
@@ -36,6 +36,7 @@ from numbers import Integral
 import numpy as np
 
 from .amp import GradScaler
+from .optim.lr_scheduler import LRScheduler
 from .optim.optimizer import Optimizer
 from .serialization import SerializationError, load, save
 from .tensor import Tensor, no_grad
@@ -115,6 +116,18 @@ def parameter_names(named: dict, optimizer: Optimizer | None):
     return result
 
 
+def _check_components(optimizer, scheduler, scaler) -> None:
+    if scaler is not None and not isinstance(scaler, GradScaler):
+        raise TypeError("scaler must be a NamiTorch GradScaler or None.")
+    if optimizer is not None and not isinstance(optimizer, Optimizer):
+        raise TypeError("optimizer must be a NamiTorch Optimizer or None.")
+    if scheduler is not None:
+        if not isinstance(scheduler, LRScheduler):
+            raise TypeError("scheduler must be a NamiTorch LRScheduler or None.")
+        if optimizer is None or scheduler.optimizer is not optimizer:
+            raise ValueError("scheduler must belong to the supplied optimizer.")
+
+
 def _fresh_rng_state(seed: int = 0) -> dict:
     """A PCG64 generator state in the reference's layout (the bit generator's
     state dictionary plus a version); RNG streams are not part of this path."""
@@ -123,22 +136,22 @@ def _fresh_rng_state(seed: int = 0) -> dict:
     return state
 
 
-def save_checkpoint(path, named_parameters, optimizer: Optimizer | None = None, *, scaler: GradScaler | None = None,
-                    step: int = 0, epoch: int = 0, config=None, cumulative_tokens: int = 0) -> None:
+def save_checkpoint(path, named_parameters, optimizer: Optimizer | None = None, scheduler: LRScheduler | None = None,
+                    *, scaler: GradScaler | None = None, step: int = 0, epoch: int = 0, config=None,
+                    cumulative_tokens: int = 0) -> None:
     """Write a training checkpoint in the reference layout; ``model`` holds
-    the named parameters (detached), ``scheduler`` is None."""
-    if scaler is not None and not isinstance(scaler, GradScaler):
-        raise TypeError("scaler must be a NamiTorch GradScaler or None.")
-    if optimizer is not None and not isinstance(optimizer, Optimizer):
-        raise TypeError("optimizer must be a NamiTorch Optimizer or None.")
+    the named parameters (detached)."""
+    _check_components(optimizer, scheduler, scaler)
     named = _named(named_parameters)
+    if scheduler is not None and scheduler.get_lr() != [group["lr"] for group in optimizer.param_groups]:
+        raise ValueError("Optimizer learning rates disagree with the scheduler state.")
     checkpoint = {
         "checkpoint_version": CHECKPOINT_VERSION,
         "model": {name: parameter.detach() for name, parameter in named.items()},
         "optimizer": pack_optimizer(optimizer),
         "optimizer_type": optimizer_type(optimizer),
         "optimizer_parameter_names": parameter_names(named, optimizer),
-        "scheduler": None,
+        "scheduler": None if scheduler is None else scheduler.state_dict(),
         "rng": {"default": _fresh_rng_state(), "generators": {}},
         "step": _counter(step, "step"),
         "epoch": _counter(epoch, "epoch"),
@@ -150,17 +163,14 @@ def save_checkpoint(path, named_parameters, optimizer: Optimizer | None = None, 
     save(checkpoint, path)
 
 
-def load_checkpoint(path, named_parameters, optimizer: Optimizer | None = None, *, scaler: GradScaler | None = None,
-                    strict: bool = True, max_array_bytes=None) -> dict:
+def load_checkpoint(path, named_parameters, optimizer: Optimizer | None = None, scheduler: LRScheduler | None = None,
+                    *, scaler: GradScaler | None = None, strict: bool = True, max_array_bytes=None) -> dict:
     """Restore parameters (copied in place, so optimizers keep their
     references), optimizer and scaler state from a checkpoint written here or
     by the reference.  Every check runs before anything is modified.  Returns
     ``{"step", "epoch", "cumulative_tokens", "config", "missing",
     "unexpected"}``."""
-    if scaler is not None and not isinstance(scaler, GradScaler):
-        raise TypeError("scaler must be a NamiTorch GradScaler or None.")
-    if optimizer is not None and not isinstance(optimizer, Optimizer):
-        raise TypeError("optimizer must be a NamiTorch Optimizer or None.")
+    _check_components(optimizer, scheduler, scaler)
     if type(strict) is not bool:
         raise TypeError("strict must be a Python bool.")
     named = _named(named_parameters)
@@ -195,12 +205,19 @@ def load_checkpoint(path, named_parameters, optimizer: Optimizer | None = None, 
         if checkpoint["optimizer_parameter_names"] != parameter_names(named, optimizer):
             raise ValueError("Checkpoint optimizer parameter names or group order do not match the model.")
         optimizer_update = optimizer._prepare_load_state_dict(unpack_optimizer(checkpoint["optimizer"]))
+    scheduler_update = None
+    if scheduler is not None:
+        scheduler_update = scheduler._prepare_load_state_dict(checkpoint["scheduler"])
+        if [group["lr"] for group in optimizer_update[1]] != scheduler_update[3]:
+            raise ValueError("Checkpoint optimizer learning rates disagree with the scheduler state.")
 
     with no_grad():
         for parameter, value in copies:
             parameter.copy_(value.to(parameter.device))
     if optimizer_update is not None:
         optimizer._install_loaded_state(*optimizer_update)
+    if scheduler_update is not None:
+        scheduler._apply_loaded_state(scheduler_update)
     if prepared_scaler is not None:
         scaler.load_state_dict(checkpoint["scaler"])
     info["missing"] = missing

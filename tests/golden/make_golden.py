@@ -249,6 +249,100 @@ def checkpoint_case(nt):
                 saved_at=3, steps=5, optimizer_type="namitorch.optim.adam.AdamW")
 
 
+def scheduler_cases(nt):
+    """Learning rates of every scheduler over 14 steps on a two-group AdamW
+    (lr 1e-3 and 3e-4), their state_dicts, and construction at last_step=4."""
+    from namitorch.optim import lr_scheduler as sched
+    specs = {
+        "StepLR": dict(step_size=3, gamma=0.5),
+        "MultiStepLR": dict(milestones=[2, 5, 9], gamma=0.3),
+        "ExponentialLR": dict(gamma=0.9),
+        "CosineAnnealingLR": dict(T_max=10, eta_min=1e-5),
+        "LinearLR": dict(start_factor=0.25, end_factor=1.0, total_iters=6),
+        "WarmupCosine": dict(warmup_steps=3, total_steps=12, min_lr=2e-5),
+    }
+    out = {}
+    for name, config in specs.items():
+        results = {}
+        for last_step in (0, 4):
+            a = nt.nn.Parameter(np.zeros(3, dtype=np.float32))
+            b = nt.nn.Parameter(np.zeros(2, dtype=np.float32))
+            optimizer = nt.optim.AdamW([{"params": [a]}, {"params": [b], "lr": 3e-4}], lr=1e-3)
+            scheduler = getattr(sched, name)(optimizer, last_step=last_step, **config)
+            lrs = [[group["lr"] for group in optimizer.param_groups]]
+            for _ in range(14):
+                scheduler.step()
+                lrs.append([group["lr"] for group in optimizer.param_groups])
+            results[f"last_step_{last_step}"] = dict(lrs=lrs, state=scheduler.state_dict(),
+                                                     last_lr=scheduler.get_last_lr())
+        out[name] = dict(config=config, **results)
+    errors = {}
+
+    def record(label, fn):
+        try:
+            fn()
+        except Exception as error:  # noqa: BLE001 - the class is part of the record
+            errors[label] = [type(error).__name__, str(error)]
+
+    a = nt.nn.Parameter(np.zeros(3, dtype=np.float32))
+    optimizer = nt.optim.AdamW([a], lr=1e-3)
+    record("warmup_ge_total", lambda: sched.WarmupCosine(optimizer, 5, 5))
+    record("min_lr_above_base", lambda: sched.WarmupCosine(optimizer, 1, 5, min_lr=1.0))
+    record("step_size_zero", lambda: sched.StepLR(optimizer, 0))
+    record("gamma_negative", lambda: sched.ExponentialLR(optimizer, -0.5))
+    record("milestones_set", lambda: sched.MultiStepLR(optimizer, {1, 2}))
+    record("last_step_bool", lambda: sched.StepLR(optimizer, 2, last_step=True))
+    scheduler = sched.StepLR(optimizer, 2)
+    optimizer.add_param_group({"params": [nt.nn.Parameter(np.zeros(2, dtype=np.float32))]})
+    record("groups_changed", scheduler.step)
+    record("load_wrong_type", lambda: sched.ExponentialLR(nt.optim.AdamW([a]), 0.5).load_state_dict(
+        sched.StepLR(nt.optim.AdamW([a]), 2).state_dict()))
+    out["errors"] = errors
+    return out
+
+
+def schedule_runner_case(nt):
+    """The runner's AMP loop (training/runner.py:234-254) with WarmupCosine
+    stepping only after updated steps; non-finite grads at steps 2 and 6."""
+    from namitorch.optim.lr_scheduler import WarmupCosine
+    params = [nt.nn.Parameter(_params(1000, np.float32, seed=51)), nt.nn.Parameter(_params(64, np.float32, seed=52))]
+    optimizer = nt.optim.AdamW([{"params": [params[0]], "weight_decay": 0.1},
+                                {"params": [params[1]], "weight_decay": 0.0}], lr=2e-3, betas=(0.9, 0.95))
+    scheduler = WarmupCosine(optimizer, 3, 12, min_lr=1e-4)
+    scaler = nt.amp.GradScaler(init_scale=4096.0, growth_interval=3)
+    raw = [_grads(p.size, 10, 1e-3, np.float32, seed_base=5100 + 10 * i) for i, p in enumerate(params)]
+    arrays, lr_used, updated_seq, scale_seq = {}, [], [], []
+    for i, p in enumerate(params):
+        arrays[f"p0_{i}"] = p._data.copy()
+    for k in range(10):
+        lr_used.append([group["lr"] for group in optimizer.param_groups])
+        scaler.scale(nt.Tensor(np.float32(1.0)))
+        for i, p in enumerate(params):
+            g = (raw[i][k].astype(np.float64) * scaler.get_scale()).astype(np.float32)
+            if (k, i) in ((2, 0), (6, 1)):
+                g[5] = np.inf if k == 2 else np.nan
+            arrays[f"grad{i}_{k}"] = g.copy()
+            p._grad = nt.Tensor(g)
+        finite = scaler.unscale_(optimizer)
+        if finite:
+            nt.optim.clip_grad_norm_(params, 1.0, error_if_nonfinite=True)
+        updated = scaler.step(optimizer)
+        scaler.update()
+        if updated:
+            scheduler.step()
+        updated_seq.append(bool(updated))
+        scale_seq.append(scaler.get_scale())
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        arrays[f"p{i}"] = p._data.copy()
+        arrays[f"m{i}"] = state["exp_avg"]._data.copy()
+        arrays[f"v{i}"] = state["exp_avg_sq"]._data.copy()
+        arrays[f"step{i}"] = np.int64(state["step"])
+    np.savez(HERE / "schedule_runner.npz", **arrays)
+    return dict(lr_used=lr_used, updated=updated_seq, scale=scale_seq, last_lr=scheduler.get_last_lr(),
+                scheduler_state=scheduler.state_dict(), steps=10)
+
+
 def serialization_errors(nt, scratch: Path):
     """Exception class names and texts of the archive writer/reader for invalid inputs."""
     from namitorch import serialization as ser
@@ -325,6 +419,8 @@ def main(reference: str) -> None:
         "scaler": scaler_cases(nt),
         "errors": error_texts(nt),
         "checkpoint": checkpoint_case(nt),
+        "schedulers": scheduler_cases(nt),
+        "schedule_runner": schedule_runner_case(nt),
     }
     import tempfile
     with tempfile.TemporaryDirectory() as scratch:

@@ -9,6 +9,9 @@
   scale held on the device by fused steps) must survive save/load exactly:
   3 steps + checkpoint + 3 steps in fresh objects equals 6 uninterrupted
   steps, bit for bit.
+* The training loop's learning-rate schedule, stepped only after updated
+  steps, gives the reference's run bit for bit, also when the skip decision
+  stays on the device (fused_step with a scheduler).
 """
 
 from __future__ import annotations
@@ -134,3 +137,47 @@ def test_device_state_roundtrip_is_exact(tmp_path):
     for name in named:
         assert resumed[name] == uninterrupted[name], name
     assert uninterrupted["tail"][5] is nt.bfloat16
+
+
+@pytest.mark.parametrize("mode", ["api", "fused", "fused_observed"])
+def test_schedule_follows_updates_like_reference(mode):
+    """The training loop's WarmupCosine steps only after updated steps
+    (runner.py:250-253); with fused_step the skip is known on the device and
+    the scheduler advances at reconciliation.  10 steps with non-finite
+    gradients at steps 2 and 6 (lr 0 at step 0) must reproduce the
+    reference's parameters, moments, scale and schedule bit for bit."""
+    golden = json.loads((GOLDEN / "golden.json").read_text())["schedule_runner"]
+    data = np.load(GOLDEN / "schedule_runner.npz")
+    params = [nt.Parameter(data["p0_0"], device=DEV), nt.Parameter(data["p0_1"], device=DEV)]
+    optimizer = nt.optim.AdamW([{"params": [params[0]], "weight_decay": 0.1},
+                                {"params": [params[1]], "weight_decay": 0.0}], lr=2e-3, betas=(0.9, 0.95))
+    scheduler = nt.optim.WarmupCosine(optimizer, 3, 12, min_lr=1e-4)
+    scaler = nt.GradScaler(init_scale=4096.0, growth_interval=3)
+    for k in range(golden["steps"]):
+        if mode != "fused":
+            assert scheduler.get_last_lr() == golden["lr_used"][k], k
+        for i, p in enumerate(params):
+            p.grad = nt.Tensor(data[f"grad{i}_{k}"], device=DEV)
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        if mode == "api":
+            finite = scaler.unscale_(optimizer)
+            if finite:
+                nt.optim.clip_grad_norm_(params, 1.0, error_if_nonfinite=True)
+            updated = scaler.step(optimizer)
+            scaler.update()
+            if updated:
+                scheduler.step()
+        else:
+            result = nt.amp.fused_step(optimizer, scaler, max_norm=1.0, scheduler=scheduler)
+            if mode == "fused_observed":
+                assert result.updated == golden["updated"][k], k
+                assert scaler.get_scale() == golden["scale"][k], k
+    assert scheduler.get_last_lr() == golden["last_lr"]
+    assert scheduler.state_dict() == golden["scheduler_state"]
+    assert scaler.get_scale() == golden["scale"][-1]
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        assert p.numpy().tobytes() == data[f"p{i}"].tobytes(), i
+        assert state["exp_avg"].numpy().tobytes() == data[f"m{i}"].tobytes(), i
+        assert state["exp_avg_sq"].numpy().tobytes() == data[f"v{i}"].tobytes(), i
+        assert state["step"] == int(data[f"step{i}"])
