@@ -1,6 +1,6 @@
 """Optimizer-step benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c1,c3,c4,c5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c1,c3,c4,c5,c4s8,c5s8] [--no-cpu]
 
 Headline (the JSON line's ``value``): BASELINE config 2 — multi-tensor fp32
 AdamW over the GPT-2-124M parameter list (148 tensors, 124,439,808 params,
@@ -19,7 +19,9 @@ same workload on this host, one core.
 
 The other BASELINE configs (C1 flat 4M fp32 hot and MALL-flushed, C3 AMP
 GPT-2, C4 GPT-1.3B bf16 + clip, C5 Llama-7B AMP + clip) are reported under
-``extra`` with their own B/param accounting.
+``extra`` with their own B/param accounting, together with one GPU's share
+of an 8-way sharded C4 and C5 step (``c4s8``, ``c5s8``: every tensor split
+into 8 contiguous slices, the local work between the collectives).
 """
 
 from __future__ import annotations
@@ -50,7 +52,7 @@ def parse_args():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="c2,c1,c3,c4,c5")
+    parser.add_argument("--configs", default="c2,c1,c3,c4,c5,c4s8,c5s8")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-only", action="store_true", help="only the C2 kernel loop (for profilers)")
     parser.add_argument("--calibrate", action="store_true",
@@ -78,9 +80,12 @@ def attach_grads(nt, torch, params, dtype, sigma=1e-3, scale=1.0, seed=2337):
         param.grad = nt.Tensor._from_storage(data.to(dtype.torch_dtype).contiguous())
 
 
-def decay_groups(params):
-    return [{"params": [p for p in params if p.ndim >= 2], "weight_decay": 0.1},
-            {"params": [p for p in params if p.ndim < 2], "weight_decay": 0.0}]
+def decay_groups(params, mask=None):
+    """Weight decay 0.1 on matrices, 0 on vectors (runner.py:83-90); `mask`
+    overrides the ndim rule (shards are flat slices of the original tensors)."""
+    mask = [p.ndim >= 2 for p in params] if mask is None else mask
+    return [{"params": [p for p, m in zip(params, mask) if m], "weight_decay": 0.1},
+            {"params": [p for p, m in zip(params, mask) if not m], "weight_decay": 0.0}]
 
 
 def event_pair(torch):
@@ -182,7 +187,7 @@ def fresh_gradients(grads):
 
 
 def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype, amp, max_norm, bytes_per_param,
-                steps, warmup, modes=("fused", "api")):
+                steps, warmup, modes=("fused", "api"), mask=None):
     from namitorch_amd.param_lists import total_params
     n = total_params(shapes)
     params = make_params(nt, torch, shapes, param_dtype)
@@ -191,7 +196,7 @@ def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype
     loss = nt.Tensor._from_storage(torch.ones((), device="cuda"))
     result = dict(params=n, tensors=len(shapes), bytes_per_param=bytes_per_param)
     for mode in modes:
-        optimizer = nt.optim.AdamW(decay_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8,
+        optimizer = nt.optim.AdamW(decay_groups(params, mask), lr=3e-4, betas=(0.9, 0.999), eps=1e-8,
                                    master_weights=True, state_dtype=state_dtype)
         scaler = nt.GradScaler(init_scale=65536.0) if amp else None
 
@@ -313,7 +318,7 @@ def main():
             c2["calibration_copy_bytes"] = {"read": source.numel() * 4, "write": target.numel() * 4, "launches": 3}
         print(json.dumps(c2))
         return
-    from namitorch_amd.param_lists import gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes
+    from namitorch_amd.param_lists import decay_mask, gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes, shard_shapes
     if "c1" in wanted:
         log("C1 flat 4M fp32")
         extra["c1_flat4m_fp32"] = bench_c1(nt, torch, args.steps, args.warmup)
@@ -334,6 +339,21 @@ def main():
                                                    grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
                                                    bytes_per_param=30, steps=max(5, args.steps // 5),
                                                    warmup=min(args.warmup, 3))
+    # One GPU's share of an 8-way sharded step (every tensor split into 8
+    # contiguous slices, ZeRO-1 style): the local pre-pass + AdamW pass that
+    # each rank would run between the collectives.
+    if "c4s8" in wanted:
+        log("C4/8 shard: gpt-1.3b list, 1/8 of every tensor, bf16 + clip")
+        extra["c4_shard8"] = bench_mixed(nt, torch, "c4s8", shard_shapes(gpt_1p3b_shapes(), 8), param_dtype=nt.bfloat16,
+                                         grad_dtype=nt.bfloat16, state_dtype=nt.bfloat16, amp=False, max_norm=1.0,
+                                         bytes_per_param=22, steps=args.steps, warmup=args.warmup, modes=("fused",),
+                                         mask=decay_mask(gpt_1p3b_shapes()))
+    if "c5s8" in wanted:
+        log("C5/8 shard: llama-7b list, 1/8 of every tensor, AMP + clip")
+        extra["c5_shard8"] = bench_mixed(nt, torch, "c5s8", shard_shapes(llama7b_shapes(), 8), param_dtype=nt.bfloat16,
+                                         grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
+                                         bytes_per_param=30, steps=max(5, args.steps // 2), warmup=args.warmup,
+                                         modes=("fused",), mask=decay_mask(llama7b_shapes()))
     baseline = None
     if not args.no_cpu:
         log("CPU baseline (NumPy oracle)")

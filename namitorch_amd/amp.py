@@ -18,6 +18,7 @@ from __future__ import annotations
 import ctypes
 import math
 import operator
+from operator import attrgetter, itemgetter
 from numbers import Real
 
 import numpy as np
@@ -25,7 +26,17 @@ import numpy as np
 from . import _native
 from .backends import get_backend
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
-from .tensor import GradTransform
+from .tensor import GradTransform, is_grad_enabled
+
+_REQUIRES = attrgetter("_requires_grad")
+_WRITABLE = attrgetter("_writable")
+_PENDING = attrgetter("_pending")
+_COUNTER = attrgetter("_version_counter")
+_VALUE = attrgetter("value")
+_DTYPE = attrgetter("_dtype")
+_FLOATING = attrgetter("_floating")
+_FIRST_OF = itemgetter(0)
+_SECOND_OF = itemgetter(1)
 
 
 class DeviceStep:
@@ -217,9 +228,9 @@ class GradScaler:
         if not callable(getattr(optimizer, "_parameters_with_grad", None)) or not callable(getattr(optimizer, "step", None)):
             raise TypeError("GradScaler requires a NamiTorch optimizer.")
         gradients = tuple((parameter, gradient) for _, parameter, gradient in optimizer._parameters_with_grad())
-        for parameter, gradient in gradients:
-            if not parameter.dtype.can_require_grad or gradient.requires_grad:
-                raise RuntimeError("GradScaler requires detached floating gradients.")
+        if any(map(_REQUIRES, map(_SECOND_OF, gradients))) or not all(
+                map(_FLOATING, map(_DTYPE, map(_FIRST_OF, gradients)))):
+            raise RuntimeError("GradScaler requires detached floating gradients.")
         return gradients
 
     @staticmethod
@@ -404,17 +415,23 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     device_step.clip_requested = maximum is not None
     device_step.scheduler = scheduler
     transform = GradTransform(device=device_step)
+    if (any(map(_REQUIRES, gradients)) and is_grad_enabled()) or not all(map(_WRITABLE, gradients)):
+        for gradient in gradients:
+            gradient._ensure_inplace_allowed()            # raises the matching error
+    if any(map(_PENDING, gradients)):
+        for gradient in gradients:
+            if gradient._pending is not None:
+                gradient._materialize()
+    # unscale_ rewrites every gradient (one version bump); the clip may (one
+    # more, undone on reconcile if the device decides not to clip).
+    bumps = int(amp) + int(maximum is not None)
     for gradient in gradients:
-        gradient._ensure_inplace_allowed()
-        if gradient._pending is not None:
-            gradient._materialize()
         gradient._pending = transform
-        if amp:
-            gradient._version_counter.value += 1          # unscale_ rewrites the gradient
-        if maximum is not None:
-            gradient._version_counter.value += 1          # clip may; undone on reconcile if not
-            clip_bumps.append((gradient, gradient._version_counter.value))
-        gradient._finite_version = gradient._version_counter.value
+        counter = gradient._version_counter
+        counter.value += bumps
+        gradient._finite_version = counter.value
+    if maximum is not None:
+        clip_bumps.extend(zip(gradients, map(_VALUE, map(_COUNTER, gradients))))
     layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
     plan = backend.plan(backend.grad_rows(gradients), layout)
     backend.grad_prepass(plan, None, block.data_ptr(), unscale=amp)

@@ -229,6 +229,12 @@ class _FirstOrderOptimizer(Optimizer):
         if closure is not None:
             with enable_grad():
                 loss = closure()
+        replay = self.__dict__.get("_replay")
+        if replay is not None:
+            with no_grad():
+                if replay.run(self):
+                    return loss
+            self._replay = None
         entries = list(self._parameters_with_grad())
         options = {
             id(group): self._prepare_options({key: value for key, value in group.items() if key != "params"}, "param_group")
@@ -269,7 +275,13 @@ class _FirstOrderOptimizer(Optimizer):
             items.append((parameter, gradient, prepared))
         with no_grad():
             self._update_many(items)
+        self._memoize_step(options)
         return loss
+
+    def _memoize_step(self, options: dict) -> None:
+        """Record what a later step may replay without the per-tensor checks
+        (subclasses that launch multi-tensor kernels); `options` maps id(group)
+        to the prepared options of this step."""
 
     def _update_many(self, items) -> None:
         """Apply the update to every (parameter, gradient, options) of a step."""

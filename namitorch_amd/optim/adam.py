@@ -25,6 +25,7 @@ unrounded float32 values).
 from __future__ import annotations
 
 import weakref
+from operator import attrgetter, eq, is_, itemgetter
 
 from .. import _native
 from ..backends import get_backend
@@ -109,6 +110,7 @@ class Adam(_FirstOrderOptimizer):
         return first, second, master
 
     def _update_many(self, items) -> None:
+        self._batches = []
         if not items:
             return
         layouts: dict = {}
@@ -171,6 +173,8 @@ class Adam(_FirstOrderOptimizer):
         records: list = []
         rows: list = []
         bookkeeping: list = []
+        slot_specs: list = []        # (id(options), step, fused) per coefficient slot
+        member_slots: list = []
         transform = members[0][1]._pending
         for _, gradient, _ in members:
             if gradient._pending != transform:
@@ -201,6 +205,8 @@ class Adam(_FirstOrderOptimizer):
             if slot is None:
                 slot = slot_of[key] = len(records)
                 records.append(self._coefficients(compute, options, step, fused))
+                slot_specs.append((id(options), step, fused))
+            member_slots.append(slot)
             if master is not None:
                 rows.append((master._ptr, gradient._ptr, first._ptr, second._ptr, parameter._ptr, parameter._numel, slot))
             else:
@@ -209,6 +215,7 @@ class Adam(_FirstOrderOptimizer):
         slots = ((_native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs) * len(records))(*records)
         plan = backend.plan(rows, layout)
         backend.adamw_multi(plan, slots, None if transform is None else make_xform(transform))
+        self._batches.append((backend, plan, compute, slot_specs, member_slots, bookkeeping))
         device_step = None if transform is None else transform.device
         for parameter, state, first, second, master, step, fused, moves in bookkeeping:
             bumped = not fused or parameter._numel
@@ -228,6 +235,169 @@ class Adam(_FirstOrderOptimizer):
                 device_step.records.append((parameter, state, first, second, master, step, bumped, moves))
         if device_step is not None:
             device_step.optimizers.add(self)
+
+    def _memoize_step(self, options: dict) -> None:
+        batches = self.__dict__.pop("_batches", None)
+        self._replay = None
+        if batches is None or len(batches) != 1:
+            return
+        cached = self.__dict__.get("_registered_cache")
+        if cached is None:
+            return
+        group_index = {id(options[id(group)]): index for index, group in enumerate(self.param_groups)}
+        self._replay = _Replay(self, cached, group_index, *batches[0])
+
+
+_GRAD = attrgetter("_grad")
+_REQUIRES = attrgetter("_requires_grad")
+_WRITABLE = attrgetter("_writable")
+_PENDING = attrgetter("_pending")
+_CLEAN = attrgetter("_clean_version")
+_VALUE = attrgetter("value")
+_COUNTER = attrgetter("_version_counter")
+_FIRST = itemgetter("exp_avg")
+_SECOND = itemgetter("exp_avg_sq")
+_MASTER = itemgetter("master")
+_STEP = itemgetter("step")
+
+
+class _Replay:
+    """Memo of the last step's single multi-tensor launch.
+
+    The full step re-validates every parameter, gradient and state entry, at
+    about a microsecond of Python per tensor.  Those checks depend only on
+    which objects are involved (a Tensor's dtype, shape, device and storage
+    never change) and on a few mutable fields.  A later step replays the
+    launch when all of these are unchanged:
+    - the registered parameters, their gradients and ``requires_grad`` flags;
+    - the state dictionaries, their buffers and step counts;
+    - the buffers' flags and the nonnegative buffer's versions.
+
+    Each is verified with a C-level pass over the tuples kept here.  The
+    replay prepares and validates the options again, recomputes the
+    coefficients for the next step counts, relaunches the cached plan and
+    applies the same bookkeeping.  Anything else makes ``run`` return False,
+    and the caller runs the full step, which builds a new memo.
+    """
+
+    __slots__ = ("registered_cache", "registered", "requires", "grads", "state", "ids", "dicts", "lens", "firsts",
+                 "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
+                 "second_counters", "fused_options", "enabled", "validate", "slots", "backend", "plan", "compute",
+                 "record_type", "moment_pairs", "move_counters", "member_groups", "bumped")
+
+    def __init__(self, optimizer, cached, group_index, backend, plan, compute, slot_specs, member_slots, bookkeeping):
+        self.registered_cache = cached
+        self.registered = cached[1]
+        self.requires = tuple(map(_REQUIRES, self.registered))
+        self.grads = tuple(map(_GRAD, self.registered))
+        self.state = optimizer.state
+        self.members = tuple(entry[0] for entry in bookkeeping)
+        self.member_grads = tuple(map(_GRAD, self.members))
+        self.ids = tuple(map(id, self.members))
+        self.dicts = tuple(entry[1] for entry in bookkeeping)
+        self.lens = tuple(map(len, self.dicts))
+        self.firsts = tuple(entry[2] for entry in bookkeeping)
+        self.seconds = tuple(entry[3] for entry in bookkeeping)
+        self.masters = tuple(entry[4] for entry in bookkeeping)
+        self.master_mode = optimizer._master_weights
+        self.steps = tuple(entry[5] for entry in bookkeeping)
+        self.buffers = self.firsts + self.seconds + (self.masters if self.master_mode else ())
+        self.second_counters = tuple(map(_COUNTER, self.seconds))
+        groups = optimizer.param_groups
+        self.fused_options = tuple(group.get("fused") for group in groups)
+        self.enabled = fused_kernels_enabled()
+        # Coefficient slots in launch order: (group index, step count used last, fused flag).
+        self.slots = [(group_index[options_id], step, fused) for options_id, step, fused in slot_specs]
+        self.member_groups = tuple(self.slots[slot][0] for slot in member_slots)
+        representatives: dict = {}
+        for parameter, group in zip(self.members, self.member_groups):
+            representatives.setdefault((parameter._dtype, group), parameter)
+        self.validate = tuple((group, parameter) for (_, group), parameter in representatives.items())
+        self.backend = backend
+        self.plan = plan
+        self.compute = compute
+        self.record_type = _native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs
+        self.bumped = tuple(bool(not entry[6] or entry[0]._numel) for entry in bookkeeping)
+        self.moment_pairs = tuple((buffer, buffer._version_counter)
+                                  for entry, bumped in zip(bookkeeping, self.bumped) if bumped
+                                  for buffer in (entry[2], entry[3]))
+        moving: list = [[] for _ in groups]
+        for entry, bumped, group in zip(bookkeeping, self.bumped, self.member_groups):
+            if bumped:
+                moving[group].append(entry[0]._version_counter)
+                if entry[4] is not None:
+                    moving[group].append(entry[4]._version_counter)
+        self.move_counters = tuple(tuple(counters) for counters in moving)
+
+    def _unchanged(self, optimizer) -> bool:
+        optimizer._registered_parameters()
+        if optimizer.__dict__.get("_registered_cache") is not self.registered_cache:
+            return False
+        registered = self.registered
+        if tuple(map(_REQUIRES, registered)) != self.requires:
+            return False
+        if not all(map(is_, map(_GRAD, registered), self.grads)):
+            return False
+        state = optimizer.state
+        if state is not self.state:
+            return False
+        dicts = tuple(map(state.get, self.ids))
+        if not all(map(is_, dicts, self.dicts)) or tuple(map(len, dicts)) != self.lens:
+            return False
+        try:
+            if not (all(map(is_, map(_FIRST, dicts), self.firsts)) and all(map(is_, map(_SECOND, dicts), self.seconds))
+                    and (not self.master_mode or all(map(is_, map(_MASTER, dicts), self.masters)))):
+                return False
+            steps = tuple(map(_STEP, dicts))
+        except KeyError:
+            return False
+        if steps != self.steps or set(map(type, steps)) != {int}:
+            return False
+        buffers = self.buffers
+        if any(map(_REQUIRES, buffers)) or not all(map(_WRITABLE, buffers)) or not all(map(_WRITABLE, self.members)):
+            return False
+        if not all(map(eq, map(_CLEAN, self.seconds), map(_VALUE, self.second_counters))):
+            return False
+        if len(set(map(id, map(_PENDING, self.member_grads)))) != 1:
+            return False
+        return fused_kernels_enabled() is self.enabled
+
+    def run(self, optimizer) -> bool:
+        if not self._unchanged(optimizer):
+            return False
+        prepared = [optimizer._prepare_options({key: value for key, value in group.items() if key != "params"},
+                                               "param_group") for group in optimizer.param_groups]
+        if tuple(options.get("fused") for options in prepared) != self.fused_options:
+            return False
+        checked: set = set()
+        for group, parameter in self.validate:
+            optimizer._validate_entry(parameter, prepared[group], checked)
+        records = [optimizer._coefficients(self.compute, prepared[group], step + 1, fused)
+                   for group, step, fused in self.slots]
+        transform = self.member_grads[0]._pending
+        self.backend.adamw_multi(self.plan, (self.record_type * len(records))(*records),
+                                 None if transform is None else make_xform(transform))
+        # Bookkeeping of the full step: moments always, parameter (and master)
+        # only for groups whose lr is nonzero, then the step counts.
+        for buffer, counter in self.moment_pairs:
+            counter.value += 1
+            buffer._clean_version = counter.value
+        moves = [options["lr"] != 0 for options in prepared]
+        for group, counters in enumerate(self.move_counters):
+            if moves[group]:
+                for counter in counters:
+                    counter.value += 1
+        steps = tuple(step + 1 for step in self.steps)
+        for values, step in zip(self.dicts, steps):
+            values["step"] = step
+        self.steps = steps
+        self.slots = [(group, step + 1, fused) for group, step, fused in self.slots]
+        device_step = None if transform is None else transform.device
+        if device_step is not None:
+            device_step.records.extend(zip(self.members, self.dicts, self.firsts, self.seconds, self.masters, steps,
+                                           self.bumped, map(moves.__getitem__, self.member_groups)))
+            device_step.optimizers.add(optimizer)
+        return True
 
 
 class AdamW(Adam):

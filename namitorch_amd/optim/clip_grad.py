@@ -19,6 +19,8 @@ the next kernel that reads them.
 
 from __future__ import annotations
 
+from operator import attrgetter
+
 import math
 from numbers import Real
 
@@ -124,7 +126,18 @@ def _remember_stats(gradients, stats: GradStats) -> None:
     _last_stats[_stats_key(gradients)] = (list(gradients), stats)
 
 
+_DEVICE = attrgetter("_device")
+_DTYPE = attrgetter("_dtype")
+
+
 def _device_groups(gradients) -> dict:
+    """Gradients grouped by (backend, dtype), in order."""
+    if gradients:
+        # Common case: one device and one dtype (C-level passes only).
+        devices = set(map(_DEVICE, gradients))
+        if len(set(map(_DTYPE, gradients))) == 1 and len(devices) == 1:
+            first = gradients[0]
+            return {(get_backend(first), first._dtype): list(gradients)}
     groups: dict = {}
     for gradient in gradients:
         groups.setdefault((get_backend(gradient), gradient.dtype), []).append(gradient)

@@ -53,6 +53,13 @@ def numel(shape: tuple[int, ...]) -> int:
     return total
 
 
+def shard_shapes(shapes, world: int) -> list[tuple[int, ...]]:
+    """One rank's share when every tensor's flat storage is split into
+    `world` equal contiguous slices (the last rank's slices may be shorter;
+    this returns the full-length ones)."""
+    return [((numel(shape) + world - 1) // world,) for shape in shapes]
+
+
 def total_params(shapes) -> int:
     return sum(numel(shape) for shape in shapes)
 

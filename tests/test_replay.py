@@ -1,0 +1,150 @@
+"""The step memo (adam._Replay) against the full step, on the host.
+
+A recording backend stands in for the device: it keeps every launch's
+rows, coefficient records and grad transform.  The same sequence of steps
+and mutations (lr changes, new or missing gradients, requires_grad flips,
+replaced or rewritten state buffers, edited step counts, pending grad
+transforms, fused-flag changes, invalid state) runs once with the memo and
+once with it disabled; launches, errors and every version counter and step
+count must agree, and the memo must actually replay the unchanged steps.
+"""
+
+from __future__ import annotations
+
+from contextlib import nullcontext
+
+import numpy as np
+import pytest
+
+import namitorch_amd as nt
+from namitorch_amd.optim import adam as adam_mod
+from namitorch_amd.tensor import GradTransform
+
+
+class _Kernel:
+    def supports(self, *arrays):
+        return True
+
+
+class _RecordingBackend:
+    def __init__(self):
+        self.device = nt.Device("cpu")
+        self.adamw = _Kernel()
+        self.launches = []
+        self._plans = {}
+
+    def context(self, *operands):
+        return nullcontext()
+
+    def plan(self, rows, layout, chunk=0):
+        key = (layout, chunk, tuple(rows))
+        return self._plans.setdefault(key, ("plan", key))
+
+    def adamw_multi(self, plan, slots, xform):
+        records = [tuple(getattr(record, name) for name, _ in record._fields_) for record in slots]
+        transform = None if xform is None else (xform.scale, xform.unscale, xform.clip, xform.clip_coef)
+        self.launches.append((plan[1], records, transform))
+
+
+def _run(monkeypatch, memo: bool):
+    backend = _RecordingBackend()
+    monkeypatch.setattr(adam_mod, "get_backend", lambda value=None: backend)
+    replays = []
+    original_run = adam_mod._Replay.run
+
+    def counting_run(self, optimizer):
+        done = original_run(self, optimizer)
+        replays.append(done)
+        return done
+
+    monkeypatch.setattr(adam_mod._Replay, "run", counting_run)
+    if not memo:
+        monkeypatch.setattr(adam_mod.Adam, "_memoize_step", lambda self, options: setattr(self, "_replay", None))
+    rng = np.random.default_rng(3)
+    shapes = [(8, 4), (5,), (3, 3), (7,), (2, 6), (4,)]
+    params = [nt.Parameter(rng.standard_normal(s).astype(np.float32)) for s in shapes]
+    for p in params:
+        p.grad = nt.Tensor(rng.standard_normal(p.shape).astype(np.float32))
+    optimizer = nt.optim.AdamW([{"params": params[:3], "weight_decay": 0.1},
+                                {"params": params[3:], "weight_decay": 0.0}], lr=1e-3)
+    errors = []
+    for k in range(18):
+        if k == 3:
+            optimizer.param_groups[0]["lr"] = 5e-4
+        elif k == 4:
+            params[2].grad = nt.Tensor(rng.standard_normal(params[2].shape).astype(np.float32))
+        elif k == 5:
+            params[3].grad = None
+        elif k == 6:
+            params[3].grad = nt.Tensor(np.ones(params[3].shape, np.float32))
+            params[1].requires_grad = False
+        elif k == 7:
+            params[1].requires_grad = True
+            state = optimizer.state[id(params[0])]
+            state["exp_avg"] = state["exp_avg"].clone()
+        elif k == 8:
+            optimizer.param_groups[1]["lr"] = 0.0
+        elif k == 9:
+            buffer = optimizer.state[id(params[4])]["exp_avg_sq"]
+            buffer.copy_(nt.Tensor(np.full(buffer.shape, 0.25, np.float32)))
+        elif k == 10:
+            optimizer.param_groups[1]["lr"] = 2e-3
+            transform = GradTransform(scale=4.0)
+            for p in params:
+                p.grad._pending = transform
+        elif k == 11:
+            for p in params:
+                p.grad._pending = None
+            optimizer.state[id(params[5])]["step"] += 2
+        elif k == 13:
+            optimizer.param_groups[0]["fused"] = False
+        elif k == 14:
+            optimizer.state[id(params[1])]["step"] = 7.0
+        elif k == 15:
+            optimizer.state[id(params[1])]["step"] = 7
+            buffer = optimizer.state[id(params[4])]["exp_avg_sq"]
+            buffer.copy_(nt.Tensor(np.full(buffer.shape, -1.0, np.float32)))
+        elif k == 16:
+            buffer = optimizer.state[id(params[4])]["exp_avg_sq"]
+            buffer.copy_(nt.Tensor(np.full(buffer.shape, 1.0, np.float32)))
+        try:
+            optimizer.step()
+        except (TypeError, ValueError) as error:
+            errors.append((k, type(error).__name__, str(error)))
+    versions = []
+    for p in params:
+        state = optimizer.state[id(p)]
+        versions.append((p._version, state["step"], state["exp_avg"]._version, state["exp_avg_sq"]._version,
+                         state["exp_avg_sq"]._clean_version))
+    return backend.launches, errors, versions, replays
+
+
+def test_memo_replays_exactly_what_the_full_step_launches(monkeypatch):
+    with monkeypatch.context() as patch:
+        full = _run(patch, memo=False)
+    with monkeypatch.context() as patch:
+        memo = _run(patch, memo=True)
+    assert memo[0] == full[0]                 # every launch: rows, coefficients, transform
+    assert memo[1] == full[1] and len(full[1]) == 2   # the invalid step counts and negative state
+    assert memo[2] == full[2]
+    assert full[3] == []
+    replayed = sum(memo[3])
+    assert replayed >= 6, memo[3]             # unchanged steps did replay
+    assert len(memo[3]) - replayed >= 8       # every mutation fell back to the full step
+
+
+def test_memo_is_dropped_by_load_state_dict(monkeypatch):
+    backend = _RecordingBackend()
+    monkeypatch.setattr(adam_mod, "get_backend", lambda value=None: backend)
+    p = nt.Parameter(np.ones(4, np.float32))
+    p.grad = nt.Tensor(np.ones(4, np.float32))
+    optimizer = nt.optim.AdamW([p])
+    optimizer.step()
+    optimizer.step()
+    saved = optimizer.state_dict()
+    optimizer.step()
+    assert optimizer._replay is not None
+    optimizer.load_state_dict(saved)
+    optimizer.step()
+    assert optimizer.state[id(p)]["step"] == 3
+    assert backend.launches[-1][1] == backend.launches[-2][1]      # same coefficients as the third step
