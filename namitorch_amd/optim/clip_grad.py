@@ -242,6 +242,7 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
         coefficient = float(np.divide(np.float64(maximum), np.add(np.float64(norm), _NORM_EPS)))
     if coefficient < 1:
         _require_writable(gradients)
+        clipped: dict = {}      # one shared transform per prior pending transform
         with no_grad():
             for gradient in gradients:
                 gradient._ensure_inplace_allowed()
@@ -250,7 +251,11 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
                     gradient._materialize()
                     pending = None
                 keep_finite = gradient._finite_version is not None and gradient._finite_version == gradient._version
-                gradient._pending = (pending or GradTransform()).then_clip(coefficient)
+                base = pending or GradTransform()
+                transform = clipped.get(base)
+                if transform is None:
+                    transform = clipped[base] = base.then_clip(coefficient)
+                gradient._pending = transform
                 gradient._version_counter.increment()
                 if keep_finite:
                     gradient._finite_version = gradient._version
