@@ -264,6 +264,27 @@ int32_t nt_ctrl_reset(nt_amp_ctrl *ctrl, float scale, int32_t growth_tracker,
  * cleared.  dst and src may not alias. */
 int32_t nt_ctrl_carry(nt_amp_ctrl *dst, const nt_amp_ctrl *src, void *stream);
 
+/* ---- gradient producer edges ------------------------------------------- */
+
+/*
+ * Zero every gradient of `plan` in one launch: Optimizer.zero_grad with
+ * set_to_none=False (optim/optimizer.py:197-206, grad.zero_() per
+ * parameter).  Gradients are the plan's `grad` column (layout.grad_dtype).
+ */
+int32_t nt_grad_zero(nt_plan *plan, void *stream);
+
+/*
+ * Accumulate incoming gradients into stored ones for every tensor of
+ * `plan` in one launch: Tensor._accumulate_grad (tensor.py:443-450) over
+ * autograd.accumulate_gradient (autograd.py:198-205).  Stored gradients are
+ * the `grad` column (layout.grad_dtype), incoming ones the `param` column
+ * (layout.param_dtype).  Each incoming value is cast to the stored dtype
+ * (round to nearest even) and added in the stored dtype, as NumPy does;
+ * with `assign` != 0 the cast value replaces the stored one (the first
+ * gradient of a leaf).
+ */
+int32_t nt_grad_accumulate(nt_plan *plan, int32_t assign, void *stream);
+
 /* ---- small single-array kernels ---------------------------------------- */
 
 /*

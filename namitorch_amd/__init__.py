@@ -7,9 +7,10 @@ through ctypes.  Optimizer and scaler state read and write NamiTorch's
 ``.nt`` archive and checkpoint layout (``serialization``, ``checkpoint``).
 """
 
-from . import amp, checkpoint, optim, serialization
+from . import amp, checkpoint, grads, optim, serialization
 from .amp import GradScaler
 from .checkpoint import load_checkpoint, save_checkpoint
+from .grads import accumulate_grads
 from .serialization import SerializationError, load, save
 from .backends import enable_fused_kernels, fused_kernels_enabled, get_backend
 from .device import Device, device
@@ -17,7 +18,7 @@ from .dtype import DType, bfloat16, float16, float32, float64
 from .tensor import Parameter, Tensor, enable_grad, is_grad_enabled, no_grad, tensor
 
 __all__ = [
-    "amp", "checkpoint", "optim", "serialization", "GradScaler", "SerializationError", "save", "load",
+    "amp", "checkpoint", "grads", "accumulate_grads", "optim", "serialization", "GradScaler", "SerializationError", "save", "load",
     "save_checkpoint", "load_checkpoint", "enable_fused_kernels", "fused_kernels_enabled", "get_backend",
     "Device", "device", "DType", "bfloat16", "float16", "float32", "float64",
     "Parameter", "Tensor", "enable_grad", "is_grad_enabled", "no_grad", "tensor",

@@ -132,6 +132,8 @@ SIGNATURES = {
     "nt_amp_finalize": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_int32, c_double, c_double, c_int32, c_void_p]),
     "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_void_p]),
     "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
+    "nt_grad_zero": (c_int32, [c_void_p, c_void_p]),
+    "nt_grad_accumulate": (c_int32, [c_void_p, c_int32, c_void_p]),
     "nt_ctrl_reset": (c_int32, [c_void_p, c_float, c_int32, c_void_p]),
     "nt_ctrl_carry": (c_int32, [c_void_p, c_void_p, c_void_p]),
     "nt_scale_array": (c_int32, [c_void_p, c_void_p, c_int32, c_double, c_void_p, c_uint64, c_void_p]),

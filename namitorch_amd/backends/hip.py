@@ -239,6 +239,30 @@ class HIPBackend:
     def grad_rows(self, tensors) -> list[tuple]:
         return [(0, tensor._ptr, 0, 0, 0, tensor.size, 0) for tensor in tensors]
 
+    def zero_tensors(self, tensors) -> None:
+        """Zero every tensor (one launch per dtype)."""
+        by_dtype: dict = {}
+        for tensor in tensors:
+            by_dtype.setdefault(tensor.dtype, []).append(tensor)
+        for dtype, group in by_dtype.items():
+            layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
+            plan = self.plan(self.grad_rows(group), layout)
+            with self.context():
+                _native.call("nt_grad_zero", plan.handle, self.stream())
+
+    def accumulate_tensors(self, stored, incoming, assign: bool) -> None:
+        """stored[i] <- cast(incoming[i]) (+ stored[i] unless `assign`), one
+        launch per (stored dtype, incoming dtype)."""
+        by_dtypes: dict = {}
+        for target, source in zip(stored, incoming):
+            by_dtypes.setdefault((target.dtype, source.dtype), []).append((target, source))
+        for (target_dtype, source_dtype), pairs in by_dtypes.items():
+            layout = (source_dtype.code, target_dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
+            rows = [(source._ptr, target._ptr, 0, 0, 0, target.size, 0) for target, source in pairs]
+            plan = self.plan(rows, layout)
+            with self.context():
+                _native.call("nt_grad_accumulate", plan.handle, int(assign), self.stream())
+
     def apply_grad_transform(self, tensors, transform) -> None:
         """Write pending GradTransforms back in place (one launch per dtype)."""
         by_dtype: dict = {}

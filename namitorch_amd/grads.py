@@ -1,0 +1,121 @@
+"""Gradient producer edges of the optimizer step.
+
+``accumulate_grads(parameters, gradients)`` is ``Tensor._accumulate_grad``
+(namitorch/tensor.py:443-450 over autograd.accumulate_gradient,
+autograd.py:198-205) for many leaves at once: one device launch per
+(stored dtype, incoming dtype) instead of one NumPy/CuPy expression per
+leaf.  A leaf without a gradient receives a new gradient Tensor holding the
+incoming values cast to its dtype; a leaf with one has the cast values added
+in place (a ``copy_``: its version counter advances).  Validation order and
+messages are the reference's.  ``Optimizer.zero_grad(set_to_none=False)``
+uses ``zero_grads``, one launch per dtype.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .backends import ensure_same_device, get_backend
+from .tensor import Tensor
+
+_GRADIENT_DTYPES = ("float16", "bfloat16", "float32", "float64")
+
+
+def _validate(parent: Tensor, gradient, operation: str, exact_dtype: bool = False) -> None:
+    """validate_gradient (autograd.py:176-187)."""
+    if not isinstance(gradient, Tensor):
+        raise RuntimeError(f"{operation} must be a registered backend gradient array.")
+    if gradient.shape != parent.shape:
+        raise RuntimeError(f"{operation} has invalid gradient shape {gradient.shape}; expected {parent.shape}.")
+    if not parent.dtype.can_require_grad or gradient.dtype.value not in _GRADIENT_DTYPES:
+        raise RuntimeError(f"{operation} requires supported floating gradients and a floating parent, "
+                           f"got {gradient.dtype.value} and {parent.dtype}.")
+    ensure_same_device(parent, gradient)
+    if exact_dtype and gradient.dtype is not parent.dtype:
+        raise RuntimeError(f"{operation} has gradient dtype {gradient.dtype.value}; expected {parent.dtype}.")
+
+
+def _validate_accumulation(parent: Tensor, gradient) -> None:
+    """validate_accumulation (autograd.py:190-195)."""
+    _validate(parent, gradient, "Gradient accumulation")
+    existing = parent._grad
+    if existing is not None:
+        _validate(parent, existing, "Stored gradient", exact_dtype=True)
+        if existing.requires_grad:
+            raise RuntimeError("Stored gradients must be detached from autograd.")
+
+
+def accumulate_grads(parameters, gradients) -> None:
+    """For each (leaf, incoming gradient): ``leaf.grad`` becomes the incoming
+    gradient cast to the leaf's dtype, or has it added in the leaf's dtype.
+    Every pair is validated before anything is written."""
+    parameters = list(parameters)
+    gradients = list(gradients)
+    if len(parameters) != len(gradients):
+        raise ValueError("accumulate_grads needs one gradient per parameter.")
+    for parameter, gradient in zip(parameters, gradients):
+        if not isinstance(parameter, Tensor):
+            raise TypeError("accumulate_grads requires NamiTorch Tensors.")
+        _validate_accumulation(parameter, gradient)
+        if parameter._grad is not None:
+            parameter._grad._ensure_inplace_allowed()
+    # A leaf listed twice accumulates twice, in order: split into rounds in
+    # which every leaf appears once (one launch cannot update a leaf twice).
+    rounds: list = []
+    seen_in: dict = {}
+    for parameter, gradient in zip(parameters, gradients):
+        index = seen_in.get(id(parameter), -1) + 1
+        seen_in[id(parameter)] = index
+        if index == len(rounds):
+            rounds.append([])
+        rounds[index].append((parameter, gradient))
+    for members in rounds:
+        _accumulate_round(members)
+
+
+def _accumulate_round(members) -> None:
+    by_backend: dict = {}
+    for parameter, gradient in members:
+        by_backend.setdefault(get_backend(parameter), []).append((parameter, gradient))
+    for backend, pairs in by_backend.items():
+        if getattr(backend, "adamw", None) is None:
+            backend._unsupported("Gradient accumulation")
+        fresh, existing = [], []
+        for parameter, gradient in pairs:
+            if gradient._pending is not None:
+                gradient._materialize()
+            stored = parameter._grad
+            if stored is None:
+                storage = torch.empty(parameter.shape, dtype=parameter.dtype.torch_dtype, device=parameter.device.torch)
+                parameter._grad = Tensor._from_storage(storage)
+                fresh.append((parameter._grad, gradient))
+            else:
+                if stored._pending is not None:
+                    stored._materialize()
+                existing.append((stored, gradient))
+        if fresh:
+            backend.accumulate_tensors([s for s, _ in fresh], [g for _, g in fresh], assign=True)
+        if existing:
+            backend.accumulate_tensors([s for s, _ in existing], [g for _, g in existing], assign=False)
+            for stored, _ in existing:
+                stored._version_counter.increment()
+
+
+def zero_grads(gradients) -> None:
+    """``grad.zero_()`` for every gradient: device gradients in one launch
+    per (device, dtype); host gradients through ``Tensor.zero_``."""
+    by_backend: dict = {}
+    for gradient in gradients:
+        gradient._ensure_inplace_allowed()
+        if gradient.device.type == "cpu":
+            gradient.zero_()
+            continue
+        by_backend.setdefault(get_backend(gradient), []).append(gradient)
+    for backend, members in by_backend.items():
+        backend.zero_tensors(members)
+        for gradient in members:
+            gradient._pending = None
+            gradient._version_counter.increment()
+
+
+__all__ = ["accumulate_grads", "zero_grads"]

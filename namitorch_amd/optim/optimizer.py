@@ -236,12 +236,13 @@ class Optimizer:
         if type(set_to_none) is not bool:
             raise TypeError("set_to_none must be a Python bool.")
         parameters = self._registered_parameters()
-        with no_grad():
+        if set_to_none:
             for parameter in parameters:
-                if set_to_none:
-                    parameter._grad = None
-                elif parameter.grad is not None:
-                    parameter.grad.zero_()
+                parameter._grad = None
+            return
+        from ..grads import zero_grads
+        with no_grad():
+            zero_grads([parameter.grad for parameter in parameters if parameter.grad is not None])
 
     def step(self, closure=None):
         raise RuntimeError("Optimizer subclass must implement step.")

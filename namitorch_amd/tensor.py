@@ -334,6 +334,12 @@ class Tensor:
         self._storage.copy_(converted)
         self._version_counter.increment()
 
+    def _accumulate_grad(self, gradient: "Tensor") -> None:
+        """Add `gradient` (cast to this leaf's dtype) into ``self.grad``, or
+        make it the gradient (tensor.py:443-450); see ``grads.accumulate_grads``."""
+        from .grads import accumulate_grads
+        accumulate_grads([self], [gradient])
+
     def zero_(self) -> "Tensor":
         return self.fill_(0)
 

@@ -7,7 +7,8 @@ operation for operation, used to check the MI355X kernels:
   optim/_common.py:39-73), plus the master-weight / bfloat16 extensions;
 * ``oracle.clip``  — _total_norm and clip_grad_norm_ (optim/clip_grad.py:63-112);
 * ``oracle.scaler`` — GradScaler unscale_/_finite/update (amp.py:114-234);
-* ``oracle.lowp``  — bfloat16 emulation (RNE) on uint16 bit patterns.
+* ``oracle.lowp``  — bfloat16 emulation (RNE) on uint16 bit patterns;
+* ``oracle.grads`` — gradient accumulation (autograd.py:198-205).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker or the timed

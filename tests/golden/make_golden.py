@@ -343,6 +343,40 @@ def schedule_runner_case(nt):
                 scheduler_state=scheduler.state_dict(), steps=10)
 
 
+def accumulate_cases(nt):
+    """autograd.accumulate_gradient (autograd.py:198-205): the incoming
+    gradient cast to the leaf's dtype, added to the stored one in that dtype
+    (or copied when there is none), for leaf dtypes float32/16/64 and incoming
+    float16/32/64, with special values (signed zeros, subnormals, values that
+    overflow float16, inf, NaN)."""
+    from namitorch.autograd import accumulate_gradient
+    rng = np.random.Generator(np.random.PCG64(61))
+    n = 1031
+    specials = np.array([0.0, -0.0, 1e-45, -3e-42, 6e-8, -6e-8, 65504.0, 65520.0, -70000.0, 1e38, 3.4e38,
+                         np.inf, -np.inf, np.nan, 1e-300, 1e300], dtype=np.float64)
+    arrays = {}
+    cases = []
+    for leaf in (np.float32, np.float16, np.float64):
+        for incoming in (np.float16, np.float32, np.float64):
+            key = f"{np.dtype(leaf).name}_{np.dtype(incoming).name}"
+            parent = nt.nn.Parameter(np.zeros(n, dtype=leaf))
+            existing = (rng.standard_normal(n) * 3.0).astype(leaf)
+            values = rng.standard_normal(n) * np.float64(rng.choice([1e-6, 1e-2, 1.0, 1e3], size=n))
+            values[: specials.size] = specials
+            existing[specials.size: 2 * specials.size] = specials.astype(leaf)
+            with np.errstate(over="ignore", invalid="ignore"):
+                gradient = values.astype(incoming)
+                added = accumulate_gradient(parent, gradient, existing.copy())
+                fresh = accumulate_gradient(parent, gradient, None)
+            arrays[f"{key}_existing"] = existing
+            arrays[f"{key}_incoming"] = gradient
+            arrays[f"{key}_added"] = np.asarray(added)
+            arrays[f"{key}_fresh"] = np.asarray(fresh)
+            cases.append(key)
+    np.savez(HERE / "accumulate.npz", **arrays)
+    return cases
+
+
 def serialization_errors(nt, scratch: Path):
     """Exception class names and texts of the archive writer/reader for invalid inputs."""
     from namitorch import serialization as ser
@@ -421,6 +455,7 @@ def main(reference: str) -> None:
         "checkpoint": checkpoint_case(nt),
         "schedulers": scheduler_cases(nt),
         "schedule_runner": schedule_runner_case(nt),
+        "accumulate": accumulate_cases(nt),
     }
     import tempfile
     with tempfile.TemporaryDirectory() as scratch:

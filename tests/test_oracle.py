@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import adam, clip, lowp, scaler
+from oracle import adam, clip, grads, lowp, scaler
 
 GOLDEN_CASES = ["adamw_f32", "adamw_f32_maximize", "adamw_f32_lr0", "adamw_f32_wd0", "adamw_f32_defaults",
                 "adam_f32_coupled", "adamw_f32_bfgrads", "adamw_f32_special", "adamw_f16", "adamw_f64"]
@@ -257,3 +257,35 @@ def test_unscale_oracle_exactness():
     q = scaler.unscale(g.astype(np.float32), odd)
     exact = np.array([float(np.float32(float(x) / odd)) for x in g.astype(np.float32)], dtype=np.float32)
     assert np.array_equal(q, exact)
+
+
+ACCUMULATE_KEYS = [f"{leaf}_{incoming}" for leaf in ("float32", "float16", "float64")
+                   for incoming in ("float16", "float32", "float64")]
+
+
+@pytest.mark.parametrize("key", ACCUMULATE_KEYS)
+def test_accumulate_oracle_matches_reference_golden(golden_dir, key):
+    data = np.load(golden_dir / "accumulate.npz")
+    leaf = key.split("_")[0]
+    added = grads.accumulate(data[f"{key}_existing"], data[f"{key}_incoming"], leaf)
+    fresh = grads.accumulate(None, data[f"{key}_incoming"], leaf)
+    assert added.dtype == data[f"{key}_added"].dtype and fresh.dtype == data[f"{key}_fresh"].dtype
+    assert added.tobytes() == data[f"{key}_added"].tobytes()
+    assert fresh.tobytes() == data[f"{key}_fresh"].tobytes()
+
+
+def test_accumulate_oracle_bf16_against_torch_and_exact_sums():
+    rng = np.random.default_rng(17)
+    existing = lowp.round_bf16((rng.standard_normal(5000) * 10.0).astype(np.float32))
+    incoming = (rng.standard_normal(5000) * np.float32(rng.choice([1e-3, 1.0, 1e3], 5000))).astype(np.float32)
+    got = grads.accumulate(existing, incoming, "bfloat16")
+    # torch: cast the incoming to bfloat16 (RNE), add in float32, round once.
+    t_in = torch.from_numpy(incoming).to(torch.bfloat16).to(torch.float32)
+    want = (torch.from_numpy(existing) + t_in).to(torch.bfloat16).to(torch.float32).numpy()
+    assert got.tobytes() == want.tobytes()
+    # Exponents within 15 of each other: the float32 sum of two bfloat16 values is exact.
+    a = lowp.round_bf16(np.float32([1.5, -3.0, 1024.0]))
+    b = lowp.round_bf16(np.float32([2.0 ** -10, 0.75, -1.0 / 32]))
+    exact = a.astype(np.float64) + b.astype(np.float64)
+    assert np.array_equal((a + b).astype(np.float64), exact)
+    assert grads.accumulate(None, incoming, "bfloat16").tobytes() == t_in.numpy().tobytes()
