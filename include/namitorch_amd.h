@@ -192,6 +192,21 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
                        void *stream, nt_plan **out);
 int32_t nt_plan_destroy(nt_plan *plan);
 
+/*
+ * Replace one pointer column of every descriptor of `plan`: column 0 param,
+ * 1 grad, 2 exp_avg, 3 exp_avg_sq, 4 model_copy; `pointers[n]` with n the
+ * plan's tensor count.  The update is a copy queued on `stream` after the
+ * work already queued there, so kernels launched earlier keep the old
+ * pointers.  Lets one plan serve gradients that are reallocated every step
+ * (Optimizer.zero_grad(set_to_none=True), optim/optimizer.py:197-206, then a
+ * new backward) without rebuilding its tables.  A pointer must keep the
+ * alignment the plan was built with (NT_ERR_VALUE otherwise; build a new
+ * plan then).  Calls on one plan must use one stream.  No reference
+ * counterpart: the reference passes arrays per launch.
+ */
+int32_t nt_plan_set_pointers(nt_plan *plan, int32_t column, const void *const *pointers, int32_t n,
+                             void *stream);
+
 /* Elements, tensors and workgroup tasks in a plan. */
 int32_t nt_plan_info(const nt_plan *plan, uint64_t *numel, int32_t *tensors,
                      int64_t *tasks);

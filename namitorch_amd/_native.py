@@ -133,6 +133,7 @@ SIGNATURES = {
     "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_void_p]),
     "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
     "nt_grad_zero": (c_int32, [c_void_p, c_void_p]),
+    "nt_plan_set_pointers": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_void_p), c_int32, c_void_p]),
     "nt_grad_accumulate": (c_int32, [c_void_p, c_int32, c_void_p]),
     "nt_ctrl_reset": (c_int32, [c_void_p, c_float, c_int32, c_void_p]),
     "nt_ctrl_carry": (c_int32, [c_void_p, c_void_p, c_void_p]),

@@ -432,8 +432,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         gradient._finite_version = counter.value
     if maximum is not None:
         clip_bumps.extend(zip(gradients, map(_VALUE, map(_COUNTER, gradients))))
-    layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
-    plan = backend.plan(backend.grad_rows(gradients), layout)
+    plan = backend.grad_plan(gradients, dtype)
     backend.grad_prepass(plan, None, block.data_ptr(), unscale=amp)
     flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)

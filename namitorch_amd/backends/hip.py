@@ -47,11 +47,12 @@ def _release_plans() -> None:
 class Plan:
     """A multi-tensor plan owned by the library; destroyed with this object."""
 
-    __slots__ = ("handle", "numel", "ntensors", "ntasks", "layout", "__weakref__")
+    __slots__ = ("handle", "numel", "ntensors", "ntasks", "layout", "columns", "__weakref__")
 
     def __init__(self, handle: int, layout: tuple):
         self.handle = handle
         self.layout = layout
+        self.columns: dict = {}       # volatile column -> pointers it currently holds
         numel = ctypes.c_uint64()
         tensors = ctypes.c_int32()
         tasks = ctypes.c_int64()
@@ -162,27 +163,67 @@ class HIPBackend:
         _native.call("nt_stream_synchronize", self.stream())
 
     # ---- plans -----------------------------------------------------------------------------
-    def plan(self, rows: list[tuple], layout: tuple, chunk: int = 0) -> Plan:
-        """Plan for rows of (param, grad, exp_avg, exp_avg_sq, copy, numel, slot)
-        raw pointers (0 = absent); cached by content."""
-        key = (layout, chunk, tuple(rows))
+    def plan(self, rows: list[tuple], layout: tuple, chunk: int = 0, pointers: dict | None = None) -> Plan:
+        """Plan for rows of (param, grad, exp_avg, exp_avg_sq, copy, numel, slot).
+
+        Columns listed in `pointers` ({column: per-row pointers}) are volatile:
+        their entries in `rows` are ignored (pass 0), the cached plan is keyed
+        without them, and a hit whose pointers differ rewrites that column on
+        the device (``nt_plan_set_pointers``, stream-ordered) instead of
+        building a new plan.  Gradients reallocated every step therefore reuse
+        one plan.  Plans are per stream: a column rewrite is ordered only on
+        the stream that queues it."""
+        volatile = () if not pointers else tuple(sorted(pointers))
+        stream = self.stream()
+        key = (layout, chunk, stream, volatile, tuple(rows))
         with self._lock:
             plan = self._plans.get(key)
             if plan is not None:
                 self._plans.move_to_end(key)
-                return plan
-            table = (_native.MtTensor * max(1, len(rows)))()
-            for index, (param, grad, first, second, copy, numel, slot) in enumerate(rows):
+                if volatile and not self._refresh(plan, pointers, stream):
+                    plan = None
+                if plan is not None:
+                    return plan
+            full = rows
+            if volatile:
+                full = [tuple(pointers[c][i] if c in pointers else value for c, value in enumerate(row))
+                        for i, row in enumerate(rows)]
+            table = (_native.MtTensor * max(1, len(full)))()
+            for index, (param, grad, first, second, copy, numel, slot) in enumerate(full):
                 table[index] = _native.MtTensor(param or None, grad or None, first or None, second or None, copy or None, numel, slot, 0)
             spec = _native.MtLayout(*layout)
             handle = ctypes.c_void_p()
             with self.context():
-                _native.call("nt_plan_create", self.device.index, table, len(rows), ctypes.byref(spec), chunk, self.stream(), ctypes.byref(handle))
+                _native.call("nt_plan_create", self.device.index, table, len(full), ctypes.byref(spec), chunk, stream, ctypes.byref(handle))
             plan = Plan(handle.value, layout)
+            plan.columns = {column: tuple(values) for column, values in (pointers or {}).items()}
             self._plans[key] = plan
+            self._plans.move_to_end(key)
             while len(self._plans) > PLAN_CACHE_SIZE:
                 self._plans.popitem(last=False)
             return plan
+
+    def _refresh(self, plan: Plan, pointers: dict, stream: int) -> bool:
+        """Point the volatile columns of a cached plan at `pointers`; False when
+        a pointer breaks the plan's alignment (the caller builds a new plan)."""
+        for column, values in pointers.items():
+            values = tuple(values)
+            if plan.columns.get(column) == values:
+                continue
+            array = (ctypes.c_void_p * max(1, len(values)))(*values)
+            with self.context():
+                status = _native.load().nt_plan_set_pointers(plan.handle, column, array, len(values), stream)
+            if status == _native.NT_ERR_VALUE:
+                return False
+            _native.check(status)
+            plan.columns[column] = values
+        return True
+
+    def grad_plan(self, tensors, dtype) -> Plan:
+        """Gradient-only plan (the `grad` column volatile)."""
+        layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
+        rows = [(0, 0, 0, 0, 0, tensor._numel, 0) for tensor in tensors]
+        return self.plan(rows, layout, pointers={1: [tensor._ptr for tensor in tensors]})
 
     # ---- multi-tensor kernels --------------------------------------------------------------
     def adamw_multi(self, plan: Plan, slots, xform: _native.GradXform | None) -> None:
@@ -236,17 +277,13 @@ class HIPBackend:
         return out
 
     # ---- single-tensor helpers --------------------------------------------------------------
-    def grad_rows(self, tensors) -> list[tuple]:
-        return [(0, tensor._ptr, 0, 0, 0, tensor.size, 0) for tensor in tensors]
-
     def zero_tensors(self, tensors) -> None:
         """Zero every tensor (one launch per dtype)."""
         by_dtype: dict = {}
         for tensor in tensors:
             by_dtype.setdefault(tensor.dtype, []).append(tensor)
         for dtype, group in by_dtype.items():
-            layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
-            plan = self.plan(self.grad_rows(group), layout)
+            plan = self.grad_plan(group, dtype)
             with self.context():
                 _native.call("nt_grad_zero", plan.handle, self.stream())
 
@@ -258,8 +295,9 @@ class HIPBackend:
             by_dtypes.setdefault((target.dtype, source.dtype), []).append((target, source))
         for (target_dtype, source_dtype), pairs in by_dtypes.items():
             layout = (source_dtype.code, target_dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
-            rows = [(source._ptr, target._ptr, 0, 0, 0, target.size, 0) for target, source in pairs]
-            plan = self.plan(rows, layout)
+            rows = [(0, 0, 0, 0, 0, target._numel, 0) for target, _ in pairs]
+            plan = self.plan(rows, layout, pointers={0: [source._ptr for _, source in pairs],
+                                                     1: [target._ptr for target, _ in pairs]})
             with self.context():
                 _native.call("nt_grad_accumulate", plan.handle, int(assign), self.stream())
 
@@ -269,8 +307,7 @@ class HIPBackend:
         for tensor in tensors:
             by_dtype.setdefault(tensor.dtype, []).append(tensor)
         for dtype, group in by_dtype.items():
-            layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
-            plan = self.plan(self.grad_rows(group), layout)
+            plan = self.grad_plan(group, dtype)
             self.grad_apply(plan, make_xform(transform))
 
     def scale_tensor(self, tensor, scale: float, ctrl: torch.Tensor | None = None):

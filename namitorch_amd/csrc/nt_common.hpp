@@ -7,6 +7,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "../../include/namitorch_amd.h"
@@ -164,7 +165,12 @@ struct alignas(64) DevTensor {
     uint32_t slot;
     uint32_t flags;       // bit 0: every role pointer is 16-byte aligned
 };
+static_assert(sizeof(DevTensor) == 64, "descriptor layout");
+static_assert(offsetof(DevTensor, param) == 0 && offsetof(DevTensor, grad) == 8 && offsetof(DevTensor, exp_avg) == 16 &&
+                  offsetof(DevTensor, exp_avg_sq) == 24 && offsetof(DevTensor, model_copy) == 32,
+              "pointer columns of the descriptor (nt_plan_set_pointers)");
 constexpr uint32_t kAligned16 = 1u;
+constexpr int kRingSlots = 4;        // pinned slots per plan for pointer-column updates
 
 struct Task {
     uint32_t tensor;

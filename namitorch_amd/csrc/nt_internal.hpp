@@ -6,6 +6,8 @@
 
 #include <string>
 
+#include <vector>
+
 #include "nt_common.hpp"
 
 struct nt_plan {
@@ -25,6 +27,14 @@ struct nt_plan {
     nt::Partial *d_partials2;    // [max(nstage2, 1)]
     double *d_pow_partials;      // [pow_grid] (general p-norm)
     void *h_staging;             // pinned host copy of the tables (async upload source)
+    // Pointer-column updates (nt_plan_set_pointers): per-tensor alignment
+    // flags as computed at creation, and a small ring of pinned slots, each
+    // reused only after the copy that read it has completed.
+    std::vector<uint32_t> flags;
+    void *h_ring;                // kRingSlots x ntensors pointers
+    hipEvent_t ring_events[nt::kRingSlots];
+    bool ring_used[nt::kRingSlots];
+    int32_t ring_next;
 };
 
 namespace nt {

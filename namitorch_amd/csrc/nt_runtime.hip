@@ -209,7 +209,13 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     int64_t grid = plan->ntasks < 4096 ? plan->ntasks : 4096;
     plan->pow_grid = (int32_t)(grid > 0 ? grid : 1);
 
+    plan->flags.reserve(host.size());
+    for (const DevTensor &d : host) plan->flags.push_back(d.flags);
+
     auto cleanup = [&](int32_t rc) {
+        for (int r = 0; r < kRingSlots; ++r)
+            if (plan->ring_events[r]) (void)hipEventDestroy(plan->ring_events[r]);
+        if (plan->h_ring) (void)hipHostFree(plan->h_ring);
         if (plan->d_tensors) (void)hipFree(plan->d_tensors);
         if (plan->d_tasks) (void)hipFree(plan->d_tasks);
         if (plan->d_partials) (void)hipFree(plan->d_partials);
@@ -228,6 +234,9 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     if ((rc = hip_check(hipMalloc((void **)&plan->d_partials2, (size_t)(plan->nstage2 > 0 ? plan->nstage2 : 1) * sizeof(Partial)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
     if ((rc = hip_check(hipMalloc((void **)&plan->d_pow_partials, (size_t)plan->pow_grid * sizeof(double)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
     if ((rc = hip_check(hipHostMalloc(&plan->h_staging, tensor_bytes + task_bytes, hipHostMallocDefault), "hipHostMalloc(plan staging)")) != NT_OK) return cleanup(rc);
+    if ((rc = hip_check(hipHostMalloc(&plan->h_ring, (size_t)kRingSlots * host.size() * sizeof(void *), hipHostMallocDefault), "hipHostMalloc(plan ring)")) != NT_OK) return cleanup(rc);
+    for (int r = 0; r < kRingSlots; ++r)
+        if ((rc = hip_check(hipEventCreateWithFlags(&plan->ring_events[r], hipEventDisableTiming), "hipEventCreate(plan ring)")) != NT_OK) return cleanup(rc);
     char *staging = static_cast<char *>(plan->h_staging);
     std::memcpy(staging, host.data(), tensor_bytes);
     if (!tasks.empty()) std::memcpy(staging + tensor_bytes, tasks.data(), tasks.size() * sizeof(Task));
@@ -252,7 +261,47 @@ int32_t nt_plan_destroy(nt_plan *plan) {
     (void)hipFree(plan->d_partials2);
     (void)hipFree(plan->d_pow_partials);
     (void)hipHostFree(plan->h_staging);
+    for (int r = 0; r < kRingSlots; ++r) (void)hipEventDestroy(plan->ring_events[r]);
+    (void)hipHostFree(plan->h_ring);
     delete plan;
+    return NT_OK;
+}
+
+int32_t nt_plan_set_pointers(nt_plan *plan, int32_t column, const void *const *pointers, int32_t n, void *stream) {
+    clear_error();
+    int32_t rc = check_plan(plan);
+    if (rc != NT_OK) return rc;
+    if (column < 0 || column > 4) return fail(NT_ERR_VALUE, "nt_plan_set_pointers: column must be 0..4");
+    if (n != plan->ntensors || (n > 0 && pointers == nullptr))
+        return fail(NT_ERR_VALUE, "nt_plan_set_pointers: one pointer per plan tensor is required");
+    if (n == 0) return NT_OK;
+    const int32_t dtypes[5] = {plan->layout.param_dtype, plan->layout.grad_dtype, plan->layout.state_dtype,
+                               plan->layout.state_dtype, plan->layout.copy_dtype};
+    const size_t size = dtype_size(dtypes[column]);
+    if (size == 0) return fail(NT_ERR_VALUE, "nt_plan_set_pointers: the plan layout has no such column");
+    for (int32_t t = 0; t < n; ++t) {
+        const uintptr_t p = (uintptr_t)pointers[t];
+        if (p == 0) return fail(NT_ERR_VALUE, "nt_plan_set_pointers: pointer " + std::to_string(t) + " is NULL");
+        if (p % size != 0 || ((plan->flags[t] & kAligned16) && p % 16 != 0))
+            return fail(NT_ERR_VALUE, "nt_plan_set_pointers: pointer " + std::to_string(t) +
+                                          " breaks the alignment the plan was built for");
+    }
+    DeviceGuard guard(plan->device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    // The slot's previous upload must have left it before it is rewritten.
+    const int32_t slot = plan->ring_next;
+    plan->ring_next = (slot + 1) % kRingSlots;
+    if (plan->ring_used[slot]) NT_HIP_TRY(hipEventSynchronize(plan->ring_events[slot]), "hipEventSynchronize(plan ring)");
+    const void **ring = static_cast<const void **>(plan->h_ring) + (size_t)slot * n;
+    std::memcpy(ring, pointers, (size_t)n * sizeof(void *));
+    hipStream_t s = (hipStream_t)stream;
+    // Strided copy into column `column` of every descriptor, ordered on the
+    // stream after the kernels already queued with the old pointers.
+    char *dst = reinterpret_cast<char *>(plan->d_tensors) + (size_t)column * sizeof(void *);
+    NT_HIP_TRY(hipMemcpy2DAsync(dst, sizeof(DevTensor), ring, sizeof(void *), sizeof(void *), (size_t)n,
+                                hipMemcpyHostToDevice, s), "hipMemcpy2DAsync(plan pointers)");
+    NT_HIP_TRY(hipEventRecord(plan->ring_events[slot], s), "hipEventRecord(plan ring)");
+    plan->ring_used[slot] = true;
     return NT_OK;
 }
 

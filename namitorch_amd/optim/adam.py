@@ -157,6 +157,10 @@ class Adam(_FirstOrderOptimizer):
     def _fused_decision(self, parameter: Tensor, gradient: Tensor, options: dict, first, second) -> bool:
         """``_use_fused``, memoized on the objects it depends on."""
         fused_option = options.get("fused")
+        if self._master_weights:
+            # Master-weight updates are always supported by the device pass:
+            # the decision depends only on the option and the global switch.
+            return self._use_fused(parameter, gradient, options)
         cache = self.__dict__.setdefault("_fused_checked", {})
         seen = cache.get(id(parameter))
         if (seen is not None and seen[0] is parameter and seen[1]() is gradient and seen[2] is first
@@ -174,6 +178,7 @@ class Adam(_FirstOrderOptimizer):
         rows: list = []
         bookkeeping: list = []
         slot_specs: list = []        # (id(options), step, fused) per coefficient slot
+        grad_pointers: list = []
         member_slots: list = []
         transform = members[0][1]._pending
         for _, gradient, _ in members:
@@ -208,12 +213,13 @@ class Adam(_FirstOrderOptimizer):
                 slot_specs.append((id(options), step, fused))
             member_slots.append(slot)
             if master is not None:
-                rows.append((master._ptr, gradient._ptr, first._ptr, second._ptr, parameter._ptr, parameter._numel, slot))
+                rows.append((master._ptr, 0, first._ptr, second._ptr, parameter._ptr, parameter._numel, slot))
             else:
-                rows.append((parameter._ptr, gradient._ptr, first._ptr, second._ptr, 0, parameter._numel, slot))
+                rows.append((parameter._ptr, 0, first._ptr, second._ptr, 0, parameter._numel, slot))
+            grad_pointers.append(gradient._ptr)
             bookkeeping.append((parameter, state, first, second, master, step, fused, options["lr"] != 0))
         slots = ((_native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs) * len(records))(*records)
-        plan = backend.plan(rows, layout)
+        plan = backend.plan(rows, layout, pointers={1: grad_pointers})
         backend.adamw_multi(plan, slots, None if transform is None else make_xform(transform))
         self._batches.append((backend, plan, compute, slot_specs, member_slots, bookkeeping))
         device_step = None if transform is None else transform.device
@@ -259,6 +265,14 @@ _FIRST = itemgetter("exp_avg")
 _SECOND = itemgetter("exp_avg_sq")
 _MASTER = itemgetter("master")
 _STEP = itemgetter("step")
+_DTYPE = attrgetter("_dtype")
+_PTR = attrgetter("_ptr")
+_SECOND_OF = itemgetter(1)
+_THIRD_OF = itemgetter(2)
+
+
+def _IS_NONE(value) -> bool:
+    return value is None
 
 
 class _Replay:
@@ -283,7 +297,7 @@ class _Replay:
     __slots__ = ("registered_cache", "registered", "requires", "grads", "state", "ids", "dicts", "lens", "firsts",
                  "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
                  "second_counters", "fused_options", "enabled", "validate", "slots", "backend", "plan", "compute",
-                 "record_type", "moment_pairs", "move_counters", "member_groups", "bumped")
+                 "record_type", "moment_pairs", "move_counters", "member_groups", "bumped", "stream")
 
     def __init__(self, optimizer, cached, group_index, backend, plan, compute, slot_specs, member_slots, bookkeeping):
         self.registered_cache = cached
@@ -315,6 +329,7 @@ class _Replay:
         self.validate = tuple((group, parameter) for (_, group), parameter in representatives.items())
         self.backend = backend
         self.plan = plan
+        self.stream = backend.stream()      # the plan's pointer columns are ordered on this stream
         self.compute = compute
         self.record_type = _native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs
         self.bumped = tuple(bool(not entry[6] or entry[0]._numel) for entry in bookkeeping)
@@ -336,7 +351,8 @@ class _Replay:
         registered = self.registered
         if tuple(map(_REQUIRES, registered)) != self.requires:
             return False
-        if not all(map(is_, map(_GRAD, registered), self.grads)):
+        current = tuple(map(_GRAD, registered))
+        if not all(map(is_, current, self.grads)) and not self._adopt(optimizer, current):
             return False
         state = optimizer.state
         if state is not self.state:
@@ -360,7 +376,26 @@ class _Replay:
             return False
         if len(set(map(_PENDING, self.member_grads))) != 1:      # equal transforms, as the full step compares
             return False
-        return fused_kernels_enabled() is self.enabled
+        return fused_kernels_enabled() is self.enabled and self.backend.stream() == self.stream
+
+    def _adopt(self, optimizer, current) -> bool:
+        """New gradient objects for the same parameters (gradients reallocated
+        every step): validate them as the full step does, then re-point the
+        cached plan's gradient column.  Master-weight mode only; elsewhere the
+        fused decision depends on the gradient arrays and the full step runs."""
+        if not self.master_mode or not all(map(is_, map(_IS_NONE, current), map(_IS_NONE, self.grads))):
+            return False
+        entries = list(optimizer._parameters_with_grad())         # raises the full step's errors
+        if len(entries) != len(self.members) or not all(map(is_, map(_SECOND_OF, entries), self.members)):
+            return False
+        grads = tuple(map(_THIRD_OF, entries))
+        if not all(map(is_, map(_DTYPE, grads), map(_DTYPE, self.member_grads))):
+            return False                                        # another storage layout
+        if not self.backend._refresh(self.plan, {1: tuple(map(_PTR, grads))}, self.stream):
+            return False
+        self.grads = current
+        self.member_grads = grads
+        return True
 
     def run(self, optimizer) -> bool:
         if not self._unchanged(optimizer):
@@ -466,6 +501,8 @@ class AdamW(Adam):
         fused = options["fused"]
         if fused is False or (fused is None and not fused_kernels_enabled()):
             return False
+        if self._master_weights:
+            return get_backend(parameter).adamw is not None
         supported = self._fused_decision_supported(parameter, gradient)
         if fused is True and not supported:
             raise RuntimeError("The parameter, gradient or optimizer state does not support fused AdamW.")

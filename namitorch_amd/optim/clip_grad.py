@@ -160,8 +160,7 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
         else:
             transform = next(iter(transforms))
             scale = None if transform is None else transform.scale
-        layout = (-1, dtype.code, -1, -1)
-        plan = backend.plan(backend.grad_rows(members), layout)
+        plan = backend.grad_plan(members, dtype)
         block = backend.new_ctrl()
         backend.grad_prepass(plan, scale)
         backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0)

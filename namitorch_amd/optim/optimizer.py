@@ -224,8 +224,9 @@ class Optimizer:
                     continue
                 if not isinstance(gradient, Tensor):
                     raise TypeError("Parameter gradients must be NamiTorch Tensors.")
-                ensure_same_device(parameter, gradient)
-                if gradient.shape != parameter.shape:
+                if gradient._device is not parameter._device and gradient._device != parameter._device:
+                    ensure_same_device(parameter, gradient)       # raises the device mismatch
+                if gradient._storage.shape != parameter._storage.shape:
                     raise ValueError(f"Gradient shape {gradient.shape} does not match parameter shape {parameter.shape}.")
                 if not self._gradient_dtype_ok(parameter, gradient):
                     raise TypeError(f"Gradient dtype {gradient.dtype} does not match parameter dtype {parameter.dtype}.")

@@ -1,0 +1,87 @@
+"""Multi-tensor plans with gradients reallocated every step: one cached plan
+is re-pointed on the device (nt_plan_set_pointers) instead of rebuilt, and
+the results equal those of gradients kept in place."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import namitorch_amd as nt
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+SHAPES = [(301, 17), (17,), (4099,), (64, 64)]
+
+
+def _setup(seed=3):
+    rng = np.random.default_rng(seed)
+    params = [nt.Parameter((rng.standard_normal(s) * 0.05).astype(np.float32), dtype="bfloat16", device=DEV)
+              for s in SHAPES]
+    optimizer = nt.optim.AdamW(params, lr=1e-3, master_weights=True)
+    return params, optimizer
+
+
+def _grad_values(k):
+    rng = np.random.default_rng(100 + k)
+    return [(rng.standard_normal(s) * 1e-3 * 1024).astype(np.float32) for s in SHAPES]
+
+
+def _run(mode, steps=6):
+    params, optimizer = _setup()
+    scaler = nt.GradScaler(init_scale=1024.0)
+    held = []
+    stable = None
+    for k in range(steps):
+        values = _grad_values(k)
+        if mode == "stable":
+            if stable is None:
+                stable = [nt.Tensor(v, dtype="bfloat16", device=DEV) for v in values]
+                for p, g in zip(params, stable):
+                    p.grad = g
+            else:
+                for g, v in zip(stable, values):
+                    g.copy_(nt.Tensor(v, dtype="bfloat16", device=DEV))
+        else:
+            grads = [nt.Tensor(v, dtype="bfloat16", device=DEV) for v in values]
+            for p, g in zip(params, grads):
+                p.grad = g
+            held.append(grads)                              # old gradients stay alive: new addresses
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        nt.amp.fused_step(optimizer, scaler, max_norm=0.5)
+    state = [optimizer.state[id(p)] for p in params]
+    return ([p.bits().tobytes() for p in params], [s["master"].bits().tobytes() for s in state],
+            [s["exp_avg"].bits().tobytes() for s in state], scaler.get_scale())
+
+
+def test_reallocated_gradients_match_and_reuse_plans():
+    backend = nt.get_backend(DEV)
+    stable = _run("stable")
+    before = len(backend._plans)
+    moving = _run("moving")
+    assert moving == stable
+    # One AdamW plan and one gradient plan serve all steps of the moving run.
+    assert len(backend._plans) <= before + 2
+
+
+def test_alignment_change_builds_a_new_plan():
+    params, optimizer = _setup()
+    base = torch.zeros(sum(int(np.prod(s)) for s in SHAPES) + 64, dtype=torch.bfloat16, device=DEV)
+    for k in range(3):
+        values = _grad_values(k)
+        offset = 8 if k == 0 else 1                         # 16-byte aligned, then 2-byte aligned
+        for p, v in zip(params, values):
+            n = v.size
+            view = base[offset: offset + n].view(p.shape)
+            view.copy_(torch.from_numpy(v).to(torch.bfloat16))
+            p.grad = nt.Tensor._from_storage(view)
+            offset += n
+        optimizer.step()
+    reference_params, reference_optimizer = _setup()
+    for k in range(3):
+        for p, v in zip(reference_params, _grad_values(k)):
+            p.grad = nt.Tensor(v, dtype="bfloat16", device=DEV)
+        reference_optimizer.step()
+    assert [p.bits().tobytes() for p in params] == [p.bits().tobytes() for p in reference_params]
