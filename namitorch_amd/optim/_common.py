@@ -27,7 +27,7 @@ import numpy as np
 import torch
 
 from ..backends import ensure_same_device, get_backend
-from ..dtype import DType, float32, from_numpy_dtype, from_torch_dtype
+from ..dtype import DType, from_numpy_dtype, from_torch_dtype
 from ..tensor import Tensor, enable_grad, no_grad
 from .optimizer import Optimizer
 

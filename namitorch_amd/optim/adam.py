@@ -32,7 +32,7 @@ from ..backends import get_backend
 from ..backends._settings import fused_kernels_enabled
 from ..backends.hip import make_xform
 from ..dtype import DType, bfloat16, float16, float32, float64, normalize_dtype
-from ..tensor import GradTransform, Tensor
+from ..tensor import Tensor
 from ._common import _FirstOrderOptimizer, _real_option, _round_scalar
 
 _LOW_PRECISION = (float16, bfloat16, float32)

@@ -19,16 +19,14 @@ the next kernel that reads them.
 
 from __future__ import annotations
 
-from operator import attrgetter
-
 import math
 from numbers import Real
+from operator import attrgetter
 
 import numpy as np
 import torch
 
 from ..backends import ensure_same_device, get_backend
-from ..dtype import float64
 from ..tensor import GradTransform, Tensor, no_grad
 
 _NORM_EPS = 1e-6

@@ -37,7 +37,6 @@ from .dtype import (
     bfloat16,
     float16,
     float32,
-    float64,
     from_numpy_dtype,
     from_torch_dtype,
     int64,
