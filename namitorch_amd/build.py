@@ -1,6 +1,7 @@
 """Build recipe of the gfx950 shared library ``libnamitorch_amd.so``.
 
-One ``hipcc`` invocation compiles every ``csrc/*.hip`` file for gfx950 and
+One ``hipcc`` invocation compiles every ``csrc/*.hip`` file for gfx950 (and the
+host-only ``csrc/*.cpp``) and
 links them into ``namitorch_amd/_lib/libnamitorch_amd.so`` (in-tree, so the
 built library travels with the source tree).  The flags fix the numerics the
 kernels rely on:
@@ -46,7 +47,8 @@ def hipcc() -> str:
 
 
 def sources() -> list[Path]:
-    return sorted(SOURCE_DIR.glob("*.hip"))
+    """The HIP sources plus the plain C++ plan-table builder."""
+    return sorted(SOURCE_DIR.glob("*.hip")) + sorted(SOURCE_DIR.glob("*.cpp"))
 
 
 def command(output: Path = LIB_PATH) -> list[str]:

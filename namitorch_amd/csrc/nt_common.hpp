@@ -11,6 +11,7 @@
 #include <stdint.h>
 
 #include "../../include/namitorch_amd.h"
+#include "nt_layout.hpp"
 
 namespace nt {
 
@@ -154,28 +155,9 @@ __device__ __forceinline__ void store1(typename T::raw *base, uint64_t i, float 
     base[i] = T::from_f32(v);
 }
 
-// ---- device descriptor / task tables ---------------------------------------------
-struct alignas(64) DevTensor {
-    void *param;
-    void *grad;
-    void *exp_avg;
-    void *exp_avg_sq;
-    void *model_copy;
-    uint64_t numel;
-    uint32_t slot;
-    uint32_t flags;       // bit 0: every role pointer is 16-byte aligned
-};
-static_assert(sizeof(DevTensor) == 64, "descriptor layout");
-static_assert(offsetof(DevTensor, param) == 0 && offsetof(DevTensor, grad) == 8 && offsetof(DevTensor, exp_avg) == 16 &&
-                  offsetof(DevTensor, exp_avg_sq) == 24 && offsetof(DevTensor, model_copy) == 32,
-              "pointer columns of the descriptor (nt_plan_set_pointers)");
-constexpr uint32_t kAligned16 = 1u;
+// ---- device descriptor / task tables: nt_layout.hpp ------------------------------
 constexpr int kRingSlots = 4;        // pinned slots per plan for pointer-column updates
-
-struct Task {
-    uint32_t tensor;
-    uint32_t chunk;
-};
+static_assert(kTile == kChunkQuantum, "plan chunks are whole workgroup tiles");
 
 // Per-workgroup partial of the grad pre-pass: float64 sum of squares of the
 // finite (unscaled) grads and max |g| as a double that is +inf when some

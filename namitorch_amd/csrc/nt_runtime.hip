@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "nt_internal.hpp"
+#include "nt_tables.hpp"
 
 namespace nt {
 
@@ -69,20 +70,6 @@ int32_t check_plan(const nt_plan *plan) {
     return NT_OK;
 }
 
-static bool valid_dtype(int32_t d, bool allow_none) {
-    return (allow_none && d == NT_DTYPE_NONE) || d == NT_F32 || d == NT_F16 || d == NT_BF16 || d == NT_F64;
-}
-
-static size_t dtype_size(int32_t d) {
-    switch (d) {
-        case NT_F32: return 4;
-        case NT_F16:
-        case NT_BF16: return 2;
-        case NT_F64: return 8;
-        default: return 0;
-    }
-}
-
 }  // namespace nt
 
 using namespace nt;
@@ -143,55 +130,15 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     clear_error();
     if (out == nullptr) return fail(NT_ERR_VALUE, "plan output pointer is NULL");
     *out = nullptr;
-    if (layout == nullptr) return fail(NT_ERR_VALUE, "plan layout is NULL");
-    if (n < 0 || (n > 0 && tensors == nullptr)) return fail(NT_ERR_VALUE, "plan tensor table is invalid");
-    if (!valid_dtype(layout->param_dtype, true) || !valid_dtype(layout->grad_dtype, false) ||
-        !valid_dtype(layout->state_dtype, true) || !valid_dtype(layout->copy_dtype, true))
-        return fail(NT_ERR_TYPE, "plan layout names an unsupported dtype code");
-    if (chunk == 0) chunk = 4096;
-    const int64_t quantum = (int64_t)kTile;
-    if (chunk < quantum || chunk % quantum != 0 || chunk > (int64_t)1 << 30)
-        return fail(NT_ERR_VALUE, "plan chunk must be a positive multiple of 2048 elements, at most 2**30");
-
-    std::vector<DevTensor> host(n > 0 ? (size_t)n : 1);
-    std::vector<Task> tasks;
-    uint64_t total = 0;
-    uint32_t max_slot = 0;
-    const size_t gsz = dtype_size(layout->grad_dtype);
-    const size_t psz = dtype_size(layout->param_dtype);
-    const size_t ssz = dtype_size(layout->state_dtype);
-    const size_t csz = dtype_size(layout->copy_dtype);
-    for (int32_t t = 0; t < n; ++t) {
-        const nt_mt_tensor &s = tensors[t];
-        if (s.grad == nullptr && s.numel > 0) return fail(NT_ERR_VALUE, "plan tensor " + std::to_string(t) + " has no gradient");
-        if (s.slot >= NT_MAX_SLOTS) return fail(NT_ERR_VALUE, "plan tensor " + std::to_string(t) + " selects a coefficient slot >= 16");
-        DevTensor d{};
-        d.param = s.param;
-        d.grad = s.grad;
-        d.exp_avg = s.exp_avg;
-        d.exp_avg_sq = s.exp_avg_sq;
-        d.model_copy = s.model_copy;
-        d.numel = s.numel;
-        d.slot = s.slot;
-        if (s.slot > max_slot) max_slot = s.slot;
-        bool aligned = true;
-        const void *ptrs[5] = {s.param, s.grad, s.exp_avg, s.exp_avg_sq, s.model_copy};
-        const size_t sizes[5] = {psz, gsz, ssz, ssz, csz};
-        for (int r = 0; r < 5; ++r) {
-            if (ptrs[r] == nullptr) continue;
-            uintptr_t p = (uintptr_t)ptrs[r];
-            if (p % 16 != 0) aligned = false;
-            if (sizes[r] != 0 && p % sizes[r] != 0)
-                return fail(NT_ERR_VALUE, "plan tensor " + std::to_string(t) + " has a pointer not aligned to its dtype");
-        }
-        d.flags = aligned ? kAligned16 : 0u;
-        host[t] = d;
-        total += s.numel;
-        uint64_t nchunks = (s.numel + (uint64_t)chunk - 1) / (uint64_t)chunk;
-        if (nchunks > 0xffffffffull) return fail(NT_ERR_VALUE, "tensor too large for the task map");
-        for (uint64_t c = 0; c < nchunks; ++c) tasks.push_back(Task{(uint32_t)t, (uint32_t)c});
-    }
-    if (tasks.size() > 0x7fffffffull) return fail(NT_ERR_VALUE, "too many workgroup tasks");
+    PlanTables tables;
+    std::string error;
+    int32_t built = build_plan_tables(tensors, n, layout, chunk, tables, error);
+    if (built != NT_OK) return fail(built, error);
+    const std::vector<DevTensor> &host = tables.tensors;
+    const std::vector<Task> &tasks = tables.tasks;
+    const uint64_t total = tables.numel;
+    const uint32_t max_slot = tables.max_slot;
+    chunk = tables.chunk;
 
     DeviceGuard guard(device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
@@ -209,8 +156,8 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     int64_t grid = plan->ntasks < 4096 ? plan->ntasks : 4096;
     plan->pow_grid = (int32_t)(grid > 0 ? grid : 1);
 
-    plan->flags.reserve(host.size());
-    for (const DevTensor &d : host) plan->flags.push_back(d.flags);
+    plan->flags.reserve((size_t)n);
+    for (int32_t t = 0; t < n; ++t) plan->flags.push_back(host[(size_t)t].flags);
 
     auto cleanup = [&](int32_t rc) {
         for (int r = 0; r < kRingSlots; ++r)
@@ -271,21 +218,10 @@ int32_t nt_plan_set_pointers(nt_plan *plan, int32_t column, const void *const *p
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
-    if (column < 0 || column > 4) return fail(NT_ERR_VALUE, "nt_plan_set_pointers: column must be 0..4");
-    if (n != plan->ntensors || (n > 0 && pointers == nullptr))
-        return fail(NT_ERR_VALUE, "nt_plan_set_pointers: one pointer per plan tensor is required");
-    if (n == 0) return NT_OK;
-    const int32_t dtypes[5] = {plan->layout.param_dtype, plan->layout.grad_dtype, plan->layout.state_dtype,
-                               plan->layout.state_dtype, plan->layout.copy_dtype};
-    const size_t size = dtype_size(dtypes[column]);
-    if (size == 0) return fail(NT_ERR_VALUE, "nt_plan_set_pointers: the plan layout has no such column");
-    for (int32_t t = 0; t < n; ++t) {
-        const uintptr_t p = (uintptr_t)pointers[t];
-        if (p == 0) return fail(NT_ERR_VALUE, "nt_plan_set_pointers: pointer " + std::to_string(t) + " is NULL");
-        if (p % size != 0 || ((plan->flags[t] & kAligned16) && p % 16 != 0))
-            return fail(NT_ERR_VALUE, "nt_plan_set_pointers: pointer " + std::to_string(t) +
-                                          " breaks the alignment the plan was built for");
-    }
+    if (n == 0 && plan->ntensors == 0) return NT_OK;
+    std::string error;
+    rc = check_pointer_column(plan->layout, plan->flags, column, pointers, n, error);
+    if (rc != NT_OK) return fail(rc, error);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     // The slot's previous upload must have left it before it is rewritten.

@@ -1,0 +1,28 @@
+"""Host unit test of the C++ plan-table builder, compiled with g++ under
+AddressSanitizer and UndefinedBehaviorSanitizer (no GPU involved)."""
+
+from __future__ import annotations
+
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ is not installed")
+def test_plan_tables_under_sanitizers(tmp_path):
+    binary = tmp_path / "plan_tables_test"
+    compile_cmd = ["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+                   "-fno-sanitize-recover=undefined", "-Wall", "-Wextra", "-Werror",
+                   str(ROOT / "tests" / "host" / "plan_tables_test.cpp"),
+                   str(ROOT / "namitorch_amd" / "csrc" / "nt_tables.cpp"), "-o", str(binary)]
+    built = subprocess.run(compile_cmd, capture_output=True, text=True)
+    assert built.returncode == 0, built.stderr
+    ran = subprocess.run([str(binary)], capture_output=True, text=True, timeout=60,
+                         env={"ASAN_OPTIONS": "detect_leaks=1", "UBSAN_OPTIONS": "print_stacktrace=1"})
+    assert ran.returncode == 0, ran.stdout + ran.stderr
+    assert "all checks passed" in ran.stdout
+    assert "runtime error" not in ran.stderr and "AddressSanitizer" not in ran.stderr
