@@ -180,7 +180,7 @@ class HIPBackend:
             plan = self._plans.get(key)
             if plan is not None:
                 self._plans.move_to_end(key)
-                if volatile and not self._refresh(plan, pointers, stream):
+                if volatile and not self._refresh_locked(plan, pointers, stream):
                     plan = None
                 if plan is not None:
                     return plan
@@ -206,6 +206,10 @@ class HIPBackend:
     def _refresh(self, plan: Plan, pointers: dict, stream: int) -> bool:
         """Point the volatile columns of a cached plan at `pointers`; False when
         a pointer breaks the plan's alignment (the caller builds a new plan)."""
+        with self._lock:
+            return self._refresh_locked(plan, pointers, stream)
+
+    def _refresh_locked(self, plan: Plan, pointers: dict, stream: int) -> bool:
         for column, values in pointers.items():
             values = tuple(values)
             if plan.columns.get(column) == values:
