@@ -85,3 +85,30 @@ def test_alignment_change_builds_a_new_plan():
             p.grad = nt.Tensor(v, dtype="bfloat16", device=DEV)
         reference_optimizer.step()
     assert [p.bits().tobytes() for p in params] == [p.bits().tobytes() for p in reference_params]
+
+
+def test_reallocated_fp32_gradients_through_optimizer_step():
+    """fp32 parameters without master weights: the full step re-points the
+    cached plan; results equal gradients rewritten in place."""
+    rng = np.random.default_rng(4)
+    p0 = [(rng.standard_normal(s) * 0.05).astype(np.float32) for s in SHAPES]
+    values = [[(np.random.default_rng(200 + k).standard_normal(s) * 1e-3).astype(np.float32) for s in SHAPES]
+              for k in range(5)]
+    results = []
+    for mode in ("stable", "moving"):
+        params = [nt.Parameter(v, device=DEV) for v in p0]
+        optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.1)
+        held = []
+        for k in range(5):
+            if mode == "stable" and k > 0:
+                for p, v in zip(params, values[k]):
+                    p.grad.copy_(nt.Tensor(v, device=DEV))
+            else:
+                grads = [nt.Tensor(v, device=DEV) for v in values[k]]
+                held.append(grads)
+                for p, g in zip(params, grads):
+                    p.grad = g
+            optimizer.step()
+        state = [optimizer.state[id(p)] for p in params]
+        results.append(([p.bits().tobytes() for p in params], [s["exp_avg_sq"].bits().tobytes() for s in state]))
+    assert results[0] == results[1]
