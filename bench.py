@@ -241,6 +241,40 @@ def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype
     return result
 
 
+# ---- gradient producer edges ------------------------------------------------------------------------------
+def bench_edges(nt, torch, shapes, steps, warmup):
+    """accumulate_grads (incoming bf16 into stored bf16: 6 B/param) and
+    zero_grad(set_to_none=False) (2 B/param) over a parameter list, each one
+    launch per step; HIP-event timed on the launch stream."""
+    from namitorch_amd.param_lists import total_params
+    n = total_params(shapes)
+    params = make_params(nt, torch, shapes, nt.bfloat16)
+    attach_grads(nt, torch, params, nt.bfloat16)
+    incoming = [nt.Tensor._from_storage(torch.full(p.shape, 2.0 ** -12, dtype=torch.bfloat16, device="cuda"))
+                for p in params]
+    optimizer = nt.optim.AdamW(params, master_weights=True)
+    result = dict(params=n, tensors=len(shapes))
+    for name, bytes_per_param, action in (
+            ("accumulate", 6, lambda: nt.accumulate_grads(params, incoming)),
+            ("zero_grad", 2, lambda: optimizer.zero_grad(set_to_none=False))):
+        for _ in range(warmup):
+            action()
+        start, stop = event_pair(torch)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            action()
+        stop.record()
+        stop.synchronize()
+        ms = start.elapsed_time(stop) / steps
+        result[name] = dict(ms=ms, bytes_per_param=bytes_per_param, GBps=bytes_per_param * n / ms / 1e6,
+                            pct_hbm_peak=100 * bytes_per_param * n / ms / 1e6 / HBM_PEAK_GBPS)
+        log(f"edges {name}: {ms:.3f} ms")
+    del params, incoming, optimizer
+    torch.cuda.empty_cache()
+    return result
+
+
 # ---- CPU baseline ---------------------------------------------------------------------------------------
 def cpu_baseline(min_seconds=10.0, max_steps=40):
     """NumPy oracle AdamW (the reference's NumPy path restated op for op) over
@@ -353,6 +387,9 @@ def main():
                                          grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
                                          bytes_per_param=30, steps=max(5, args.steps // 2), warmup=args.warmup,
                                          modes=("fused",), mask=decay_mask(llama7b_shapes()))
+    if "edges" in wanted:
+        log("gradient edges: accumulate and zero over the gpt-1.3b list (bf16)")
+        extra["grad_edges_gpt1p3b"] = bench_edges(nt, torch, gpt_1p3b_shapes(), max(5, args.steps // 2), args.warmup)
     baseline = None
     if not args.no_cpu:
         log("CPU baseline (NumPy oracle)")
