@@ -18,7 +18,7 @@ from __future__ import annotations
 import ctypes
 import math
 import operator
-from operator import attrgetter, itemgetter
+from operator import attrgetter, eq, is_, itemgetter
 from numbers import Real
 
 import numpy as np
@@ -37,6 +37,8 @@ _DTYPE = attrgetter("_dtype")
 _FLOATING = attrgetter("_floating")
 _FIRST_OF = itemgetter(0)
 _SECOND_OF = itemgetter(1)
+_FINITE_VERSION = attrgetter("_finite_version")
+_VERSION_VALUE = attrgetter("_version_counter.value")
 
 
 class DeviceStep:
@@ -257,15 +259,20 @@ class GradScaler:
         state = {"optimizer": optimizer, "stage": "unscaling", "gradients": gradients, "finite": False}
         self._optimizer_states[identity] = state
         transform = GradTransform(scale=self._scale)
-        for _, gradient in gradients:
-            gradient._ensure_inplace_allowed()
-            if gradient._pending is not None:
-                gradient._materialize()
+        grads = tuple(map(_SECOND_OF, gradients))
+        if (any(map(_REQUIRES, grads)) and is_grad_enabled()) or not all(map(_WRITABLE, grads)):
+            for gradient in grads:
+                gradient._ensure_inplace_allowed()            # raises the matching error
+        if any(map(_PENDING, grads)):
+            for gradient in grads:
+                if gradient._pending is not None:
+                    gradient._materialize()
+        for gradient in grads:
             gradient._pending = transform
-            gradient._version_counter.increment()
+            gradient._version_counter.value += 1
         state["finite"] = self._finite(gradients)
-        for _, gradient in gradients:
-            gradient._finite_version = gradient._version
+        for gradient in grads:
+            gradient._finite_version = gradient._version_counter.value
         state["stage"] = "unscaled"
         return state["finite"]
 
@@ -280,14 +287,13 @@ class GradScaler:
         if state["stage"] != "unscaled":
             raise RuntimeError("step() may be called only once per optimizer before update().")
         current = self._gradients(optimizer)
-        if len(current) != len(state["gradients"]) or any(
-            first[0] is not second[0] or first[1] is not second[1] for first, second in zip(current, state["gradients"])
-        ):
+        previous = state["gradients"]
+        grads = tuple(map(_SECOND_OF, current))
+        if len(current) != len(previous) or not (all(map(is_, map(_FIRST_OF, current), map(_FIRST_OF, previous)))
+                                                 and all(map(is_, grads, map(_SECOND_OF, previous)))):
             raise RuntimeError("Optimizer gradients changed after unscale_; clipping must modify the existing gradients in-place.")
-        unchanged = all(
-            gradient._finite_version is not None and gradient._finite_version == gradient._version
-            for _, gradient in current
-        )
+        # Finite as checked by unscale_ unless something else wrote a gradient since.
+        unchanged = all(map(eq, map(_FINITE_VERSION, grads), map(_VERSION_VALUE, grads)))
         now_finite = state["finite"] if unchanged else self._finite(current)
         state["finite"] = now_finite and state["finite"]
         if state["finite"]:
