@@ -1,6 +1,6 @@
 """Optimizer-step benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c1,c3,c4,c5,c4s8,c5s8] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c1,c3,c4,c5,c4s8,c5s8,ceilings] [--no-cpu]
 
 Headline (the JSON line's ``value``): BASELINE config 2 — multi-tensor fp32
 AdamW over the GPT-2-124M parameter list (148 tensors, 124,439,808 params,
@@ -22,6 +22,9 @@ GPT-2, C4 GPT-1.3B bf16 + clip, C5 Llama-7B AMP + clip) are reported under
 ``extra`` with their own B/param accounting, together with one GPU's share
 of an 8-way sharded C4 and C5 step (``c4s8``, ``c5s8``: every tensor split
 into 8 contiguous slices, the local work between the collectives).
+``ceilings`` adds the bandwidth of each fp32 read/write stream mix under the
+pass's access pattern (``nt_stream_probe``); ``roofline.frac_of_mix_ceiling``
+is the pass against the probe with its own mix (16 B read, 12 B written).
 """
 
 from __future__ import annotations
@@ -51,7 +54,7 @@ def parse_args():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="c2,c1,c3,c4,c5,c4s8,c5s8")
+    parser.add_argument("--configs", default="c2,c1,c3,c4,c5,c4s8,c5s8,ceilings")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-only", action="store_true", help="only the C2 kernel loop (for profilers)")
     parser.add_argument("--calibrate", action="store_true",
@@ -275,6 +278,48 @@ def bench_edges(nt, torch, shapes, steps, warmup):
     return result
 
 
+# ---- streaming ceilings ---------------------------------------------------------------------------------
+PROBE_MIXES = ((1, 0), (4, 0), (0, 1), (0, 3), (1, 1), (2, 2), (4, 3), (5, 4))
+
+
+def bench_ceilings(nt, torch, steps, warmup, count=30376 * 4096):
+    """The bandwidth each fp32 read/write stream mix reaches with the pass's
+    access pattern (nt_stream_probe), over streams of `count` elements (the
+    C2 parameter count rounded down to 4096).  (4, 3) is the fp32 AdamW
+    pass's mix (16 B read, 12 B written per parameter), (1, 1) and (2, 2) the
+    equal mixes of the C4/C5 passes, (4, 0) a multi-stream read like the
+    pre-pass.  HIP-event timed on the launch stream."""
+    import ctypes
+    from namitorch_amd import _native
+    streams = [torch.ones(count, dtype=torch.float32, device="cuda") for _ in range(max(r + w for r, w in PROBE_MIXES))]
+    handle = torch.cuda.current_stream().cuda_stream
+    result = {"elements_per_stream": count}
+    for reads, writes in PROBE_MIXES:
+        read_ptrs = (ctypes.c_void_p * 8)(*[t.data_ptr() for t in streams[:reads]])
+        write_list = streams[reads:reads + writes] if writes else streams[-1:]
+        write_ptrs = (ctypes.c_void_p * 8)(*[t.data_ptr() for t in write_list])
+
+        def launch():
+            _native.call("nt_stream_probe", read_ptrs, reads, write_ptrs, writes, count, handle)
+
+        for _ in range(warmup):
+            launch()
+        start, stop = event_pair(torch)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            launch()
+        stop.record()
+        stop.synchronize()
+        ms = start.elapsed_time(stop) / steps
+        gbps = 4 * (reads + writes) * count / ms / 1e6
+        result[f"r{reads}w{writes}"] = dict(ms=ms, GBps=gbps, pct_hbm_peak=100 * gbps / HBM_PEAK_GBPS)
+        log(f"probe r{reads}w{writes}: {gbps:.0f} GB/s")
+    del streams
+    torch.cuda.empty_cache()
+    return result
+
+
 # ---- CPU baseline ---------------------------------------------------------------------------------------
 def cpu_baseline(min_seconds=10.0, max_steps=40):
     """NumPy oracle AdamW (the reference's NumPy path restated op for op) over
@@ -390,6 +435,11 @@ def main():
     if "edges" in wanted:
         log("gradient edges: accumulate and zero over the gpt-1.3b list (bf16)")
         extra["grad_edges_gpt1p3b"] = bench_edges(nt, torch, gpt_1p3b_shapes(), max(5, args.steps // 2), args.warmup)
+    ceilings = None
+    if "ceilings" in wanted:
+        log("streaming ceilings of the read/write mixes (nt_stream_probe)")
+        ceilings = bench_ceilings(nt, torch, max(10, args.steps // 2), args.warmup)
+        extra["stream_ceilings"] = ceilings
     baseline = None
     if not args.no_cpu:
         log("CPU baseline (NumPy oracle)")
@@ -416,7 +466,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": pmc_traffic(),
                      "kernel": "nt::adamw_mt_kernel<TF32,TF32,TF32,TNone,RoundF32,false>",
-                     "kernel_ms": c2["kernel_ms"]},
+                     "kernel_ms": c2["kernel_ms"],
+                     "mix_ceiling_GBps": ceilings["r4w3"]["GBps"] if ceilings else None,
+                     "frac_of_mix_ceiling": achieved / ceilings["r4w3"]["GBps"] if ceilings else None},
         "cpu_baseline": baseline,
         "extra": extra,
     }

@@ -319,6 +319,24 @@ int32_t nt_scale_array(const void *in, void *out, int32_t dtype,
 int32_t nt_any_negative(const void *array, int32_t dtype, uint64_t count,
                         int32_t *flag, void *stream);
 
+/* ---- measurement ------------------------------------------------------- */
+
+/*
+ * Streaming probe, no counterpart in the reference: a measurement aid for
+ * benchmarks.  It moves `count` fp32 elements through `nreads` read and
+ * `nwrites` write streams with the pass's access pattern (4096-element
+ * workgroups, four 16-byte nontemporal groups per lane, reads before
+ * writes) and one add per written element, so its bandwidth is the ceiling
+ * of that read/write mix on the device.  Supported (nreads, nwrites):
+ * (0,1) (0,3) (1,0) (1,1) (2,2) (4,0) (4,3) (5,4).  `count` is a positive
+ * multiple of 4096 and every stream holds `count` floats, 16-byte aligned;
+ * a read-only probe passes one write stream that is written only if the
+ * sum of the reads has one particular NaN bit pattern.
+ */
+int32_t nt_stream_probe(const float *const *reads, int32_t nreads,
+                        float *const *writes, int32_t nwrites,
+                        uint64_t count, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
