@@ -81,13 +81,16 @@ extern "C" {
 int32_t nt_stream_probe(const float *const *reads, int32_t nreads, float *const *writes, int32_t nwrites,
                         uint64_t count, void *stream) {
     clear_error();
-    ProbeLauncher launcher = probe_launcher(nreads, nwrites);
+    const bool in_range = nreads >= 0 && nreads < kProbeMax && nwrites >= 0 && nwrites < kProbeMax;
+    ProbeLauncher launcher = in_range ? probe_launcher(nreads, nwrites) : nullptr;
     if (launcher == nullptr)
         return fail(NT_ERR_VALUE, "nt_stream_probe: supported (reads, writes): (0,1) (0,3) (1,0) (1,1) (2,2) (4,0) (4,3) (5,4)");
     if (count == 0 || count % (uint64_t)kProbeChunk != 0)
         return fail(NT_ERR_VALUE, "nt_stream_probe: count must be a positive multiple of 4096");
     if (count / (uint64_t)kProbeChunk > 0x7fffffffull) return fail(NT_ERR_VALUE, "nt_stream_probe: count too large");
-    if (nwrites == 0 && (writes == nullptr || writes[0] == nullptr || (uintptr_t)writes[0] % 16 != 0))
+    if ((nreads > 0 && reads == nullptr) || writes == nullptr)
+        return fail(NT_ERR_VALUE, "nt_stream_probe: NULL stream table");
+    if (nwrites == 0 && (writes[0] == nullptr || (uintptr_t)writes[0] % 16 != 0))
         return fail(NT_ERR_VALUE, "nt_stream_probe: a read-only probe needs one 16-byte aligned write stream");
     ProbeArgs args{};
     for (int32_t r = 0; r < nreads; ++r) {

@@ -63,5 +63,11 @@ def test_probe_rejects_bad_arguments():
         _probe([a], [b], count=0)
     with pytest.raises(ValueError, match="aligned"):
         _probe([a[1:]], [b])
+    stream = torch.cuda.current_stream().cuda_stream
+    for nreads, nwrites in ((-1, 17), (8, 0), (0, 8), (2, -1)):          # out of range, or aliases of a mix
+        with pytest.raises(ValueError, match="supported"):
+            _native.call("nt_stream_probe", _pointers([a]), nreads, _pointers([b]), nwrites, COUNT, stream)
+    with pytest.raises(ValueError, match="NULL"):
+        _native.call("nt_stream_probe", None, 1, _pointers([b]), 1, COUNT, stream)
     torch.cuda.synchronize()
     assert torch.all(b == 1.0)
