@@ -293,6 +293,32 @@ static int32_t dispatch_state(nt_plan *plan, const MtArgs &args, hipStream_t str
     }
 }
 
+// The dtype combinations the pass is built for, checked before anything is
+// launched (also for an empty plan, so a bad layout fails the same way for
+// every parameter list).
+static int32_t check_mt_layout(const nt_mt_layout &L) {
+    if (L.param_dtype == NT_DTYPE_NONE) return fail(NT_ERR_VALUE, "nt_adamw_mt: plan has no parameters");
+    if (L.param_dtype == NT_F64) {
+        if (L.grad_dtype != NT_F64 || L.state_dtype != NT_F64 || L.copy_dtype != NT_DTYPE_NONE)
+            return fail(NT_ERR_TYPE, "float64 AdamW requires float64 grads and states");
+        return NT_OK;
+    }
+    if (L.param_dtype == NT_F16) {
+        // float16 parameters: NumPy float16 arithmetic, states and grads float16.
+        if (L.grad_dtype != NT_F16 || L.state_dtype != NT_F16 || L.copy_dtype != NT_DTYPE_NONE)
+            return fail(NT_ERR_TYPE, "float16 AdamW requires float16 grads and states");
+        return NT_OK;
+    }
+    if (L.param_dtype != NT_F32) return fail(NT_ERR_TYPE, "unsupported parameter dtype");
+    if (L.grad_dtype != NT_F32 && L.grad_dtype != NT_F16 && L.grad_dtype != NT_BF16)
+        return fail(NT_ERR_TYPE, "unsupported gradient dtype for fp32 AdamW");
+    if (L.state_dtype != NT_F32 && L.state_dtype != NT_BF16)
+        return fail(NT_ERR_TYPE, "unsupported optimizer-state dtype for fp32 AdamW");
+    if (L.copy_dtype != NT_DTYPE_NONE && L.copy_dtype != NT_BF16 && L.copy_dtype != NT_F16 && L.copy_dtype != NT_F32)
+        return fail(NT_ERR_TYPE, "unsupported model-copy dtype for fp32 AdamW");
+    return NT_OK;
+}
+
 }  // namespace nt
 
 using namespace nt;
@@ -328,16 +354,14 @@ int32_t nt_adamw_mt(nt_plan *plan, const void *slots, int32_t nslots, const nt_g
     if ((uint32_t)nslots <= plan->max_slot)
         return fail(NT_ERR_VALUE, "nt_adamw_mt: the plan selects coefficient slot " + std::to_string(plan->max_slot) +
                                       " but only " + std::to_string(nslots) + " slots were given");
-    if (plan->ntasks == 0) return NT_OK;
     const nt_mt_layout &L = plan->layout;
-    if (L.param_dtype == NT_DTYPE_NONE) return fail(NT_ERR_VALUE, "nt_adamw_mt: plan has no parameters");
+    if ((rc = check_mt_layout(L)) != NT_OK) return rc;
+    if (plan->ntasks == 0) return NT_OK;
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
 
     if (L.param_dtype == NT_F64) {
-        if (L.grad_dtype != NT_F64 || L.state_dtype != NT_F64 || L.copy_dtype != NT_DTYPE_NONE)
-            return fail(NT_ERR_TYPE, "float64 AdamW requires float64 grads and states");
         MtArgs64 a{};
         const nt_adamw_coefs64 *src = static_cast<const nt_adamw_coefs64 *>(slots);
         for (int i = 0; i < nslots; ++i) a.slots[i] = src[i];
@@ -358,13 +382,7 @@ int32_t nt_adamw_mt(nt_plan *plan, const void *slots, int32_t nslots, const nt_g
     a.honor_skip = xform ? xform->honor_skip : 0;
     a.chunk = plan->chunk;
 
-    if (L.param_dtype == NT_F16) {
-        // float16 parameters: NumPy float16 arithmetic, states and grads float16.
-        if (L.grad_dtype != NT_F16 || L.state_dtype != NT_F16 || L.copy_dtype != NT_DTYPE_NONE)
-            return fail(NT_ERR_TYPE, "float16 AdamW requires float16 grads and states");
-        return launch_mt<TF16, TF16, TF16, TNone, RoundF16, false>(plan, a, s);
-    }
-    if (L.param_dtype != NT_F32) return fail(NT_ERR_TYPE, "unsupported parameter dtype");
+    if (L.param_dtype == NT_F16) return launch_mt<TF16, TF16, TF16, TNone, RoundF16, false>(plan, a, s);
     switch (L.grad_dtype) {
         case NT_F32: return dispatch_state<TF32>(plan, a, s);
         case NT_F16: return dispatch_state<TF16>(plan, a, s);

@@ -21,6 +21,9 @@ void clear_error() { g_last_error.clear(); }
 
 int32_t hip_check(hipError_t err, const char *what) {
     if (err == hipSuccess) return NT_OK;
+    // Consume the runtime's per-thread last error, so that a later launch
+    // check (hipGetLastError) reports that launch and not this failure.
+    (void)hipGetLastError();
     return fail(NT_ERR_HIP, std::string(what) + ": " + hipGetErrorName(err) + " (" +
                                 hipGetErrorString(err) + ")");
 }
@@ -40,7 +43,8 @@ DeviceGuard::DeviceGuard(int32_t device) {
 
 DeviceGuard::~DeviceGuard() {
     int cur = -1;
-    if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+    if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_ && hipSetDevice(prev_) != hipSuccess)
+        (void)hipGetLastError();
 }
 
 Xform make_xform(const nt_grad_xform *x) {
@@ -170,6 +174,7 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
         if (plan->d_pow_partials) (void)hipFree(plan->d_pow_partials);
         if (plan->h_staging) (void)hipHostFree(plan->h_staging);
         delete plan;
+        (void)hipGetLastError();
         return rc;
     };
     const size_t tensor_bytes = host.size() * sizeof(DevTensor);
@@ -211,6 +216,7 @@ int32_t nt_plan_destroy(nt_plan *plan) {
     for (int r = 0; r < kRingSlots; ++r) (void)hipEventDestroy(plan->ring_events[r]);
     (void)hipHostFree(plan->h_ring);
     delete plan;
+    (void)hipGetLastError();   // teardown is best effort; leave no error for a later launch check
     return NT_OK;
 }
 
