@@ -25,6 +25,7 @@ import numpy as np
 
 from . import _native
 from .backends import get_backend
+from .backends._graph_capture import reject_during_capture
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
 from .tensor import GradTransform, is_grad_enabled
 
@@ -207,6 +208,7 @@ class GradScaler:
         return self._scale if self._enabled else 1.0
 
     def scale(self, loss):
+        reject_during_capture("GradScaler")
         dtype = getattr(loss, "dtype", None)
         if not hasattr(dtype, "can_require_grad") or not dtype.can_require_grad or not hasattr(loss, "_storage"):
             raise TypeError("GradScaler.scale requires a floating NamiTorch Tensor.")
@@ -242,6 +244,7 @@ class GradScaler:
         return stats.finite
 
     def unscale_(self, optimizer):
+        reject_during_capture("GradScaler")
         if not self._enabled:
             return True
         self._reconcile()
@@ -277,6 +280,7 @@ class GradScaler:
         return state["finite"]
 
     def step(self, optimizer):
+        reject_during_capture("GradScaler")
         if not self._enabled:
             optimizer.step()
             return True
@@ -305,6 +309,7 @@ class GradScaler:
         return False
 
     def update(self):
+        reject_during_capture("GradScaler")
         if not self._enabled:
             return
         self._reconcile()
@@ -380,6 +385,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     before the next step computes its coefficients, or at the first read of
     the schedule.
     """
+    reject_during_capture("Optimizer steps")
     if scheduler is not None:
         from .optim.lr_scheduler import LRScheduler
         if not isinstance(scheduler, LRScheduler):

@@ -16,6 +16,7 @@ from __future__ import annotations
 import torch
 
 from .backends import ensure_same_device, get_backend
+from .backends._graph_capture import reject_during_capture
 from .tensor import Tensor
 
 _GRADIENT_DTYPES = ("float16", "bfloat16", "float32", "float64")
@@ -53,12 +54,13 @@ def accumulate_grads(parameters, gradients) -> None:
     gradients = list(gradients)
     if len(parameters) != len(gradients):
         raise ValueError("accumulate_grads needs one gradient per parameter.")
+    reject_during_capture("In-place Tensor updates")
     for parameter, gradient in zip(parameters, gradients):
         if not isinstance(parameter, Tensor):
             raise TypeError("accumulate_grads requires NamiTorch Tensors.")
         _validate_accumulation(parameter, gradient)
         if parameter._grad is not None:
-            parameter._grad._ensure_inplace_allowed()
+            parameter._grad._check_inplace()
     # A leaf listed twice accumulates twice, in order: split into rounds in
     # which every leaf appears once (one launch cannot update a leaf twice).
     rounds: list = []
@@ -105,8 +107,9 @@ def zero_grads(gradients) -> None:
     """``grad.zero_()`` for every gradient: device gradients in one launch
     per (device, dtype); host gradients through ``Tensor.zero_``."""
     by_backend: dict = {}
+    reject_during_capture("In-place Tensor updates")
     for gradient in gradients:
-        gradient._ensure_inplace_allowed()
+        gradient._check_inplace()
         if gradient.device.type == "cpu":
             gradient.zero_()
             continue

@@ -27,6 +27,7 @@ import numpy as np
 import torch
 
 from ..backends import ensure_same_device, get_backend
+from ..backends._graph_capture import reject_during_capture
 from ..dtype import DType, from_numpy_dtype, from_torch_dtype
 from ..tensor import Tensor, enable_grad, no_grad
 from .optimizer import Optimizer
@@ -222,6 +223,7 @@ class _FirstOrderOptimizer(Optimizer):
         checked.add(key)
 
     def step(self, closure=None):
+        reject_during_capture("Optimizer steps")
         if closure is not None and not callable(closure):
             raise TypeError("Optimizer closure must be callable or None.")
         self._reconcile_device_steps()

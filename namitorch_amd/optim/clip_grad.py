@@ -27,6 +27,7 @@ import numpy as np
 import torch
 
 from ..backends import ensure_same_device, get_backend
+from ..backends._graph_capture import reject_during_capture
 from ..tensor import GradTransform, Tensor, no_grad
 
 _NORM_EPS = 1e-6
@@ -186,6 +187,7 @@ def _pow_total(blocks, amax: float, order: float) -> float:
 
 
 def _total_norm(gradients: list[Tensor], norm_type: float) -> float:
+    reject_during_capture("Host Tensor reads")          # the norm comes back to the host
     if not gradients:
         return 0.0
     key = _stats_key(gradients)
@@ -240,9 +242,10 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
     if coefficient < 1:
         _require_writable(gradients)
         clipped: dict = {}      # one shared transform per prior pending transform
+        reject_during_capture("In-place Tensor updates")
         with no_grad():
             for gradient in gradients:
-                gradient._ensure_inplace_allowed()
+                gradient._check_inplace()
                 pending = gradient._pending
                 if pending is not None and pending.clip is not None:
                     gradient._materialize()

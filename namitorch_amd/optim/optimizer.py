@@ -15,6 +15,7 @@ import numpy as np
 import torch
 
 from ..backends import ensure_same_device
+from ..backends._graph_capture import reject_during_capture
 from ..device import Device
 from ..dtype import from_numpy_dtype
 from ..tensor import Parameter, Tensor, no_grad
@@ -345,6 +346,7 @@ class Optimizer:
         self._install_loaded_state(*self._prepare_load_state_dict(state_dict))
 
     def to(self, device):
+        reject_during_capture("Moving optimizer state")
         target = Device(device)
         parameters = {id(parameter): parameter for parameter in self._registered_parameters()}
         if any(parameter.device != target for parameter in parameters.values()):

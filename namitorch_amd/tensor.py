@@ -31,6 +31,7 @@ from numbers import Real
 import numpy as np
 import torch
 
+from .backends._graph_capture import reject_during_capture
 from .device import Device
 from .dtype import (
     DType,
@@ -306,6 +307,12 @@ class Tensor:
 
     # ---- in-place updates (tensor.py:1252-1287) ------------------------------------------
     def _ensure_inplace_allowed(self) -> None:
+        reject_during_capture("In-place Tensor updates")
+        self._check_inplace()
+
+    def _check_inplace(self) -> None:
+        """The per-tensor half of ``_ensure_inplace_allowed``, for loops that
+        have already checked for graph capture once."""
         if self._requires_grad and is_grad_enabled():
             raise RuntimeError("In-place assignment is not allowed on a Tensor with requires_grad=True.")
         if not self._writable:
@@ -352,6 +359,7 @@ class Tensor:
     # ---- conversions ---------------------------------------------------------------------
     def numpy(self) -> np.ndarray:
         """Host copy; bfloat16 is returned as (exact) float32 values."""
+        reject_during_capture("Host Tensor reads")
         storage = self._data
         if self._dtype is bfloat16:
             storage = storage.to(torch.float32)
@@ -359,14 +367,16 @@ class Tensor:
 
     def bits(self) -> np.ndarray:
         """Host copy of the raw bit patterns (uint16 for 16-bit types)."""
+        reject_during_capture("Host Tensor reads")
         storage = self._data
         view = {2: torch.int16, 4: torch.int32, 8: torch.int64, 1: torch.uint8}[self._dtype.itemsize]
         unsigned = {2: np.uint16, 4: np.uint32, 8: np.uint64, 1: np.uint8}[self._dtype.itemsize]
         return storage.view(view).cpu().numpy().view(unsigned).copy()
 
     def item(self):
+        reject_during_capture("Host Tensor reads")
         if self.size != 1:
-            raise ValueError("item() requires a Tensor with exactly one element.")
+            raise ValueError(f"item() requires exactly one element, got {self.size}.")
         return self._data.reshape(()).item()
 
     def detach(self) -> "Tensor":
