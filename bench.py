@@ -22,15 +22,19 @@ GPT-2, C4 GPT-1.3B bf16 + clip, C5 Llama-7B AMP + clip) are reported under
 ``extra`` with their own B/param accounting, together with one GPU's share
 of an 8-way sharded C4 and C5 step (``c4s8``, ``c5s8``: every tensor split
 into 8 contiguous slices, the local work between the collectives).
-``ceilings`` adds the bandwidth of each fp32 read/write stream mix under the
-pass's access pattern (``nt_stream_probe``); ``roofline.frac_of_mix_ceiling``
-is the pass against the probe with its own mix (16 B read, 12 B written).
+``chunks`` (optional) times the pass with 4096- and 2048-element tasks,
+alternately on the same buffers, for the C2-C5 layouts.
+``ceilings`` adds the bandwidth of each read/write stream mix under the
+pass's access pattern (``nt_stream_probe``), the C4/C5 pass mixes included;
+``roofline.frac_of_mix_ceiling`` is the pass against the probe with its own
+mix, in place (16 B read, 12 B written back where they were read).
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import sys
@@ -279,44 +283,140 @@ def bench_edges(nt, torch, shapes, steps, warmup):
 
 
 # ---- streaming ceilings ---------------------------------------------------------------------------------
-PROBE_MIXES = ((1, 0), (4, 0), (0, 1), (0, 3), (1, 1), (2, 2), (4, 3), (5, 4))
+# (name, fp32 reads, 16-bit reads, fp32 writes, 16-bit writes, elements per stream, in-place map).  The
+# in-place map names, per write stream, the read stream it rewrites (None: a separate buffer), as the
+# passes rewrite parameter/master, exp_avg and exp_avg_sq where they read them.
+C2_STREAM = 30376 * 4096          # the C2 parameter count rounded down to 4096
+LARGE_STREAM = 1 << 28            # 1 GiB per fp32 stream: far beyond the 256 MB MALL, like the C4/C5 streams
+PROBE_MIXES = (("r1w0", 1, 0, 0, 0, C2_STREAM, None), ("r4w0", 4, 0, 0, 0, C2_STREAM, None),
+               ("r0w1", 0, 0, 1, 0, C2_STREAM, None), ("r0w3", 0, 0, 3, 0, C2_STREAM, None),
+               ("r1w1", 1, 0, 1, 0, C2_STREAM, None), ("r2w2", 2, 0, 2, 0, C2_STREAM, None),
+               ("r4w3", 4, 0, 3, 0, C2_STREAM, None), ("r5w4", 5, 0, 4, 0, C2_STREAM, None),
+               ("r4w3_inplace", 4, 0, 3, 0, C2_STREAM, (0, 2, 3)),
+               ("r4w3_inplace_large", 4, 0, 3, 0, LARGE_STREAM, (0, 2, 3)),
+               ("c4_pass_mix_large", 1, 3, 1, 3, LARGE_STREAM, None),
+               ("c4_pass_mix_inplace_large", 1, 3, 1, 3, LARGE_STREAM, (0, 2, 3, None)),
+               ("c5_pass_mix_large", 3, 1, 3, 1, LARGE_STREAM, None),
+               ("c5_pass_mix_inplace_large", 3, 1, 3, 1, LARGE_STREAM, (0, 1, 2, None)))
 
 
-def bench_ceilings(nt, torch, steps, warmup, count=30376 * 4096):
-    """The bandwidth each fp32 read/write stream mix reaches with the pass's
-    access pattern (nt_stream_probe), over streams of `count` elements (the
-    C2 parameter count rounded down to 4096).  (4, 3) is the fp32 AdamW
-    pass's mix (16 B read, 12 B written per parameter), (1, 1) and (2, 2) the
-    equal mixes of the C4/C5 passes, (4, 0) a multi-stream read like the
-    pre-pass.  HIP-event timed on the launch stream."""
+def bench_ceilings(nt, torch, steps, warmup):
+    """The bandwidth each read/write stream mix reaches with the pass's
+    access pattern (nt_stream_probe).  r4w3 is the fp32 AdamW pass's mix
+    (16 B read, 12 B written per parameter), run at the C2 size for the
+    headline's comparison; the *_large mixes run 1 GiB fp32 streams like the
+    multi-GB streams of C4/C5: c4_pass_mix is the C4 pass's (fp32 master +
+    bf16 grad/m/v read, fp32 master + bf16 m/v/copy written: 10 B each way)
+    and c5_pass_mix the C3/C5 pass's (fp32 master/m/v + a 16-bit grad read,
+    fp32 master/m/v + a bf16 copy written: 14 B each way); *_inplace
+    variants rewrite the streams they read, as the passes do; r4w0 is a
+    multi-stream read like the pre-pass.  HIP-event timed on the launch
+    stream; every stream is a fresh allocation of this process."""
     import ctypes
     from namitorch_amd import _native
-    streams = [torch.ones(count, dtype=torch.float32, device="cuda") for _ in range(max(r + w for r, w in PROBE_MIXES))]
     handle = torch.cuda.current_stream().cuda_stream
-    result = {"elements_per_stream": count}
-    for reads, writes in PROBE_MIXES:
-        read_ptrs = (ctypes.c_void_p * 8)(*[t.data_ptr() for t in streams[:reads]])
-        write_list = streams[reads:reads + writes] if writes else streams[-1:]
-        write_ptrs = (ctypes.c_void_p * 8)(*[t.data_ptr() for t in write_list])
+    result = {"elements_per_stream": {"C2": C2_STREAM, "large": LARGE_STREAM}}
+    for count in (C2_STREAM, LARGE_STREAM):
+        mixes = [m for m in PROBE_MIXES if m[5] == count]
+        wide = [torch.zeros(count, dtype=torch.float32, device="cuda") for _ in range(max(m[1] + m[3] for m in mixes))]
+        narrow = [torch.zeros(count, dtype=torch.bfloat16, device="cuda") for _ in range(max(m[2] + m[4] for m in mixes))]
+        for name, r32, r16, w32, w16, _, inplace in mixes:
+            reads = wide[:r32] + narrow[:r16]
+            writes = wide[r32:r32 + w32] + narrow[r16:r16 + w16] if w32 + w16 else wide[-1:]
+            if inplace is not None:
+                writes = [reads[source] if source is not None else fresh for source, fresh in zip(inplace, writes)]
+            read_ptrs = (ctypes.c_void_p * 8)(*[t.data_ptr() for t in reads])
+            write_ptrs = (ctypes.c_void_p * 8)(*[t.data_ptr() for t in writes])
+            args = (read_ptrs, r32 + r16, r16, write_ptrs, w32 + w16, w16, count, handle)
+            for _ in range(warmup):
+                _native.call("nt_stream_probe", *args)
+            start, stop = event_pair(torch)
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(steps):
+                _native.call("nt_stream_probe", *args)
+            stop.record()
+            stop.synchronize()
+            ms = start.elapsed_time(stop) / steps
+            gbps = (4 * (r32 + w32) + 2 * (r16 + w16)) * count / ms / 1e6
+            result[name] = dict(ms=ms, GBps=gbps, pct_hbm_peak=100 * gbps / HBM_PEAK_GBPS,
+                                bytes_per_element=dict(read=4 * r32 + 2 * r16, write=4 * w32 + 2 * w16))
+            log(f"probe {name}: {gbps:.0f} GB/s")
+        del wide, narrow
+        torch.cuda.empty_cache()
+    return result
 
-        def launch():
-            _native.call("nt_stream_probe", read_ptrs, reads, write_ptrs, writes, count, handle)
 
-        for _ in range(warmup):
-            launch()
-        start, stop = event_pair(torch)
+# ---- pass task size ---------------------------------------------------------------------------------------
+def bench_chunks(nt, torch, launches=20, reps=4):
+    """The AdamW pass with 4096- and 2048-element tasks, timed alternately in
+    one process on the same buffers (so both see the same physical
+    placement), for each BASELINE layout; the optimizer picks the chunk per
+    layout (optim/adam.py _pass_chunk).  Random N(0, 0.02) params, N(0, 1e-3)
+    grads, zero moments; C4/C5 launches carry their clip (and unscale)
+    transforms, as in their steps."""
+    import ctypes
+    from namitorch_amd import _native
+    from namitorch_amd.param_lists import gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes
+    f32, f16, bf16, none = _native.NT_F32, _native.NT_F16, _native.NT_BF16, _native.NT_DTYPE_NONE
+    torch_dtype = {f32: torch.float32, f16: torch.float16, bf16: torch.bfloat16}
+    size = {f32: 4, f16: 2, bf16: 2, none: 0}
+    configs = (("c2", gpt2_shapes, (f32, f32, f32, none), None),
+               ("c3", gpt2_shapes, (f32, f16, f32, bf16), dict(scale=65536.0, unscale=1, clip_coef=1.0, clip=0)),
+               ("c4", gpt_1p3b_shapes, (f32, bf16, bf16, bf16), dict(scale=1.0, unscale=0, clip_coef=0.5, clip=1)),
+               ("c5", llama7b_shapes, (f32, bf16, f32, bf16), dict(scale=65536.0, unscale=1, clip_coef=0.5, clip=1)))
+    stream = torch.cuda.current_stream().cuda_stream
+    coefs = (_native.AdamWCoefs * 1)(_native.AdamWCoefs(3e-4, 0.9, 0.999, 0.1, 0.001, 1e-8, 0.1, 1 - 3e-5, 0.1, 0.001,
+                                                         0, 1, 0, 0))
+    generator = torch.Generator(device="cuda").manual_seed(7)
+    result = {}
+    for name, shapes_fn, layout, xform in configs:
+        pdt, gdt, sdt, cdt = layout
+        rows, keep = [], []
+        for shape in shapes_fn():
+            n = math.prod(shape)
+            p = (torch.randn(n, generator=generator, device="cuda") * 0.02).to(torch_dtype[pdt])
+            g = (torch.randn(n, generator=generator, device="cuda") * 1e-3).to(torch_dtype[gdt])
+            m = torch.zeros(n, dtype=torch_dtype[sdt], device="cuda")
+            v = torch.zeros(n, dtype=torch_dtype[sdt], device="cuda")
+            c = torch.empty(n, dtype=torch_dtype[cdt], device="cuda") if cdt != none else None
+            keep += [p, g, m, v, c]
+            rows.append(_native.MtTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
+                                         None if c is None else c.data_ptr(), n, 0, 0))
+        table = (_native.MtTensor * len(rows))(*rows)
+        params = sum(row.numel for row in rows)
+        moved = params * (2 * size[pdt] + size[gdt] + 4 * size[sdt] + size[cdt])
+        transform = None if xform is None else ctypes.byref(_native.GradXform(**xform))
+        plans = {}
+        for chunk in (4096, 2048):
+            handle = ctypes.c_void_p()
+            _native.call("nt_plan_create", 0, table, len(rows), ctypes.byref(_native.MtLayout(*layout)), chunk, stream,
+                         ctypes.byref(handle))
+            plans[chunk] = handle
+        times = {chunk: [] for chunk in plans}
+        for _ in range(reps):
+            for chunk, handle in plans.items():
+                for _ in range(2):
+                    _native.call("nt_adamw_mt", handle, coefs, 1, transform, stream)
+                start, stop = event_pair(torch)
+                start.record()
+                for _ in range(launches):
+                    _native.call("nt_adamw_mt", handle, coefs, 1, transform, stream)
+                stop.record()
+                stop.synchronize()
+                times[chunk].append(start.elapsed_time(stop) / launches)
+        entry = {}
+        for chunk, values in times.items():
+            best = min(values)
+            entry[str(chunk)] = dict(best_ms=best, median_ms=sorted(values)[len(values) // 2], GBps=moved / best / 1e6)
+        entry["faster"] = min(plans, key=lambda chunk: min(times[chunk]))
+        result[name] = entry
+        log(f"chunks {name}: 4096 {min(times[4096]):.4f} ms, 2048 {min(times[2048]):.4f} ms")
         torch.cuda.synchronize()
-        start.record()
-        for _ in range(steps):
-            launch()
-        stop.record()
-        stop.synchronize()
-        ms = start.elapsed_time(stop) / steps
-        gbps = 4 * (reads + writes) * count / ms / 1e6
-        result[f"r{reads}w{writes}"] = dict(ms=ms, GBps=gbps, pct_hbm_peak=100 * gbps / HBM_PEAK_GBPS)
-        log(f"probe r{reads}w{writes}: {gbps:.0f} GB/s")
-    del streams
-    torch.cuda.empty_cache()
+        for handle in plans.values():
+            _native.call("nt_plan_destroy", handle)
+        del keep, rows, table
+        torch.cuda.empty_cache()
     return result
 
 
@@ -432,6 +532,9 @@ def main():
                                          grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
                                          bytes_per_param=30, steps=max(5, args.steps // 2), warmup=args.warmup,
                                          modes=("fused",), mask=decay_mask(llama7b_shapes()))
+    if "chunks" in wanted:
+        log("AdamW pass task size: 4096 against 2048 elements, same buffers")
+        extra["pass_chunks"] = bench_chunks(nt, torch)
     if "edges" in wanted:
         log("gradient edges: accumulate and zero over the gpt-1.3b list (bf16)")
         extra["grad_edges_gpt1p3b"] = bench_edges(nt, torch, gpt_1p3b_shapes(), max(5, args.steps // 2), args.warmup)
@@ -467,8 +570,8 @@ def main():
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": pmc_traffic(),
                      "kernel": "nt::adamw_mt_kernel<TF32,TF32,TF32,TNone,RoundF32,false>",
                      "kernel_ms": c2["kernel_ms"],
-                     "mix_ceiling_GBps": ceilings["r4w3"]["GBps"] if ceilings else None,
-                     "frac_of_mix_ceiling": achieved / ceilings["r4w3"]["GBps"] if ceilings else None},
+                     "mix_ceiling_GBps": ceilings["r4w3_inplace"]["GBps"] if ceilings else None,
+                     "frac_of_mix_ceiling": achieved / ceilings["r4w3_inplace"]["GBps"] if ceilings else None},
         "cpu_baseline": baseline,
         "extra": extra,
     }

@@ -323,18 +323,23 @@ int32_t nt_any_negative(const void *array, int32_t dtype, uint64_t count,
 
 /*
  * Streaming probe, no counterpart in the reference: a measurement aid for
- * benchmarks.  It moves `count` fp32 elements through `nreads` read and
+ * benchmarks.  It moves `count` elements through `nreads` read and
  * `nwrites` write streams with the pass's access pattern (4096-element
- * workgroups, four 16-byte nontemporal groups per lane, reads before
- * writes) and one add per written element, so its bandwidth is the ceiling
- * of that read/write mix on the device.  Supported (nreads, nwrites):
- * (0,1) (0,3) (1,0) (1,1) (2,2) (4,0) (4,3) (5,4).  `count` is a positive
- * multiple of 4096 and every stream holds `count` floats, 16-byte aligned;
- * a read-only probe passes one write stream that is written only if the
- * sum of the reads has one particular NaN bit pattern.
+ * workgroups, four nontemporal groups of four elements per lane: 16 bytes
+ * for fp32 streams, 8 bytes for 16-bit streams; reads before writes) and
+ * one add per written element, so its bandwidth is the ceiling of that
+ * read/write mix on the device.  The last `nreads16` read and `nwrites16`
+ * write streams are 16-bit (bfloat16), the others fp32.  Supported
+ * (nreads, nreads16, nwrites, nwrites16): (0,0,1,0) (0,0,3,0) (1,0,0,0)
+ * (1,0,1,0) (2,0,2,0) (4,0,0,0) (4,0,3,0) (5,0,4,0), and the pass mixes
+ * (4,3,4,3) (C4: fp32 master + three bf16 streams each way) and (4,1,4,1)
+ * (C3/C5: three fp32 streams + one 16-bit stream each way).  `count` is a
+ * positive multiple of 4096, every stream holds `count` elements and is
+ * 16-byte aligned; a read-only probe passes one fp32 write stream that is
+ * written only if the sum of the reads has one particular NaN bit pattern.
  */
-int32_t nt_stream_probe(const float *const *reads, int32_t nreads,
-                        float *const *writes, int32_t nwrites,
+int32_t nt_stream_probe(const void *const *reads, int32_t nreads, int32_t nreads16,
+                        void *const *writes, int32_t nwrites, int32_t nwrites16,
                         uint64_t count, void *stream);
 
 #ifdef __cplusplus

@@ -1,13 +1,16 @@
 // nt_probe.hip — streaming probe: the memory access pattern of the
 // multi-tensor AdamW pass with the arithmetic reduced to one add per stream,
-// so that a benchmark can report the bandwidth this access mix reaches on the
-// device next to what the pass reaches.
+// so that a benchmark can report the bandwidth each access mix reaches on
+// the device next to what the pass reaches.
 //
-// Each workgroup covers 4096 consecutive fp32 elements of every stream
-// (like a pass task), each lane four groups of four elements with
-// nontemporal 16-byte accesses: all reads first, then the writes grouped by
-// stream.  Stream w (write) receives read stream w plus read stream R-1, so
-// every read is used and nothing is optimised away.
+// Each workgroup covers 4096 consecutive elements of every stream (like a
+// pass task), each lane four groups of four elements with nontemporal
+// accesses: 16 bytes per group for fp32 streams and 8 bytes for 16-bit
+// streams, as the pass issues them.  All reads come first, then the writes
+// grouped by stream.  Write stream w receives read stream (w mod R) plus
+// read stream R-1 (1.0 when there are no reads), so every read is used and
+// nothing is optimised away; 16-bit streams hold bfloat16 values, read
+// exactly and written truncated to their upper 16 bits.
 #include <hip/hip_runtime.h>
 
 #include "nt_internal.hpp"
@@ -18,26 +21,48 @@ constexpr int kProbeMax = 8;
 constexpr int kProbeChunk = kBlock * kVec * kPass2Unroll;   // 4096 elements
 
 struct ProbeArgs {
-    const float *reads[kProbeMax];
-    float *writes[kProbeMax];
+    const void *reads[kProbeMax];
+    void *writes[kProbeMax];
 };
 
-template <int R, int W>
+__device__ __forceinline__ f32x4 bf16x4_to_f32(u32x2 w) {
+    return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                 __uint_as_float(w.y & 0xffff0000u)};
+}
+
+__device__ __forceinline__ u32x2 f32x4_to_bf16_trunc(f32x4 v) {
+    return u32x2{(__float_as_uint(v.x) >> 16) | (__float_as_uint(v.y) & 0xffff0000u),
+                 (__float_as_uint(v.z) >> 16) | (__float_as_uint(v.w) & 0xffff0000u)};
+}
+
+// R read streams of which the last R16 are 16-bit; W write streams of which
+// the last W16 are 16-bit.
+template <int R, int R16, int W, int W16>
 __global__ __launch_bounds__(kBlock) void stream_probe_kernel(ProbeArgs args) {
+    constexpr int R32 = R - R16, W32 = W - W16;
     const uint64_t start = (uint64_t)blockIdx.x * kProbeChunk + (uint64_t)threadIdx.x * kVec;
     f32x4 in[R > 0 ? R : 1][kPass2Unroll];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int u = 0; u < kPass2Unroll; ++u)
-            in[r][u] = gload<true, f32x4, gf32x4>(args.reads[r] + start + (uint64_t)u * kBlock * kVec);
+        for (int u = 0; u < kPass2Unroll; ++u) {
+            const uint64_t i = start + (uint64_t)u * kBlock * kVec;
+            if (r < R32)
+                in[r][u] = gload<true, f32x4, gf32x4>(static_cast<const float *>(args.reads[r]) + i);
+            else
+                in[r][u] = bf16x4_to_f32(gload<true, u32x2, gu32x2>(static_cast<const uint16_t *>(args.reads[r]) + i));
+        }
 #pragma unroll
     for (int w = 0; w < W; ++w)
 #pragma unroll
         for (int u = 0; u < kPass2Unroll; ++u) {
+            const uint64_t i = start + (uint64_t)u * kBlock * kVec;
             f32x4 value = {1.0f, 1.0f, 1.0f, 1.0f};
             if constexpr (R > 0) value = in[w % R][u] + in[R - 1][u];
-            gstore<true, f32x4, gf32x4>(args.writes[w] + start + (uint64_t)u * kBlock * kVec, value);
+            if (w < W32)
+                gstore<true, f32x4, gf32x4>(static_cast<float *>(args.writes[w]) + i, value);
+            else
+                gstore<true, u32x2, gu32x2>(static_cast<uint16_t *>(args.writes[w]) + i, f32x4_to_bf16_trunc(value));
         }
     if constexpr (W == 0 && R > 0) {
         // Read-only probe: keep the loads alive with a store nobody reads
@@ -47,29 +72,38 @@ __global__ __launch_bounds__(kBlock) void stream_probe_kernel(ProbeArgs args) {
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int u = 0; u < kPass2Unroll; ++u) sum += in[r][u];
-        if (__builtin_bit_cast(uint32_t, sum.x) == 0x7fbadbadu) args.writes[kProbeMax - 1][start] = sum.y;
+        if (__builtin_bit_cast(uint32_t, sum.x) == 0x7fbadbadu)
+            static_cast<float *>(args.writes[kProbeMax - 1])[start] = sum.y;
     }
 }
 
-template <int R, int W>
+template <int R, int R16, int W, int W16>
 static void launch_probe(dim3 grid, hipStream_t s, const ProbeArgs &args) {
-    stream_probe_kernel<R, W><<<grid, dim3(kBlock), 0, s>>>(args);
+    stream_probe_kernel<R, R16, W, W16><<<grid, dim3(kBlock), 0, s>>>(args);
 }
 
 typedef void (*ProbeLauncher)(dim3, hipStream_t, const ProbeArgs &);
 
-static ProbeLauncher probe_launcher(int reads, int writes) {
-    switch (reads * 16 + writes) {
-        case 0 * 16 + 1: return launch_probe<0, 1>;
-        case 0 * 16 + 3: return launch_probe<0, 3>;
-        case 1 * 16 + 0: return launch_probe<1, 0>;
-        case 1 * 16 + 1: return launch_probe<1, 1>;
-        case 2 * 16 + 2: return launch_probe<2, 2>;
-        case 4 * 16 + 0: return launch_probe<4, 0>;
-        case 4 * 16 + 3: return launch_probe<4, 3>;
-        case 5 * 16 + 4: return launch_probe<5, 4>;
-        default: return nullptr;
-    }
+struct ProbeMix {
+    int reads, reads16, writes, writes16;
+    ProbeLauncher launch;
+};
+
+// fp32 mixes, then the C4 pass's mix (fp32 master + three bf16 streams each
+// way) and the C3/C5 pass's mix (three fp32 streams + one 16-bit stream
+// each way).
+static const ProbeMix kMixes[] = {
+    {0, 0, 1, 0, launch_probe<0, 0, 1, 0>}, {0, 0, 3, 0, launch_probe<0, 0, 3, 0>},
+    {1, 0, 0, 0, launch_probe<1, 0, 0, 0>}, {1, 0, 1, 0, launch_probe<1, 0, 1, 0>},
+    {2, 0, 2, 0, launch_probe<2, 0, 2, 0>}, {4, 0, 0, 0, launch_probe<4, 0, 0, 0>},
+    {4, 0, 3, 0, launch_probe<4, 0, 3, 0>}, {5, 0, 4, 0, launch_probe<5, 0, 4, 0>},
+    {4, 3, 4, 3, launch_probe<4, 3, 4, 3>}, {4, 1, 4, 1, launch_probe<4, 1, 4, 1>},
+};
+
+static ProbeLauncher probe_launcher(int reads, int reads16, int writes, int writes16) {
+    for (const ProbeMix &m : kMixes)
+        if (m.reads == reads && m.reads16 == reads16 && m.writes == writes && m.writes16 == writes16) return m.launch;
+    return nullptr;
 }
 
 }  // namespace nt
@@ -78,20 +112,21 @@ using namespace nt;
 
 extern "C" {
 
-int32_t nt_stream_probe(const float *const *reads, int32_t nreads, float *const *writes, int32_t nwrites,
-                        uint64_t count, void *stream) {
+int32_t nt_stream_probe(const void *const *reads, int32_t nreads, int32_t nreads16, void *const *writes,
+                        int32_t nwrites, int32_t nwrites16, uint64_t count, void *stream) {
     clear_error();
-    const bool in_range = nreads >= 0 && nreads < kProbeMax && nwrites >= 0 && nwrites < kProbeMax;
-    ProbeLauncher launcher = in_range ? probe_launcher(nreads, nwrites) : nullptr;
+    ProbeLauncher launcher = probe_launcher(nreads, nreads16, nwrites, nwrites16);
     if (launcher == nullptr)
-        return fail(NT_ERR_VALUE, "nt_stream_probe: supported (reads, writes): (0,1) (0,3) (1,0) (1,1) (2,2) (4,0) (4,3) (5,4)");
+        return fail(NT_ERR_VALUE, "nt_stream_probe: supported (reads, 16-bit reads, writes, 16-bit writes): "
+                                  "(0,0,1,0) (0,0,3,0) (1,0,0,0) (1,0,1,0) (2,0,2,0) (4,0,0,0) (4,0,3,0) "
+                                  "(5,0,4,0) (4,3,4,3) (4,1,4,1)");
     if (count == 0 || count % (uint64_t)kProbeChunk != 0)
         return fail(NT_ERR_VALUE, "nt_stream_probe: count must be a positive multiple of 4096");
     if (count / (uint64_t)kProbeChunk > 0x7fffffffull) return fail(NT_ERR_VALUE, "nt_stream_probe: count too large");
     if ((nreads > 0 && reads == nullptr) || writes == nullptr)
         return fail(NT_ERR_VALUE, "nt_stream_probe: NULL stream table");
     if (nwrites == 0 && (writes[0] == nullptr || (uintptr_t)writes[0] % 16 != 0))
-        return fail(NT_ERR_VALUE, "nt_stream_probe: a read-only probe needs one 16-byte aligned write stream");
+        return fail(NT_ERR_VALUE, "nt_stream_probe: a read-only probe needs one 16-byte aligned fp32 write stream");
     ProbeArgs args{};
     for (int32_t r = 0; r < nreads; ++r) {
         if (reads[r] == nullptr || (uintptr_t)reads[r] % 16 != 0)
