@@ -38,6 +38,7 @@ _DTYPE = attrgetter("_dtype")
 _FLOATING = attrgetter("_floating")
 _FIRST_OF = itemgetter(0)
 _SECOND_OF = itemgetter(1)
+_PARAMETER_AND_GRADIENT = itemgetter(1, 2)
 _FINITE_VERSION = attrgetter("_finite_version")
 _VERSION_VALUE = attrgetter("_version_counter.value")
 
@@ -231,7 +232,9 @@ class GradScaler:
     def _gradients(optimizer):
         if not callable(getattr(optimizer, "_parameters_with_grad", None)) or not callable(getattr(optimizer, "step", None)):
             raise TypeError("GradScaler requires a NamiTorch optimizer.")
-        gradients = tuple((parameter, gradient) for _, parameter, gradient in optimizer._parameters_with_grad())
+        entries = optimizer._grad_entries() if callable(getattr(optimizer, "_grad_entries", None)) \
+            else tuple(optimizer._parameters_with_grad())
+        gradients = tuple(map(_PARAMETER_AND_GRADIENT, entries))
         if any(map(_REQUIRES, map(_SECOND_OF, gradients))) or not all(
                 map(_FLOATING, map(_DTYPE, map(_FIRST_OF, gradients)))):
             raise RuntimeError("GradScaler requires detached floating gradients.")
@@ -257,7 +260,7 @@ class GradScaler:
         if not gradients:
             raise RuntimeError("No gradients were found for this optimizer.")
         previous = {id(parameter) for state in self._optimizer_states.values() for parameter, _ in state["gradients"]}
-        if any(id(parameter) in previous for parameter, _ in gradients):
+        if previous and any(id(parameter) in previous for parameter, _ in gradients):
             raise RuntimeError("Optimizers cannot share gradients in the same GradScaler iteration.")
         state = {"optimizer": optimizer, "stage": "unscaling", "gradients": gradients, "finite": False}
         self._optimizer_states[identity] = state

@@ -237,7 +237,7 @@ class _FirstOrderOptimizer(Optimizer):
                 if replay.run(self):
                     return loss
             self._replay = None
-        entries = list(self._parameters_with_grad())
+        entries = list(self._grad_entries())
         options = {
             id(group): self._prepare_options({key: value for key, value in group.items() if key != "params"}, "param_group")
             for group in self.param_groups

@@ -24,8 +24,11 @@ unrounded float32 values).
 
 from __future__ import annotations
 
+import math
 import weakref
-from operator import attrgetter, eq, is_, itemgetter
+from collections import deque
+from itertools import repeat
+from operator import add, attrgetter, eq, is_, itemgetter, setitem
 
 from .. import _native
 from ..backends import get_backend
@@ -275,6 +278,39 @@ def _IS_NONE(value) -> bool:
     return value is None
 
 
+def _options_key(groups) -> tuple | None:
+    """The option values of every parameter group, exactly: names, types,
+    and values, with floats by their bit pattern.  Two steps with equal keys
+    prepare equal options and pass the same checks.  None (do not memoize)
+    for values whose checks must run every step: non-finite floats, or
+    anything other than scalars and tuples/lists of scalars."""
+    key: list = []
+    for group in groups:
+        for name, value in group.items():
+            if name == "params":
+                continue
+            kind = type(value)
+            if kind is float:
+                if not math.isfinite(value):
+                    return None
+                value = value.hex()
+            elif kind is tuple or kind is list:
+                items = []
+                for item in value:
+                    if type(item) is float and math.isfinite(item):
+                        items.append((float, item.hex()))
+                    elif type(item) in (int, bool):
+                        items.append((type(item), item))
+                    else:
+                        return None
+                value = tuple(items)
+            elif kind not in (int, bool, str, type(None)):
+                return None
+            key.append((name, kind, value))
+        key.append(None)
+    return tuple(key)
+
+
 _SIXTEEN_BIT = (_native.NT_F16, _native.NT_BF16)
 
 
@@ -310,7 +346,8 @@ class _Replay:
     __slots__ = ("registered_cache", "registered", "requires", "grads", "state", "ids", "dicts", "lens", "firsts",
                  "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
                  "second_counters", "fused_options", "enabled", "validate", "slots", "backend", "plan", "compute",
-                 "record_type", "moment_pairs", "move_counters", "member_groups", "bumped", "stream")
+                 "record_type", "moment_pairs", "move_counters", "member_groups", "bumped", "stream", "options_key",
+                 "prepared")
 
     def __init__(self, optimizer, cached, group_index, backend, plan, compute, slot_specs, member_slots, bookkeeping):
         self.registered_cache = cached
@@ -356,6 +393,8 @@ class _Replay:
                 if entry[4] is not None:
                     moving[group].append(entry[4]._version_counter)
         self.move_counters = tuple(tuple(counters) for counters in moving)
+        self.options_key = None
+        self.prepared = None
 
     def _unchanged(self, optimizer) -> bool:
         optimizer._registered_parameters()
@@ -387,7 +426,9 @@ class _Replay:
             return False
         if not all(map(eq, map(_CLEAN, self.seconds), map(_VALUE, self.second_counters))):
             return False
-        if len(set(map(_PENDING, self.member_grads))) != 1:      # equal transforms, as the full step compares
+        # Equal transforms, as the full step compares; usually one shared object.
+        pending = tuple(map(_PENDING, self.member_grads))
+        if not pending or (not all(map(is_, pending, repeat(pending[0]))) and len(set(pending)) != 1):
             return False
         return fused_kernels_enabled() is self.enabled and self.backend.stream() == self.stream
 
@@ -398,7 +439,7 @@ class _Replay:
         fused decision depends on the gradient arrays and the full step runs."""
         if not self.master_mode or not all(map(is_, map(_IS_NONE, current), map(_IS_NONE, self.grads))):
             return False
-        entries = list(optimizer._parameters_with_grad())         # raises the full step's errors
+        entries = optimizer._grad_entries()                      # raises the full step's errors
         if len(entries) != len(self.members) or not all(map(is_, map(_SECOND_OF, entries), self.members)):
             return False
         grads = tuple(map(_THIRD_OF, entries))
@@ -413,13 +454,18 @@ class _Replay:
     def run(self, optimizer) -> bool:
         if not self._unchanged(optimizer):
             return False
-        prepared = [optimizer._prepare_options({key: value for key, value in group.items() if key != "params"},
-                                               "param_group") for group in optimizer.param_groups]
-        if tuple(options.get("fused") for options in prepared) != self.fused_options:
-            return False
-        checked: set = set()
-        for group, parameter in self.validate:
-            optimizer._validate_entry(parameter, prepared[group], checked)
+        key = _options_key(optimizer.param_groups)
+        if key is not None and key == self.options_key:
+            prepared = self.prepared                 # same option values: same preparation and checks
+        else:
+            prepared = [optimizer._prepare_options({name: value for name, value in group.items() if name != "params"},
+                                                   "param_group") for group in optimizer.param_groups]
+            if tuple(options.get("fused") for options in prepared) != self.fused_options:
+                return False
+            checked: set = set()
+            for group, parameter in self.validate:
+                optimizer._validate_entry(parameter, prepared[group], checked)
+            self.options_key, self.prepared = key, prepared
         records = [optimizer._coefficients(self.compute, prepared[group], step + 1, fused)
                    for group, step, fused in self.slots]
         transform = self.member_grads[0]._pending
@@ -435,9 +481,8 @@ class _Replay:
             if moves[group]:
                 for counter in counters:
                     counter.value += 1
-        steps = tuple(step + 1 for step in self.steps)
-        for values, step in zip(self.dicts, steps):
-            values["step"] = step
+        steps = tuple(map(add, self.steps, repeat(1)))
+        deque(map(setitem, self.dicts, repeat("step"), steps), 0)
         self.steps = steps
         self.slots = [(group, step + 1, fused) for group, step, fused in self.slots]
         device_step = None if transform is None else transform.device

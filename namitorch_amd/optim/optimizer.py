@@ -10,6 +10,8 @@ from __future__ import annotations
 
 import weakref
 from collections import defaultdict
+from itertools import compress, repeat
+from operator import attrgetter, is_
 
 import numpy as np
 import torch
@@ -19,6 +21,20 @@ from ..backends._graph_capture import reject_during_capture
 from ..device import Device
 from ..dtype import from_numpy_dtype
 from ..tensor import Parameter, Tensor, no_grad
+
+
+_REQUIRES = attrgetter("_requires_grad")
+_GRAD = attrgetter("_grad")
+_CALL_REF = weakref.ReferenceType.__call__
+
+
+class _Gone:
+    pass
+
+
+# A weak reference whose object is already gone: calling it returns None,
+# which stands in for "this parameter had no gradient" in the entries memo.
+_NO_GRADIENT = weakref.ref(_Gone())
 
 
 def _copy_value(value, path: str, parameter_shape=None, active=None):
@@ -233,6 +249,36 @@ class Optimizer:
                     raise TypeError(f"Gradient dtype {gradient.dtype} does not match parameter dtype {parameter.dtype}.")
                 checked[id(parameter)] = (parameter, weakref.ref(gradient))
                 yield group, parameter, gradient
+
+    def _grad_entries(self) -> tuple:
+        """``tuple(self._parameters_with_grad())``, memoized.
+
+        The entries are a pure function of the registered parameters, their
+        ``requires_grad`` flags and the gradient objects they hold (a
+        Tensor's device, shape and dtype never change).  When all three are
+        unchanged since the last call the entries are rebuilt from the memo
+        with C-level passes; anything else runs the iterator, which raises
+        its errors.  Gradients are held through weak references, so the memo
+        keeps no old gradient alive."""
+        registered = self._registered_parameters()
+        cache = self.__dict__.get("_registered_cache")
+        requires = tuple(map(_REQUIRES, registered))
+        grads = tuple(map(_GRAD, registered))
+        # Which parameters have no gradient is part of the key: a gradient
+        # that was dropped and freed leaves a dead reference, which also
+        # returns None.
+        missing = tuple(map(is_, grads, repeat(None)))
+        memo = self.__dict__.get("_entries_memo")
+        if (memo is not None and memo[0] is cache and memo[1] == requires and memo[2] == missing
+                and all(map(is_, grads, map(_CALL_REF, memo[3])))):
+            return tuple(zip(memo[4], memo[5], compress(grads, memo[6])))
+        entries = tuple(self._parameters_with_grad())
+        if cache is not None and self.__dict__.get("_registered_cache") is cache:
+            refs = tuple(_NO_GRADIENT if gradient is None else weakref.ref(gradient) for gradient in grads)
+            mask = tuple(flag and gradient is not None for flag, gradient in zip(requires, grads))
+            self.__dict__["_entries_memo"] = (cache, requires, missing, refs, tuple(entry[0] for entry in entries),
+                                              tuple(entry[1] for entry in entries), mask)
+        return entries
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         if type(set_to_none) is not bool:

@@ -7,6 +7,8 @@ replaced or rewritten state buffers, edited step counts, pending grad
 transforms, fused-flag changes, invalid state) runs once with the memo and
 once with it disabled; launches, errors and every version counter and step
 count must agree, and the memo must actually replay the unchanged steps.
+Option changes (learning rates, betas, eps, a NaN learning rate) must reach
+the coefficients or raise exactly as the full step does.
 """
 
 from __future__ import annotations
@@ -76,7 +78,7 @@ def _run(monkeypatch, memo: bool, master: bool = False):
     optimizer = nt.optim.AdamW([{"params": params[:3], "weight_decay": 0.1},
                                 {"params": params[3:], "weight_decay": 0.0}], lr=1e-3, master_weights=master)
     errors = []
-    for k in range(18):
+    for k in range(23):
         if k == 3:
             optimizer.param_groups[0]["lr"] = 5e-4
         elif k == 4:
@@ -118,6 +120,14 @@ def _run(monkeypatch, memo: bool, master: bool = False):
         elif k == 16:
             buffer = optimizer.state[id(params[4])]["exp_avg_sq"]
             buffer.copy_(nt.Tensor(np.full(buffer.shape, 1.0, np.float32), dtype=buffer.dtype))
+        elif k == 18:
+            optimizer.param_groups[0]["betas"] = (0.8, 0.99)
+        elif k == 19:
+            optimizer.param_groups[1]["eps"] = 1e-6
+        elif k == 20:
+            optimizer.param_groups[1]["lr"] = float("nan")
+        elif k == 21:
+            optimizer.param_groups[1]["lr"] = 2e-3
         try:
             optimizer.step()
         except (TypeError, ValueError) as error:
@@ -137,7 +147,7 @@ def test_memo_replays_exactly_what_the_full_step_launches(monkeypatch, master):
     with monkeypatch.context() as patch:
         memo = _run(patch, memo=True, master=master)
     assert memo[0] == full[0]                 # every launch: rows, coefficients, transform
-    assert memo[1] == full[1] and len(full[1]) == 2   # the invalid step counts and negative state
+    assert memo[1] == full[1] and len(full[1]) == 3   # invalid step counts, negative state, NaN lr
     assert memo[2] == full[2]
     assert full[3] == []
     replayed = sum(memo[3])
