@@ -172,3 +172,15 @@ def test_memo_is_dropped_by_load_state_dict(monkeypatch):
     optimizer.step()
     assert optimizer.state[id(p)]["step"] == 3
     assert backend.launches[-1][1] == backend.launches[-2][1]      # same coefficients as the third step
+
+
+def test_comparison_detects_a_memo_that_ignores_option_changes(monkeypatch):
+    """The comparison above is sensitive to the options key: with a key that
+    never changes, the memo replays stale coefficients after the lr, betas
+    and eps changes, and the launches no longer match the full step's."""
+    with monkeypatch.context() as patch:
+        full = _run(patch, memo=False)
+    with monkeypatch.context() as patch:
+        patch.setattr(adam_mod, "_options_key", lambda groups: ("unchanging",))
+        stale = _run(patch, memo=True)
+    assert stale[0] != full[0]
