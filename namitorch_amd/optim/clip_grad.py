@@ -21,7 +21,8 @@ from __future__ import annotations
 
 import math
 from numbers import Real
-from operator import attrgetter
+from itertools import repeat
+from operator import attrgetter, eq, is_
 
 import numpy as np
 import torch
@@ -116,13 +117,22 @@ class GradStats:
 _last_stats: dict = {}
 
 
+_PENDING = attrgetter("_pending")
+_VERSION_VALUE = attrgetter("_version_counter.value")
+_FINITE_VERSION = attrgetter("_finite_version")
+_COUNTER = attrgetter("_version_counter")
+
+
 def _stats_key(gradients) -> frozenset:
-    return frozenset((id(gradient), gradient._version, gradient._pending) for gradient in gradients)
+    """(gradient, version, pending transform) of every gradient, by identity.
+    The cache entry holds the gradients and their transforms, so the
+    identities in a stored key cannot be reused by other objects."""
+    return frozenset(zip(map(id, gradients), map(_VERSION_VALUE, gradients), map(id, map(_PENDING, gradients))))
 
 
 def _remember_stats(gradients, stats: GradStats) -> None:
     _last_stats.clear()
-    _last_stats[_stats_key(gradients)] = (list(gradients), stats)
+    _last_stats[_stats_key(gradients)] = (list(gradients), list(map(_PENDING, gradients)), stats)
 
 
 _DEVICE = attrgetter("_device")
@@ -193,7 +203,7 @@ def _total_norm(gradients: list[Tensor], norm_type: float) -> float:
     key = _stats_key(gradients)
     cached = _last_stats.get(key)
     if cached is not None and (norm_type == 2 or math.isinf(norm_type)):
-        stats, blocks = cached[1], None
+        stats, blocks = cached[2], None
     else:
         stats, blocks = grad_stats(gradients)
     scale = stats.prescale()
@@ -213,7 +223,8 @@ def _total_norm(gradients: list[Tensor], norm_type: float) -> float:
 
 def _norm_tensor(norm: float, gradients) -> Tensor:
     device = gradients[0].device if gradients else None
-    storage = torch.tensor(norm, dtype=torch.float64, device=None if device is None else device.torch)
+    # A fill with the value as a kernel argument: no host-to-device copy to wait for.
+    storage = torch.full((), norm, dtype=torch.float64, device=None if device is None else device.torch)
     return Tensor._from_storage(storage, False)
 
 
@@ -241,8 +252,26 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
         coefficient = float(np.divide(np.float64(maximum), np.add(np.float64(norm), _NORM_EPS)))
     if coefficient < 1:
         _require_writable(gradients)
-        clipped: dict = {}      # one shared transform per prior pending transform
+        # One shared clip transform per prior pending transform object (usually
+        # the single unscale transform of unscale_, or none), found by
+        # identity; the dict keeps each base alive, so identities stay unique.
+        clipped: dict = {}
+        unscaled_none = GradTransform()
         reject_during_capture("In-place Tensor updates")
+        pendings = tuple(map(_PENDING, gradients))
+        if pendings and all(map(is_, pendings, repeat(pendings[0]))) and (pendings[0] is None or pendings[0].clip is None):
+            # Common case, one shared prior transform (or none): the loop below
+            # with C-level passes.  Inside no_grad only writability can fail the
+            # in-place check, and _require_writable has checked it.
+            base = unscaled_none if pendings[0] is None else pendings[0]
+            transform = base.then_clip(coefficient)
+            keep = tuple(map(eq, map(_FINITE_VERSION, gradients), map(_VERSION_VALUE, gradients)))
+            for gradient, counter, kept in zip(gradients, map(_COUNTER, gradients), keep):
+                gradient._pending = transform
+                counter.value += 1
+                if kept:
+                    gradient._finite_version = counter.value
+            return _norm_tensor(norm, gradients)
         with no_grad():
             for gradient in gradients:
                 gradient._check_inplace()
@@ -251,11 +280,11 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
                     gradient._materialize()
                     pending = None
                 keep_finite = gradient._finite_version is not None and gradient._finite_version == gradient._version
-                base = pending or GradTransform()
-                transform = clipped.get(base)
-                if transform is None:
-                    transform = clipped[base] = base.then_clip(coefficient)
-                gradient._pending = transform
+                base = unscaled_none if pending is None else pending
+                shared = clipped.get(id(base))
+                if shared is None:
+                    shared = clipped[id(base)] = (base, base.then_clip(coefficient))
+                gradient._pending = shared[1]
                 gradient._version_counter.increment()
                 if keep_finite:
                     gradient._finite_version = gradient._version
