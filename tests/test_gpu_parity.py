@@ -417,6 +417,46 @@ def test_fused_step_matches_api_sequence(config):
         assert not api_trace[config["inf_step"]][0]
 
 
+@pytest.mark.parametrize("scale", [None, 65536.0, 1.0, 3.0])
+@pytest.mark.parametrize("magnitude", ["normal", "tiny", "subnormal", "nonfinite"])
+def test_fp16_grad_norm_paths(scale, magnitude):
+    """Pre-pass exactness on float16 gradients, which are unscaled and
+    rounded element by element: unscaled values that land in the float16
+    subnormal range, float16 subnormal inputs, and values that overflow to
+    inf on storage give the oracle's norm and found_inf, with no scale, a
+    power-of-two scale, scale 1 and any other scale."""
+    rng = _rng(93)
+    n = 70001
+    g32 = (rng.standard_normal(n) * 4.0).astype(np.float32)
+    if magnitude == "tiny":
+        g32[::991] *= np.float32(1e-4)          # unscaled by 65536: float16 subnormals
+    elif magnitude == "subnormal":
+        g32[5] = np.float32(3e-7)               # float16 subnormal inputs
+        g32[60000] = np.float32(-1e-6)
+    elif magnitude == "nonfinite":
+        g32[77] = np.inf
+        g32[4099] = np.float32(7e4)             # overflows float16 on storage
+    g = g32.astype(np.float16)
+    param = nt.Parameter(np.zeros(n, dtype=np.float32), dtype="float16", device=DEV)
+    param.grad = nt.Tensor(g, dtype="float16", device=DEV)
+    if scale is None:
+        norm = nt.optim.clip_grad_norm_([param], 1e30).item()
+        want = oclip.total_norm([g.astype(np.float64)])
+    else:
+        optimizer = nt.optim.AdamW([param], master_weights=True)
+        scaler = nt.GradScaler(init_scale=scale)
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        finite = scaler.unscale_(optimizer)
+        unscaled = oscaler.unscale(g, scale, "float16")
+        assert finite == oscaler.finite([unscaled])
+        norm = nt.optim.clip_grad_norm_([param], 1e30).item()
+        want = oclip.total_norm([unscaled.astype(np.float64)])
+    if math.isfinite(want):
+        assert abs(norm - want) <= NORM_RTOL * want, (norm, want)
+    else:
+        assert (math.isnan(norm) and math.isnan(want)) or norm == want, (norm, want)
+
+
 @pytest.mark.parametrize("scale", [None, 65536.0, 3.0])
 @pytest.mark.parametrize("magnitude", ["normal", "huge", "tiny", "subnormal"])
 def test_bf16_grad_norm_paths(scale, magnitude):
