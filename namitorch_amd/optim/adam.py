@@ -30,6 +30,8 @@ from collections import deque
 from itertools import repeat
 from operator import add, attrgetter, eq, is_, itemgetter, setitem
 
+import numpy as np
+
 from .. import _native
 from ..backends import get_backend
 from ..backends._settings import fused_kernels_enabled
@@ -347,7 +349,7 @@ class _Replay:
                  "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
                  "second_counters", "fused_options", "enabled", "validate", "slots", "backend", "plan", "compute",
                  "record_type", "moment_pairs", "move_counters", "member_groups", "bumped", "stream", "options_key",
-                 "prepared")
+                 "prepared", "adoptable", "spans", "sizes")
 
     def __init__(self, optimizer, cached, group_index, backend, plan, compute, slot_specs, member_slots, bookkeeping):
         self.registered_cache = cached
@@ -395,6 +397,25 @@ class _Replay:
         self.move_counters = tuple(tuple(counters) for counters in moving)
         self.options_key = None
         self.prepared = None
+        # Adopting new gradient objects without master weights: the fused
+        # decision of a member depends on its gradient only through overlap
+        # with the parameter and moments (device, dtype, shape and layout are
+        # what validation already checks), so a memo whose every
+        # grad-dependent decision was "fused" keeps the byte ranges to test
+        # new gradients against.
+        self.adoptable = self.master_mode
+        self.spans = self.sizes = None
+        if not self.master_mode:
+            depends = [self.fused_options[group] is not False and self.enabled for group in self.member_groups]
+            fused = [entry[6] for entry in bookkeeping]
+            pointers = [(entry[0]._ptr, entry[2]._ptr, entry[3]._ptr) for entry in bookkeeping]
+            self.adoptable = (all(f or not d for f, d in zip(fused, depends)) and any(depends)
+                              and None not in (value for row in pointers for value in row))
+            if self.adoptable:
+                self.sizes = np.array([entry[0]._numel * entry[0]._dtype.itemsize if d else 0
+                                       for entry, d in zip(bookkeeping, depends)], dtype=np.int64)
+                lows = np.array(pointers, dtype=np.int64).reshape(len(bookkeeping), 3)
+                self.spans = (lows, lows + self.sizes[:, None])
 
     def _unchanged(self, optimizer) -> bool:
         optimizer._registered_parameters()
@@ -435,9 +456,10 @@ class _Replay:
     def _adopt(self, optimizer, current) -> bool:
         """New gradient objects for the same parameters (gradients reallocated
         every step): validate them as the full step does, then re-point the
-        cached plan's gradient column.  Master-weight mode only; elsewhere the
-        fused decision depends on the gradient arrays and the full step runs."""
-        if not self.master_mode or not all(map(is_, map(_IS_NONE, current), map(_IS_NONE, self.grads))):
+        cached plan's gradient column.  Without master weights the fused
+        decision must also come out the same: no new gradient may overlap its
+        parameter or moments (otherwise the full step decides)."""
+        if not self.adoptable or not all(map(is_, map(_IS_NONE, current), map(_IS_NONE, self.grads))):
             return False
         entries = optimizer._grad_entries()                      # raises the full step's errors
         if len(entries) != len(self.members) or not all(map(is_, map(_SECOND_OF, entries), self.members)):
@@ -445,6 +467,12 @@ class _Replay:
         grads = tuple(map(_THIRD_OF, entries))
         if not all(map(is_, map(_DTYPE, grads), map(_DTYPE, self.member_grads))):
             return False                                        # another storage layout
+        if self.spans is not None:
+            lows, highs = self.spans
+            start = np.fromiter(map(_PTR, grads), dtype=np.int64, count=len(grads))
+            end = start + self.sizes
+            if bool(np.any((start[:, None] < highs) & (lows < end[:, None]) & (self.sizes[:, None] > 0))):
+                return False                                    # the full step decides "not fused"
         if not self.backend._refresh(self.plan, {1: tuple(map(_PTR, grads))}, self.stream):
             return False
         self.grads = current
@@ -525,6 +553,12 @@ class AdamW(Adam):
         if self._master_weights:
             return gradient.dtype in _LOW_PRECISION and parameter.dtype in _LOW_PRECISION
         return gradient.dtype is parameter.dtype
+
+    def _gradient_dtypes_ok(self, parameters: tuple, gradients: tuple) -> bool:
+        if self._master_weights:
+            allowed = _LOW_PRECISION.__contains__
+            return all(map(allowed, map(_DTYPE, gradients))) and all(map(allowed, map(_DTYPE, parameters)))
+        return super()._gradient_dtypes_ok(parameters, gradients)
 
     def _fused_supported(self, parameter: Tensor, gradient: Tensor) -> bool:
         """What the reference's ``supports`` checks (backends/cuda/adamw.py:33-46)."""

@@ -10,8 +10,8 @@ from __future__ import annotations
 
 import weakref
 from collections import defaultdict
-from itertools import compress, repeat
-from operator import attrgetter, is_
+from itertools import chain, compress, repeat
+from operator import and_, attrgetter, eq, is_, is_not, itemgetter
 
 import numpy as np
 import torch
@@ -25,16 +25,13 @@ from ..tensor import Parameter, Tensor, no_grad
 
 _REQUIRES = attrgetter("_requires_grad")
 _GRAD = attrgetter("_grad")
+_DTYPE = attrgetter("_dtype")
+_DEVICE = attrgetter("_device")
+_STORAGE_SHAPE = attrgetter("_storage.shape")
+_PARAMS = itemgetter("params")
+_FIRST_OF = itemgetter(0)
+_SECOND_OF = itemgetter(1)
 _CALL_REF = weakref.ReferenceType.__call__
-
-
-class _Gone:
-    pass
-
-
-# A weak reference whose object is already gone: calling it returns None,
-# which stands in for "this parameter had no gradient" in the entries memo.
-_NO_GRADIENT = weakref.ref(_Gone())
 
 
 def _copy_value(value, path: str, parameter_shape=None, active=None):
@@ -222,6 +219,29 @@ class Optimizer:
         """Gradients must have the parameter's dtype (optimizer.py:193-194)."""
         return gradient.dtype is parameter.dtype
 
+    def _gradient_dtypes_ok(self, parameters: tuple, gradients: tuple) -> bool:
+        """``_gradient_dtype_ok`` for every pair, in C-level passes."""
+        return all(map(is_, map(_DTYPE, gradients), map(_DTYPE, parameters)))
+
+    def _bulk_entries(self, registered, requires: tuple, grads: tuple) -> tuple | None:
+        """The entries of ``_parameters_with_grad`` with its checks done as
+        C-level passes over all gradients at once; None when any check fails,
+        and the iterator then raises the first failure in its own order."""
+        mask = tuple(map(and_, requires, map(is_not, grads, repeat(None))))
+        parameters = tuple(compress(registered, mask))
+        gradients = tuple(compress(grads, mask))
+        if not all(map(isinstance, gradients, repeat(Tensor))):
+            return None
+        devices = tuple(map(_DEVICE, gradients)), tuple(map(_DEVICE, parameters))
+        if not (all(map(is_, *devices)) or all(map(eq, *devices))):
+            return None
+        if not (all(map(eq, map(_STORAGE_SHAPE, gradients), map(_STORAGE_SHAPE, parameters)))
+                and self._gradient_dtypes_ok(parameters, gradients)):
+            return None
+        groups = self.param_groups
+        owners = chain.from_iterable(map(repeat, groups, map(len, map(_PARAMS, groups))))
+        return tuple(zip(compress(owners, mask), parameters, gradients))
+
     def _parameters_with_grad(self):
         self._registered_parameters()
         # A (parameter, gradient) pair that passed the checks once passes them
@@ -264,20 +284,21 @@ class Optimizer:
         cache = self.__dict__.get("_registered_cache")
         requires = tuple(map(_REQUIRES, registered))
         grads = tuple(map(_GRAD, registered))
-        # Which parameters have no gradient is part of the key: a gradient
-        # that was dropped and freed leaves a dead reference, which also
-        # returns None.
-        missing = tuple(map(is_, grads, repeat(None)))
+        # Which parameters have a gradient is part of the key; the memo
+        # holds references to those gradients only.
+        present = tuple(map(is_not, grads, repeat(None)))
         memo = self.__dict__.get("_entries_memo")
-        if (memo is not None and memo[0] is cache and memo[1] == requires and memo[2] == missing
-                and all(map(is_, grads, map(_CALL_REF, memo[3])))):
+        if (memo is not None and memo[0] is cache and memo[1] == requires and memo[2] == present
+                and all(map(is_, compress(grads, present), map(_CALL_REF, memo[3])))):
             return tuple(zip(memo[4], memo[5], compress(grads, memo[6])))
-        entries = tuple(self._parameters_with_grad())
+        entries = self._bulk_entries(registered, requires, grads)
+        if entries is None:
+            entries = tuple(self._parameters_with_grad())
         if cache is not None and self.__dict__.get("_registered_cache") is cache:
-            refs = tuple(_NO_GRADIENT if gradient is None else weakref.ref(gradient) for gradient in grads)
-            mask = tuple(flag and gradient is not None for flag, gradient in zip(requires, grads))
-            self.__dict__["_entries_memo"] = (cache, requires, missing, refs, tuple(entry[0] for entry in entries),
-                                              tuple(entry[1] for entry in entries), mask)
+            refs = tuple(map(weakref.ref, compress(grads, present)))
+            mask = tuple(map(and_, requires, present))
+            self.__dict__["_entries_memo"] = (cache, requires, present, refs, tuple(map(_FIRST_OF, entries)),
+                                              tuple(map(_SECOND_OF, entries)), mask)
         return entries
 
     def zero_grad(self, set_to_none: bool = True) -> None:

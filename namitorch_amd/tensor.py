@@ -57,6 +57,17 @@ class _VersionCounter:
 
 # ---- grad mode (namitorch/autograd.py:15-42) -----------------------------------------
 _grad_mode = threading.local()
+# One immutable Device per torch device: tensors on one device share it, so
+# device comparisons between them are identity checks.
+_DEVICES: dict = {}
+
+
+def _storage_device(place: torch.device) -> Device:
+    found = _DEVICES.get(place)
+    if found is None:
+        found = Device("cpu") if place.type == "cpu" else Device("cuda", place.index)
+        _DEVICES[place] = found
+    return found
 
 
 def is_grad_enabled() -> bool:
@@ -200,7 +211,7 @@ class Tensor:
             raise TypeError("Tensor storage must be a contiguous array.")
         self._storage = storage
         self._dtype = from_torch_dtype(storage.dtype)
-        self._device = Device("cpu") if storage.device.type == "cpu" else Device("cuda", storage.device.index)
+        self._device = _storage_device(storage.device)
         if requires_grad and not self._dtype.can_require_grad:
             raise TypeError(f"Only floating Tensors can require gradients, got {self._dtype.name}.")
         self._requires_grad = requires_grad

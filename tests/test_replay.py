@@ -42,12 +42,20 @@ class _RecordingBackend:
         return 0
 
     def _refresh(self, plan, pointers, stream):
+        # Re-point the volatile columns, as nt_plan_set_pointers does; the
+        # launch records what the plan holds at launch time.
+        layout, chunk, rows, _ = plan[1]
+        plan[1] = (layout, chunk, rows, tuple((c, tuple(v)) for c, v in sorted(pointers.items())))
         return True
 
     def plan(self, rows, layout, chunk=0, pointers=None):
         volatile = tuple(sorted((pointers or {}).items()))
         key = (layout, chunk, tuple(rows), tuple((c, tuple(v)) for c, v in volatile))
-        return self._plans.setdefault(key, ("plan", key))
+        stable = (layout, chunk, tuple(rows), tuple(c for c, _ in volatile))
+        plan = self._plans.setdefault(stable, ["plan", key])
+        if plan[1] != key:
+            self._refresh(plan, dict(pointers or {}), 0)
+        return plan
 
     def adamw_multi(self, plan, slots, xform):
         records = [tuple(getattr(record, name) for name, _ in record._fields_) for record in slots]
@@ -58,6 +66,22 @@ class _RecordingBackend:
 def _run(monkeypatch, memo: bool, master: bool = False):
     backend = _RecordingBackend()
     monkeypatch.setattr(adam_mod, "get_backend", lambda value=None: backend)
+    # Host tensors get addresses as device tensors have them, so the memo's
+    # overlap test for adopted gradients runs: one synthetic address per
+    # storage (aliases of a storage share it), numbered in creation order and
+    # never reused, 2**32 bytes apart, so both runs see the same addresses.
+    initialize = nt.Tensor._initialize
+    addresses: dict = {}
+    storages: list = []                                   # kept alive, so ids are not reused
+
+    def with_pointer(self, storage, *args, **kwargs):
+        initialize(self, storage, *args, **kwargs)
+        if id(storage) not in addresses:
+            storages.append(storage)
+            addresses[id(storage)] = len(storages) << 32
+        self._ptr = addresses[id(storage)]
+
+    monkeypatch.setattr(nt.Tensor, "_initialize", with_pointer)
     replays = []
     original_run = adam_mod._Replay.run
 
@@ -78,7 +102,7 @@ def _run(monkeypatch, memo: bool, master: bool = False):
     optimizer = nt.optim.AdamW([{"params": params[:3], "weight_decay": 0.1},
                                 {"params": params[3:], "weight_decay": 0.0}], lr=1e-3, master_weights=master)
     errors = []
-    for k in range(23):
+    for k in range(26):
         if k == 3:
             optimizer.param_groups[0]["lr"] = 5e-4
         elif k == 4:
@@ -128,6 +152,13 @@ def _run(monkeypatch, memo: bool, master: bool = False):
             optimizer.param_groups[1]["lr"] = float("nan")
         elif k == 21:
             optimizer.param_groups[1]["lr"] = 2e-3
+        elif k == 22:                                         # every gradient reallocated again
+            for p in params:
+                p.grad = nt.Tensor(rng.standard_normal(p.shape).astype(np.float32), dtype=dtype)
+        elif k == 23:                                         # a gradient aliasing its parameter's storage
+            params[2].grad = nt.Tensor._from_storage(params[2]._storage)
+        elif k == 24:
+            params[2].grad = nt.Tensor(rng.standard_normal(params[2].shape).astype(np.float32), dtype=dtype)
         try:
             optimizer.step()
         except (TypeError, ValueError) as error:
@@ -151,10 +182,11 @@ def test_memo_replays_exactly_what_the_full_step_launches(monkeypatch, master):
     assert memo[2] == full[2]
     assert full[3] == []
     replayed = sum(memo[3])
-    # Unchanged steps replay; in master-weight mode so do steps whose
-    # gradients were reallocated (k = 4 and 12).  Other mutations fall back.
-    assert replayed >= (8 if master else 6), memo[3]
-    assert len(memo[3]) - replayed >= (6 if master else 8), memo[3]
+    # Unchanged steps replay, and so do steps whose gradients were
+    # reallocated (k = 4, 12, 22, 24).  Other mutations fall back, the
+    # aliasing gradient (k = 23) included.
+    assert replayed >= 10, memo[3]
+    assert len(memo[3]) - replayed >= 6, memo[3]
 
 
 def test_memo_is_dropped_by_load_state_dict(monkeypatch):
