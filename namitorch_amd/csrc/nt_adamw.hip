@@ -118,6 +118,7 @@ struct MtArgs {
     const nt_amp_ctrl *ctrl;
     int64_t chunk;
     int32_t honor_skip;
+    int32_t split_shift;     // each task runs on 2**split_shift workgroups
 };
 
 struct MtArgs64 {
@@ -149,16 +150,23 @@ __device__ __forceinline__ bool xform_from_ctrl(const nt_amp_ctrl *ctrl, int hon
     return true;
 }
 
-template <class P, class G, class S, class C, class R, bool HAS_COPY>
-__global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__restrict__ tensors,
-                                                          const Task *__restrict__ tasks, MtArgs args) {
+// BLOCK lanes per workgroup, UNROLL 4-element groups in flight per lane.
+// Workgroup b covers part (b mod 2**split_shift) of task (b >> split_shift):
+// a slice of chunk / 2**split_shift elements.
+template <class P, class G, class S, class C, class R, bool HAS_COPY, int BLOCK, int UNROLL>
+__global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__restrict__ tensors,
+                                                         const Task *__restrict__ tasks, MtArgs args) {
+    constexpr int kTileElems = BLOCK * kVec * UNROLL;
     Xform xf = args.xf;
     if (!xform_from_ctrl(args.ctrl, args.honor_skip, xf)) return;
-    const Task task = tasks[blockIdx.x];
+    const uint32_t part = blockIdx.x & ((1u << args.split_shift) - 1u);
+    const Task task = tasks[blockIdx.x >> args.split_shift];
     const DevTensor d = tensors[task.tensor];
     const nt_adamw_coefs c = args.slots[d.slot];
-    const uint64_t start = (uint64_t)task.chunk * (uint64_t)args.chunk;
-    const uint64_t end = min(start + (uint64_t)args.chunk, d.numel);
+    const uint64_t width = (uint64_t)args.chunk >> args.split_shift;
+    const uint64_t start = (uint64_t)task.chunk * (uint64_t)args.chunk + (uint64_t)part * width;
+    if (start >= d.numel) return;                 // a slice past the end of a tensor's last task
+    const uint64_t end = min(start + width, d.numel);
 
     auto *pp = reinterpret_cast<typename P::raw *>(d.param);
     auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
@@ -173,12 +181,12 @@ __global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__res
         const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
         // All groups of an iteration are loaded first, then updated, then
         // stored stream by stream (fewer read/write turnarounds per wave).
-        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kPass2Tile) {
-            float p[kPass2Unroll][kVec], g[kPass2Unroll][kVec], a[kPass2Unroll][kVec], b[kPass2Unroll][kVec];
-            bool ok[kPass2Unroll];
+        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTileElems) {
+            float p[UNROLL][kVec], g[UNROLL][kVec], a[UNROLL][kVec], b[UNROLL][kVec];
+            bool ok[UNROLL];
 #pragma unroll
-            for (int u = 0; u < kPass2Unroll; ++u) {
-                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+            for (int u = 0; u < UNROLL; ++u) {
+                const uint64_t i = base + (uint64_t)u * BLOCK * kVec;
                 ok[u] = i < vend;
                 if (ok[u]) {
                     Vec4IO<G, true>::load(gp, i, g[u]);
@@ -188,7 +196,7 @@ __global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__res
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kPass2Unroll; ++u) {
+            for (int u = 0; u < UNROLL; ++u) {
                 if (ok[u]) {
 #pragma unroll
                     for (int k = 0; k < kVec; ++k) {
@@ -198,25 +206,25 @@ __global__ __launch_bounds__(kBlock) void adamw_mt_kernel(const DevTensor *__res
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kPass2Unroll; ++u)
-                if (ok[u]) Vec4IO<S, true>::store(ap, base + (uint64_t)u * kBlock * kVec, a[u]);   // rounds to S
+            for (int u = 0; u < UNROLL; ++u)
+                if (ok[u]) Vec4IO<S, true>::store(ap, base + (uint64_t)u * BLOCK * kVec, a[u]);   // rounds to S
 #pragma unroll
-            for (int u = 0; u < kPass2Unroll; ++u)
-                if (ok[u]) Vec4IO<S, true>::store(bp, base + (uint64_t)u * kBlock * kVec, b[u]);
+            for (int u = 0; u < UNROLL; ++u)
+                if (ok[u]) Vec4IO<S, true>::store(bp, base + (uint64_t)u * BLOCK * kVec, b[u]);
             if (update) {
 #pragma unroll
-                for (int u = 0; u < kPass2Unroll; ++u)
-                    if (ok[u]) Vec4IO<P, true>::store(pp, base + (uint64_t)u * kBlock * kVec, p[u]);
+                for (int u = 0; u < UNROLL; ++u)
+                    if (ok[u]) Vec4IO<P, true>::store(pp, base + (uint64_t)u * BLOCK * kVec, p[u]);
                 if constexpr (HAS_COPY) {
 #pragma unroll
-                    for (int u = 0; u < kPass2Unroll; ++u)
-                        if (ok[u]) Vec4IO<C, true>::store(cp, base + (uint64_t)u * kBlock * kVec, p[u]);   // RNE copy
+                    for (int u = 0; u < UNROLL; ++u)
+                        if (ok[u]) Vec4IO<C, true>::store(cp, base + (uint64_t)u * BLOCK * kVec, p[u]);   // RNE copy
                 }
             }
         }
         scalar_from = vend;
     }
-    for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock) {
+    for (uint64_t i = scalar_from + threadIdx.x; i < end; i += BLOCK) {
         float p = read_param ? load1<P>(pp, i) : 0.0f;
         float a = load1<S>(ap, i), b = load1<S>(bp, i);
         float g = clip_one<G>(unscale_one<G>(load1<G>(gp, i), xf), xf);
@@ -265,10 +273,33 @@ struct TNone {
     __device__ static float round_f32(float x) { return x; }
 };
 
+// Launch shape of the pass.  A task whose size is a power-of-two multiple of
+// kPassSlice is split over one-wave workgroups of kPassSlice elements, one
+// 4-element group per lane: many short workgroups stream the pass's
+// read/write mix faster than fewer long ones.  Other task sizes run whole
+// tasks on kBlock lanes with kPass2Unroll groups in flight per lane.
+static int32_t pass_split_shift(const nt_plan *plan) {
+    if (plan->chunk % kPassSlice != 0) return 0;
+    const int64_t parts = plan->chunk / kPassSlice;
+    if (parts > 64 || (parts & (parts - 1)) != 0) return 0;
+    int32_t shift = 0;
+    while ((int64_t(1) << shift) < parts) ++shift;
+    if ((int64_t)plan->ntasks > (int64_t(0x7fffffff) >> shift)) return 0;    // grid size
+    return shift;
+}
+
 template <class P, class G, class S, class C, class R, bool HAS_COPY>
 static int32_t launch_mt(nt_plan *plan, const MtArgs &args, hipStream_t stream) {
-    adamw_mt_kernel<P, G, S, C, R, HAS_COPY><<<dim3((unsigned)plan->ntasks), dim3(kBlock), 0, stream>>>(
-        plan->d_tensors, plan->d_tasks, args);
+    MtArgs a = args;
+    a.split_shift = pass_split_shift(plan);
+    if (a.split_shift > 0) {
+        static_assert(kPassSlice == 64 * kVec, "one 4-element group per lane of one wave");
+        adamw_mt_kernel<P, G, S, C, R, HAS_COPY, 64, 1><<<dim3((unsigned)(plan->ntasks << a.split_shift)), dim3(64), 0,
+                                                          stream>>>(plan->d_tensors, plan->d_tasks, a);
+    } else {
+        adamw_mt_kernel<P, G, S, C, R, HAS_COPY, kBlock, kPass2Unroll><<<dim3((unsigned)plan->ntasks), dim3(kBlock), 0,
+                                                                         stream>>>(plan->d_tensors, plan->d_tasks, a);
+    }
     NT_LAUNCH_CHECK("adamw_mt_kernel launch");
     return NT_OK;
 }

@@ -21,6 +21,7 @@ constexpr int kUnroll = 2;         // independent vector groups per thread per i
 constexpr int kTile = kBlock * kVec * kUnroll;   // elements per workgroup iteration
 constexpr int kPass2Unroll = 4;    // groups in flight per lane in the multi-tensor AdamW pass
 constexpr int kPass2Tile = kBlock * kVec * kPass2Unroll;
+constexpr int kPassSlice = 256;    // elements per one-wave workgroup of the split multi-tensor pass
 
 // ---- bit casts ---------------------------------------------------------------
 __device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
