@@ -324,9 +324,10 @@ int32_t nt_any_negative(const void *array, int32_t dtype, uint64_t count,
 /*
  * Streaming probe, no counterpart in the reference: a measurement aid for
  * benchmarks.  It moves `count` elements through `nreads` read and
- * `nwrites` write streams with the pass's access pattern (4096-element
- * workgroups, four nontemporal groups of four elements per lane: 16 bytes
- * for fp32 streams, 8 bytes for 16-bit streams; reads before writes) and
+ * `nwrites` write streams with the pass's access pattern (one-wave
+ * workgroups of 256 elements, one nontemporal group of four elements per
+ * lane: 16 bytes for fp32 streams, 8 bytes for 16-bit streams; reads before
+ * writes) and
  * one add per written element, so its bandwidth is the ceiling of that
  * read/write mix on the device.  The last `nreads16` read and `nwrites16`
  * write streams are 16-bit (bfloat16), the others fp32.  Supported

@@ -150,23 +150,20 @@ __device__ __forceinline__ bool xform_from_ctrl(const nt_amp_ctrl *ctrl, int hon
     return true;
 }
 
-// BLOCK lanes per workgroup, UNROLL 4-element groups in flight per lane.
-// Workgroup b covers part (b mod 2**split_shift) of task (b >> split_shift):
-// a slice of chunk / 2**split_shift elements.
+// BLOCK lanes per workgroup, UNROLL 4-element groups in flight per lane;
+// each workgroup takes one slice of a task (task_slice).
 template <class P, class G, class S, class C, class R, bool HAS_COPY, int BLOCK, int UNROLL>
 __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__restrict__ tensors,
                                                          const Task *__restrict__ tasks, MtArgs args) {
     constexpr int kTileElems = BLOCK * kVec * UNROLL;
     Xform xf = args.xf;
     if (!xform_from_ctrl(args.ctrl, args.honor_skip, xf)) return;
-    const uint32_t part = blockIdx.x & ((1u << args.split_shift) - 1u);
-    const Task task = tasks[blockIdx.x >> args.split_shift];
-    const DevTensor d = tensors[task.tensor];
+    const DevTensor *dp;
+    Slice slice;
+    if (!task_slice(tensors, tasks, args.chunk, args.split_shift, dp, slice)) return;
+    const DevTensor d = *dp;
     const nt_adamw_coefs c = args.slots[d.slot];
-    const uint64_t width = (uint64_t)args.chunk >> args.split_shift;
-    const uint64_t start = (uint64_t)task.chunk * (uint64_t)args.chunk + (uint64_t)part * width;
-    if (start >= d.numel) return;                 // a slice past the end of a tensor's last task
-    const uint64_t end = min(start + width, d.numel);
+    const uint64_t start = slice.start, end = slice.end;
 
     auto *pp = reinterpret_cast<typename P::raw *>(d.param);
     auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
@@ -278,20 +275,10 @@ struct TNone {
 // 4-element group per lane: many short workgroups stream the pass's
 // read/write mix faster than fewer long ones.  Other task sizes run whole
 // tasks on kBlock lanes with kPass2Unroll groups in flight per lane.
-static int32_t pass_split_shift(const nt_plan *plan) {
-    if (plan->chunk % kPassSlice != 0) return 0;
-    const int64_t parts = plan->chunk / kPassSlice;
-    if (parts > 64 || (parts & (parts - 1)) != 0) return 0;
-    int32_t shift = 0;
-    while ((int64_t(1) << shift) < parts) ++shift;
-    if ((int64_t)plan->ntasks > (int64_t(0x7fffffff) >> shift)) return 0;    // grid size
-    return shift;
-}
-
 template <class P, class G, class S, class C, class R, bool HAS_COPY>
 static int32_t launch_mt(nt_plan *plan, const MtArgs &args, hipStream_t stream) {
     MtArgs a = args;
-    a.split_shift = pass_split_shift(plan);
+    a.split_shift = split_shift(plan, kPassSlice);
     if (a.split_shift > 0) {
         static_assert(kPassSlice == 64 * kVec, "one 4-element group per lane of one wave");
         adamw_mt_kernel<P, G, S, C, R, HAS_COPY, 64, 1><<<dim3((unsigned)(plan->ntasks << a.split_shift)), dim3(64), 0,

@@ -489,35 +489,45 @@ __global__ __launch_bounds__(kBlock) void norm_pow_finalize_kernel(const double 
     *ctrl = c;
 }
 
-// In-place grad transform: g <- clip(unscale(g)).
-template <class G>
-__global__ __launch_bounds__(kBlock) void grad_apply_kernel(const DevTensor *__restrict__ tensors,
-                                                            const Task *__restrict__ tasks, int64_t chunk, Xform xf,
-                                                            const nt_amp_ctrl *ctrl) {
+// In-place grad transform: g <- clip(unscale(g)).  One slice (task_slice)
+// per workgroup: kBlock lanes with UNROLL 4-element groups each.  fp32
+// gradients run 1024-element slices with one group per lane; 16-bit ones,
+// whose f64 clip rounding costs twice the ALU work per byte, keep whole
+// tasks with two groups per lane in flight (both measured fastest).
+template <class G> struct ApplyShape {
+    static constexpr int unroll = G::code == NT_F32 ? 1 : 2;
+    static constexpr int64_t slice = G::code == NT_F32 ? (int64_t)kBlock * kVec : 0;   // 0: whole tasks
+};
+
+template <class G, int UNROLL = ApplyShape<G>::unroll, int BLOCK = kBlock>
+__global__ __launch_bounds__(BLOCK) void grad_apply_kernel(const DevTensor *__restrict__ tensors,
+                                                           const Task *__restrict__ tasks, int64_t chunk, Xform xf,
+                                                           const nt_amp_ctrl *ctrl, int32_t shift) {
     if (ctrl != nullptr) {
         if (xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale_used, xf.unscale, xf.inv_scale);
         xf.clip = ctrl->clip;
         xf.clip_coef = ctrl->clip_coef;
     }
     if (!xf.unscale && !xf.clip) return;
-    const Task task = tasks[blockIdx.x];
-    const DevTensor d = tensors[task.tensor];
-    const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
-    const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+    const DevTensor *dp;
+    Slice slice;
+    if (!task_slice(tensors, tasks, chunk, shift, dp, slice)) return;
+    const DevTensor &d = *dp;
+    const uint64_t start = slice.start, end = slice.end;
     auto *gp = reinterpret_cast<typename G::raw *>(d.grad);
     uint64_t scalar_from = start;
     if (d.flags & kAligned16) {
         const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
-        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTile) {
-            float g[kUnroll][kVec];
+        for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += (uint64_t)BLOCK * kVec * UNROLL) {
+            float g[UNROLL][kVec];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+            for (int u = 0; u < UNROLL; ++u) {
+                const uint64_t i = base + (uint64_t)u * BLOCK * kVec;
                 if (i < vend) Vec4IO<G, true>::load(gp, i, g[u]);
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+            for (int u = 0; u < UNROLL; ++u) {
+                const uint64_t i = base + (uint64_t)u * BLOCK * kVec;
                 if (i < vend) {
 #pragma unroll
                     for (int k = 0; k < kVec; ++k) g[u][k] = clip_one<G>(unscale_one<G>(g[u][k], xf), xf);
@@ -527,7 +537,7 @@ __global__ __launch_bounds__(kBlock) void grad_apply_kernel(const DevTensor *__r
         }
         scalar_from = vend;
     }
-    for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock)
+    for (uint64_t i = scalar_from + threadIdx.x; i < end; i += BLOCK)
         store1<G>(gp, i, clip_one<G>(unscale_one<G>(load1<G>(gp, i), xf), xf));
 }
 
@@ -633,8 +643,11 @@ template <class G> struct NormPowL {
     }
 };
 template <class G> struct ApplyL {
-    template <class... A> static void launch(dim3 g, hipStream_t s, A... a) {
-        grad_apply_kernel<G><<<g, dim3(kBlock), 0, s>>>(a...);
+    // Grid: the plan's tasks, each split as ApplyShape<G> says.
+    static void launch(dim3, hipStream_t s, const nt_plan *plan, Xform xf, const nt_amp_ctrl *ctrl) {
+        const int32_t shift = ApplyShape<G>::slice ? split_shift(plan, ApplyShape<G>::slice) : 0;
+        grad_apply_kernel<G><<<dim3((unsigned)(plan->ntasks << shift)), dim3(kBlock), 0, s>>>(
+            plan->d_tensors, plan->d_tasks, plan->chunk, xf, ctrl, shift);
     }
 };
 
@@ -747,12 +760,11 @@ int32_t nt_grad_apply(nt_plan *plan, const nt_grad_xform *xform, void *stream) {
     const nt_amp_ctrl *ctrl = xform->ctrl;
     if (ctrl != nullptr) xf.unscale = xform->unscale ? 1 : 0;
     hipStream_t s = (hipStream_t)stream;
-    dim3 grid((unsigned)plan->ntasks);
     if (plan->layout.grad_dtype == NT_F64) {
-        grad_apply_f64_kernel<<<grid, dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, plan->chunk, xf, ctrl);
+        grad_apply_f64_kernel<<<dim3((unsigned)plan->ntasks), dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks,
+                                                                                    plan->chunk, xf, ctrl);
     } else {
-        rc = grad_dispatch<ApplyL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
-                                   (const Task *)plan->d_tasks, plan->chunk, xf, ctrl);
+        rc = grad_dispatch<ApplyL>(plan->layout.grad_dtype, dim3(), s, (const nt_plan *)plan, xf, ctrl);
         if (rc != NT_OK) return rc;
     }
     NT_LAUNCH_CHECK("grad_apply_kernel launch");

@@ -17,17 +17,23 @@
 namespace nt {
 
 // ---- zero ------------------------------------------------------------------------------
-// One workgroup per task; 16-byte zero stores where the tensor is aligned.
+// 16-byte zero stores where the tensor is aligned; a slice is one store per
+// lane of a kBlock-lane workgroup (write-only streams run fastest that way).
+template <class T>
+constexpr int64_t zero_slice() { return (int64_t)kBlock * (16 / (int64_t)sizeof(T)); }
+
 template <class T>
 __global__ __launch_bounds__(kBlock) void grad_zero_kernel(const DevTensor *__restrict__ tensors,
-                                                           const Task *__restrict__ tasks, int64_t chunk) {
+                                                           const Task *__restrict__ tasks, int64_t chunk,
+                                                           int32_t shift) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(1))) u32x4 gu32x4;
     constexpr int kPer = 16 / (int)sizeof(T);           // elements per 16-byte store
-    const Task task = tasks[blockIdx.x];
-    const DevTensor &d = tensors[task.tensor];
-    const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
-    const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+    const DevTensor *dp;
+    Slice slice;
+    if (!task_slice(tensors, tasks, chunk, shift, dp, slice)) return;
+    const DevTensor &d = *dp;
+    const uint64_t start = slice.start, end = slice.end;
     T *g = reinterpret_cast<T *>(d.grad);
     uint64_t scalar_from = start;
     if (d.flags & kAligned16) {
@@ -48,13 +54,18 @@ __device__ __forceinline__ float accumulate_one(float stored, float incoming) {
     return D::round_f32(stored + converted);
 }
 
+// A slice is one kTile iteration: kUnroll 4-element groups per lane.  For
+// this read-read-write mix that ran faster than one-wave slices or one
+// group per lane.
 template <class D, class S, bool ASSIGN>
 __global__ __launch_bounds__(kBlock) void grad_accumulate_kernel(const DevTensor *__restrict__ tensors,
-                                                                 const Task *__restrict__ tasks, int64_t chunk) {
-    const Task task = tasks[blockIdx.x];
-    const DevTensor &d = tensors[task.tensor];
-    const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
-    const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+                                                                 const Task *__restrict__ tasks, int64_t chunk,
+                                                                 int32_t shift) {
+    const DevTensor *dp;
+    Slice slice;
+    if (!task_slice(tensors, tasks, chunk, shift, dp, slice)) return;
+    const DevTensor &d = *dp;
+    const uint64_t start = slice.start, end = slice.end;
     auto *dst = reinterpret_cast<typename D::raw *>(d.grad);
     const auto *src = reinterpret_cast<const typename S::raw *>(d.param);
     uint64_t scalar_from = start;
@@ -139,21 +150,30 @@ __global__ __launch_bounds__(kBlock) void grad_accumulate_any_kernel(const DevTe
     }
 }
 
-template <class D, class S>
-static void launch_accumulate(dim3 grid, hipStream_t s, const DevTensor *t, const Task *k, int64_t chunk, bool assign) {
-    if (assign) grad_accumulate_kernel<D, S, true><<<grid, dim3(kBlock), 0, s>>>(t, k, chunk);
-    else grad_accumulate_kernel<D, S, false><<<grid, dim3(kBlock), 0, s>>>(t, k, chunk);
+template <class D, class S, bool ASSIGN>
+static void launch_accumulate(const nt_plan *plan, hipStream_t s) {
+    const int32_t shift = split_shift(plan, kTile);
+    grad_accumulate_kernel<D, S, ASSIGN><<<dim3((unsigned)(plan->ntasks << shift)), dim3(kBlock), 0, s>>>(
+        plan->d_tensors, plan->d_tasks, plan->chunk, shift);
 }
 
 template <class D>
-static bool dispatch_source(int32_t src, dim3 grid, hipStream_t s, const DevTensor *t, const Task *k, int64_t chunk,
-                            bool assign) {
+static bool dispatch_source(int32_t src, const nt_plan *plan, hipStream_t s, bool assign) {
     switch (src) {
-        case NT_F32: launch_accumulate<D, TF32>(grid, s, t, k, chunk, assign); return true;
-        case NT_F16: launch_accumulate<D, TF16>(grid, s, t, k, chunk, assign); return true;
-        case NT_BF16: launch_accumulate<D, TBF16>(grid, s, t, k, chunk, assign); return true;
+        case NT_F32: assign ? launch_accumulate<D, TF32, true>(plan, s) : launch_accumulate<D, TF32, false>(plan, s); return true;
+        case NT_F16: assign ? launch_accumulate<D, TF16, true>(plan, s) : launch_accumulate<D, TF16, false>(plan, s); return true;
+        case NT_BF16:
+            assign ? launch_accumulate<D, TBF16, true>(plan, s) : launch_accumulate<D, TBF16, false>(plan, s);
+            return true;
         default: return false;
     }
+}
+
+template <class T>
+static void launch_zero(const nt_plan *plan, hipStream_t s) {
+    const int32_t shift = split_shift(plan, zero_slice<T>());
+    grad_zero_kernel<T><<<dim3((unsigned)(plan->ntasks << shift)), dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks,
+                                                                                       plan->chunk, shift);
 }
 
 }  // namespace nt
@@ -170,14 +190,11 @@ int32_t nt_grad_zero(nt_plan *plan, void *stream) {
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
-    dim3 grid((unsigned)plan->ntasks);
-    const DevTensor *t = plan->d_tensors;
-    const Task *k = plan->d_tasks;
     switch (plan->layout.grad_dtype) {
-        case NT_F32: grad_zero_kernel<uint32_t><<<grid, dim3(kBlock), 0, s>>>(t, k, plan->chunk); break;
+        case NT_F32: launch_zero<uint32_t>(plan, s); break;
         case NT_F16:
-        case NT_BF16: grad_zero_kernel<uint16_t><<<grid, dim3(kBlock), 0, s>>>(t, k, plan->chunk); break;
-        case NT_F64: grad_zero_kernel<uint64_t><<<grid, dim3(kBlock), 0, s>>>(t, k, plan->chunk); break;
+        case NT_BF16: launch_zero<uint16_t>(plan, s); break;
+        case NT_F64: launch_zero<uint64_t>(plan, s); break;
         default: return fail(NT_ERR_TYPE, "nt_grad_zero: unsupported gradient dtype");
     }
     NT_LAUNCH_CHECK("grad_zero_kernel launch");
@@ -200,9 +217,9 @@ int32_t nt_grad_accumulate(nt_plan *plan, int32_t assign, void *stream) {
     bool launched = false;
     if (dst != NT_F64 && src != NT_F64) {
         switch (dst) {
-            case NT_F32: launched = dispatch_source<TF32>(src, grid, s, t, k, plan->chunk, assign != 0); break;
-            case NT_F16: launched = dispatch_source<TF16>(src, grid, s, t, k, plan->chunk, assign != 0); break;
-            case NT_BF16: launched = dispatch_source<TBF16>(src, grid, s, t, k, plan->chunk, assign != 0); break;
+            case NT_F32: launched = dispatch_source<TF32>(src, plan, s, assign != 0); break;
+            case NT_F16: launched = dispatch_source<TF16>(src, plan, s, assign != 0); break;
+            case NT_BF16: launched = dispatch_source<TBF16>(src, plan, s, assign != 0); break;
             default: break;
         }
     } else {

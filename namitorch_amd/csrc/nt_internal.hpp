@@ -39,6 +39,41 @@ struct nt_plan {
 
 namespace nt {
 
+// ---- split launches ----------------------------------------------------------------------
+// A plan task of `chunk` elements may run on 2**shift workgroups, each taking
+// a slice of chunk >> shift elements: workgroup b covers slice
+// (b mod 2**shift) of task (b >> shift).  Streaming kernels use it to pick
+// the workgroup shape that moves their read/write mix fastest while the task
+// map stays as built.
+struct Slice {
+    uint64_t start, end;
+};
+
+// This workgroup's slice; false when it starts past the end of its tensor
+// (the last task of a tensor may be short).
+__device__ __forceinline__ bool task_slice(const DevTensor *__restrict__ tensors, const Task *__restrict__ tasks,
+                                           int64_t chunk, int32_t shift, const DevTensor *&d, Slice &slice) {
+    const uint32_t part = blockIdx.x & ((1u << shift) - 1u);
+    const Task task = tasks[blockIdx.x >> shift];
+    d = &tensors[task.tensor];
+    const uint64_t width = (uint64_t)chunk >> shift;
+    slice.start = (uint64_t)task.chunk * (uint64_t)chunk + (uint64_t)part * width;
+    slice.end = min(slice.start + width, d->numel);
+    return slice.start < d->numel;
+}
+
+// log2(chunk / slice) when that is a power of two in [1, 64] and the grid
+// stays below 2**31 workgroups, else 0 (one workgroup per task).
+inline int32_t split_shift(const nt_plan *plan, int64_t slice) {
+    if (plan->chunk % slice != 0) return 0;
+    const int64_t parts = plan->chunk / slice;
+    if (parts > 64 || (parts & (parts - 1)) != 0) return 0;
+    int32_t shift = 0;
+    while ((int64_t(1) << shift) < parts) ++shift;
+    if (plan->ntasks > (int64_t(0x7fffffff) >> shift)) return 0;
+    return shift;
+}
+
 // Record `msg` as this thread's last error and return `code`.
 int32_t fail(int32_t code, const std::string &msg);
 // Convert a HIP status into NT_ERR_HIP with context; NT_OK on success.

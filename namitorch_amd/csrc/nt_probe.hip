@@ -3,11 +3,11 @@
 // so that a benchmark can report the bandwidth each access mix reaches on
 // the device next to what the pass reaches.
 //
-// Each workgroup covers 4096 consecutive elements of every stream (like a
-// pass task), each lane four groups of four elements with nontemporal
-// accesses: 16 bytes per group for fp32 streams and 8 bytes for 16-bit
-// streams, as the pass issues them.  All reads come first, then the writes
-// grouped by stream.  Write stream w receives read stream (w mod R) plus
+// Each workgroup is one wave covering 256 consecutive elements of every
+// stream (like a slice of a pass task), each lane one group of four elements
+// with nontemporal accesses: 16 bytes for fp32 streams and 8 bytes for
+// 16-bit streams, as the pass issues them.  All reads come first, then the
+// writes grouped by stream.  Write stream w receives read stream (w mod R) plus
 // read stream R-1 (1.0 when there are no reads), so every read is used and
 // nothing is optimised away; 16-bit streams hold bfloat16 values, read
 // exactly and written truncated to their upper 16 bits.
@@ -18,7 +18,11 @@
 namespace nt {
 
 constexpr int kProbeMax = 8;
-constexpr int kProbeChunk = kBlock * kVec * kPass2Unroll;   // 4096 elements
+constexpr int kProbeLanes = 64;
+constexpr int kProbeUnroll = 1;
+constexpr int kProbeSlice = kProbeLanes * kVec * kProbeUnroll;   // elements per workgroup
+static_assert(kProbeSlice == kPassSlice, "the probe streams like the split pass");
+constexpr uint64_t kProbeQuantum = 4096;                        // count granularity of the entry point
 
 struct ProbeArgs {
     const void *reads[kProbeMax];
@@ -38,15 +42,15 @@ __device__ __forceinline__ u32x2 f32x4_to_bf16_trunc(f32x4 v) {
 // R read streams of which the last R16 are 16-bit; W write streams of which
 // the last W16 are 16-bit.
 template <int R, int R16, int W, int W16>
-__global__ __launch_bounds__(kBlock) void stream_probe_kernel(ProbeArgs args) {
+__global__ __launch_bounds__(kProbeLanes) void stream_probe_kernel(ProbeArgs args) {
     constexpr int R32 = R - R16, W32 = W - W16;
-    const uint64_t start = (uint64_t)blockIdx.x * kProbeChunk + (uint64_t)threadIdx.x * kVec;
-    f32x4 in[R > 0 ? R : 1][kPass2Unroll];
+    const uint64_t start = (uint64_t)blockIdx.x * kProbeSlice + (uint64_t)threadIdx.x * kVec;
+    f32x4 in[R > 0 ? R : 1][kProbeUnroll];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int u = 0; u < kPass2Unroll; ++u) {
-            const uint64_t i = start + (uint64_t)u * kBlock * kVec;
+        for (int u = 0; u < kProbeUnroll; ++u) {
+            const uint64_t i = start + (uint64_t)u * kProbeLanes * kVec;
             if (r < R32)
                 in[r][u] = gload<true, f32x4, gf32x4>(static_cast<const float *>(args.reads[r]) + i);
             else
@@ -55,8 +59,8 @@ __global__ __launch_bounds__(kBlock) void stream_probe_kernel(ProbeArgs args) {
 #pragma unroll
     for (int w = 0; w < W; ++w)
 #pragma unroll
-        for (int u = 0; u < kPass2Unroll; ++u) {
-            const uint64_t i = start + (uint64_t)u * kBlock * kVec;
+        for (int u = 0; u < kProbeUnroll; ++u) {
+            const uint64_t i = start + (uint64_t)u * kProbeLanes * kVec;
             f32x4 value = {1.0f, 1.0f, 1.0f, 1.0f};
             if constexpr (R > 0) value = in[w % R][u] + in[R - 1][u];
             if (w < W32)
@@ -71,7 +75,7 @@ __global__ __launch_bounds__(kBlock) void stream_probe_kernel(ProbeArgs args) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int u = 0; u < kPass2Unroll; ++u) sum += in[r][u];
+            for (int u = 0; u < kProbeUnroll; ++u) sum += in[r][u];
         if (__builtin_bit_cast(uint32_t, sum.x) == 0x7fbadbadu)
             static_cast<float *>(args.writes[kProbeMax - 1])[start] = sum.y;
     }
@@ -79,7 +83,7 @@ __global__ __launch_bounds__(kBlock) void stream_probe_kernel(ProbeArgs args) {
 
 template <int R, int R16, int W, int W16>
 static void launch_probe(dim3 grid, hipStream_t s, const ProbeArgs &args) {
-    stream_probe_kernel<R, R16, W, W16><<<grid, dim3(kBlock), 0, s>>>(args);
+    stream_probe_kernel<R, R16, W, W16><<<grid, dim3(kProbeLanes), 0, s>>>(args);
 }
 
 typedef void (*ProbeLauncher)(dim3, hipStream_t, const ProbeArgs &);
@@ -120,9 +124,9 @@ int32_t nt_stream_probe(const void *const *reads, int32_t nreads, int32_t nreads
         return fail(NT_ERR_VALUE, "nt_stream_probe: supported (reads, 16-bit reads, writes, 16-bit writes): "
                                   "(0,0,1,0) (0,0,3,0) (1,0,0,0) (1,0,1,0) (2,0,2,0) (4,0,0,0) (4,0,3,0) "
                                   "(5,0,4,0) (4,3,4,3) (4,1,4,1)");
-    if (count == 0 || count % (uint64_t)kProbeChunk != 0)
+    if (count == 0 || count % kProbeQuantum != 0)
         return fail(NT_ERR_VALUE, "nt_stream_probe: count must be a positive multiple of 4096");
-    if (count / (uint64_t)kProbeChunk > 0x7fffffffull) return fail(NT_ERR_VALUE, "nt_stream_probe: count too large");
+    if (count / (uint64_t)kProbeSlice > 0x7fffffffull) return fail(NT_ERR_VALUE, "nt_stream_probe: count too large");
     if ((nreads > 0 && reads == nullptr) || writes == nullptr)
         return fail(NT_ERR_VALUE, "nt_stream_probe: NULL stream table");
     if (nwrites == 0 && (writes[0] == nullptr || (uintptr_t)writes[0] % 16 != 0))
@@ -139,7 +143,7 @@ int32_t nt_stream_probe(const void *const *reads, int32_t nreads, int32_t nreads
         args.writes[w] = writes[w];
     }
     if (nwrites == 0) args.writes[kProbeMax - 1] = writes[0];
-    launcher(dim3((unsigned)(count / (uint64_t)kProbeChunk)), (hipStream_t)stream, args);
+    launcher(dim3((unsigned)(count / (uint64_t)kProbeSlice)), (hipStream_t)stream, args);
     NT_LAUNCH_CHECK("stream_probe_kernel launch");
     return NT_OK;
 }

@@ -38,7 +38,7 @@ from ..backends._settings import fused_kernels_enabled
 from ..backends.hip import make_xform
 from ..dtype import DType, bfloat16, float16, float32, float64, normalize_dtype
 from ..tensor import Tensor
-from ._common import _FirstOrderOptimizer, _real_option, _round_scalar
+from ._common import _FirstOrderOptimizer, _real_option, _round_scalar, _zeros_views
 
 _LOW_PRECISION = (float16, bfloat16, float32)
 
@@ -99,6 +99,25 @@ class Adam(_FirstOrderOptimizer):
         record_type = _native.AdamWCoefs64 if dtype is float64 else _native.AdamWCoefs
         return record_type(*coefficients, int(options["maximize"]), int(lr != 0),
                            int(not self._decoupled_weight_decay), 0)
+
+    def _create_buffers(self, parameters) -> None:
+        """The missing buffers of `parameters`, created together: zero moments
+        and the fp32 master copy as views of one flat allocation per (buffer,
+        device, dtype).  Values are those ``_buffers`` gives one at a time."""
+        names = ("exp_avg", "exp_avg_sq") + (("master",) if self._master_weights else ())
+        states = self.state
+        for name in names:
+            groups: dict = {}
+            for parameter in parameters:
+                if states[id(parameter)].get(name) is None:
+                    key = (parameter._device, self._state_dtype(parameter, name))
+                    groups.setdefault(key, []).append(parameter)
+            for (device, dtype), members in groups.items():
+                views = _zeros_views([parameter.shape for parameter in members], dtype, device)
+                for parameter, view in zip(members, views):
+                    if name == "master":
+                        view._storage.copy_(parameter._data)       # exact: widening to float32
+                    states[id(parameter)][name] = view
 
     def _buffers(self, parameter: Tensor, state: dict):
         first = state.get("exp_avg")
@@ -196,6 +215,11 @@ class Adam(_FirstOrderOptimizer):
         master_mode = self._master_weights
         fused_cache = self.__dict__.setdefault("_fused_checked", {})
         enabled = fused_kernels_enabled()
+        fresh = [parameter for parameter, _, _ in members
+                 if states[id(parameter)].get("exp_avg") is None or states[id(parameter)].get("exp_avg_sq") is None
+                 or (master_mode and states[id(parameter)].get("master") is None)]
+        if len(fresh) > 1:
+            self._create_buffers(fresh)
         for parameter, gradient, options in members:
             state = states[id(parameter)]
             first = state.get("exp_avg")
