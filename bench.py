@@ -352,7 +352,8 @@ def bench_chunks(nt, torch, launches=20, reps=4):
     """The AdamW pass with 4096- and 2048-element tasks, timed alternately in
     one process on the same buffers (so both see the same physical
     placement), for each BASELINE layout; the optimizer picks the chunk per
-    layout (optim/adam.py _pass_chunk).  Random N(0, 0.02) params, N(0, 1e-3)
+    layout (optim/adam.py _pass_chunk).  Both run the same one-wave
+    256-element workgroups; the task size sets the task map and the tails.  Random N(0, 0.02) params, N(0, 1e-3)
     grads, zero moments; C4/C5 launches carry their clip (and unscale)
     transforms, as in their steps."""
     import ctypes
@@ -568,7 +569,7 @@ def main():
                    "step_pct_hbm_peak": 100 * 28 * c2["params_per_s"] / 1e9 / HBM_PEAK_GBPS},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": pmc_traffic(),
-                     "kernel": "nt::adamw_mt_kernel<TF32,TF32,TF32,TNone,RoundF32,false>",
+                     "kernel": "nt::adamw_mt_kernel<TF32,TF32,TF32,TNone,RoundF32,false,64,1>",
                      "kernel_ms": c2["kernel_ms"],
                      "mix_ceiling_GBps": ceilings["r4w3_inplace"]["GBps"] if ceilings else None,
                      "frac_of_mix_ceiling": achieved / ceilings["r4w3_inplace"]["GBps"] if ceilings else None},

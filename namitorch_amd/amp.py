@@ -64,10 +64,20 @@ class DeviceStep:
         self.scheduler = None                 # advanced at reconciliation iff the step updated
 
     def capture(self) -> None:
-        """Queue the copy of the control block to pinned host memory."""
+        """Queue the copy of the control block to pinned host memory.  The
+        copy runs on the backend's side stream once the work queued so far
+        on the current stream is done, so the AdamW pass queued next does not
+        wait behind it.  Nothing writes the block after the finalize kernel."""
+        import torch
         with self.backend.context():
-            self.snapshot.copy_(self.block, non_blocking=True)
-            self.event.record()
+            ready = torch.cuda.Event()
+            ready.record()
+            side = self.backend.side_stream()
+            side.wait_event(ready)
+            with torch.cuda.stream(side):
+                self.snapshot.copy_(self.block, non_blocking=True)
+                self.event.record(side)
+            self.block.record_stream(side)        # not reused before the copy has read it
 
     def ctrl(self) -> _native.AmpCtrl:
         if self._ctrl is None:

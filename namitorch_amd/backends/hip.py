@@ -134,6 +134,7 @@ class HIPBackend:
         self.adamw = AdamWHIPKernel(self)
         self._plans: OrderedDict = OrderedDict()
         self._lock = threading.RLock()
+        self._side_stream = None
         _backends_alive.add(self)
 
     def __repr__(self):
@@ -161,6 +162,14 @@ class HIPBackend:
 
     def synchronize(self) -> None:
         _native.call("nt_stream_synchronize", self.stream())
+
+    def side_stream(self) -> torch.cuda.Stream:
+        """A stream of this device (default priority) for small copies that
+        work queued on the caller's stream should not wait behind."""
+        with self._lock:
+            if self._side_stream is None:
+                self._side_stream = torch.cuda.Stream(device=self.device.torch)
+            return self._side_stream
 
     # ---- plans -----------------------------------------------------------------------------
     def plan(self, rows: list[tuple], layout: tuple, chunk: int = 0, pointers: dict | None = None) -> Plan:
