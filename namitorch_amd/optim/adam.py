@@ -100,6 +100,20 @@ class Adam(_FirstOrderOptimizer):
         return record_type(*coefficients, int(options["maximize"]), int(lr != 0),
                            int(not self._decoupled_weight_decay), 0)
 
+    @staticmethod
+    def _next_coefficients(dtype: DType, options: dict, step: int, fused: bool, previous):
+        """``_coefficients`` for `step` from the record of an earlier step with
+        the same options: only the two bias corrections depend on the step."""
+        beta1, beta2 = options["betas"]
+        first = _round_scalar(dtype, 1 - beta1 ** step)
+        second = _round_scalar(dtype, 1 - beta2 ** step)
+        if fused and (first <= 0 or second <= 0):
+            raise ValueError("Fused AdamW eps and bias corrections must be positive.")
+        record = type(previous).from_buffer_copy(previous)
+        record.correction1 = first
+        record.correction2 = second
+        return record
+
     def _create_buffers(self, parameters) -> None:
         """The missing buffers of `parameters`, created together: zero moments
         and the fp32 master copy as views of one flat allocation per (buffer,
@@ -373,7 +387,7 @@ class _Replay:
                  "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
                  "second_counters", "fused_options", "enabled", "validate", "slots", "backend", "plan", "compute",
                  "record_type", "moment_pairs", "move_counters", "member_groups", "bumped", "stream", "options_key",
-                 "prepared", "adoptable", "spans", "sizes")
+                 "prepared", "adoptable", "spans", "sizes", "records")
 
     def __init__(self, optimizer, cached, group_index, backend, plan, compute, slot_specs, member_slots, bookkeeping):
         self.registered_cache = cached
@@ -421,6 +435,7 @@ class _Replay:
         self.move_counters = tuple(tuple(counters) for counters in moving)
         self.options_key = None
         self.prepared = None
+        self.records = None                  # the last launch's coefficient records, one per slot
         # Adopting new gradient objects without master weights: the fused
         # decision of a member depends on its gradient only through overlap
         # with the parameter and moments (device, dtype, shape and layout are
@@ -461,10 +476,11 @@ class _Replay:
             if not (all(map(is_, map(_FIRST, dicts), self.firsts)) and all(map(is_, map(_SECOND, dicts), self.seconds))
                     and (not self.master_mode or all(map(is_, map(_MASTER, dicts), self.masters)))):
                 return False
-            steps = tuple(map(_STEP, dicts))
+            # The step counts are the int objects the last step stored (an
+            # equal value of another type or object takes the full step).
+            if not all(map(is_, map(_STEP, dicts), self.steps)):
+                return False
         except KeyError:
-            return False
-        if steps != self.steps or set(map(type, steps)) != {int}:
             return False
         buffers = self.buffers
         if any(map(_REQUIRES, buffers)) or not all(map(_WRITABLE, buffers)) or not all(map(_WRITABLE, self.members)):
@@ -507,8 +523,10 @@ class _Replay:
         if not self._unchanged(optimizer):
             return False
         key = _options_key(optimizer.param_groups)
+        previous = None
         if key is not None and key == self.options_key:
             prepared = self.prepared                 # same option values: same preparation and checks
+            previous = self.records
         else:
             prepared = [optimizer._prepare_options({name: value for name, value in group.items() if name != "params"},
                                                    "param_group") for group in optimizer.param_groups]
@@ -518,8 +536,13 @@ class _Replay:
             for group, parameter in self.validate:
                 optimizer._validate_entry(parameter, prepared[group], checked)
             self.options_key, self.prepared = key, prepared
-        records = [optimizer._coefficients(self.compute, prepared[group], step + 1, fused)
-                   for group, step, fused in self.slots]
+        if previous is not None:
+            records = [optimizer._next_coefficients(self.compute, prepared[group], step + 1, fused, record)
+                       for (group, step, fused), record in zip(self.slots, previous)]
+        else:
+            records = [optimizer._coefficients(self.compute, prepared[group], step + 1, fused)
+                       for group, step, fused in self.slots]
+        self.records = records
         transform = self.member_grads[0]._pending
         self.backend.adamw_multi(self.plan, (self.record_type * len(records))(*records),
                                  None if transform is None else make_xform(transform))
