@@ -150,21 +150,22 @@ __global__ __launch_bounds__(kBlock) void grad_accumulate_any_kernel(const DevTe
     }
 }
 
-template <class D, class S, bool ASSIGN>
-static void launch_accumulate(const nt_plan *plan, hipStream_t s) {
+template <class D, class S>
+static void launch_accumulate(const nt_plan *plan, hipStream_t s, bool assign) {
     const int32_t shift = split_shift(plan, kTile);
-    grad_accumulate_kernel<D, S, ASSIGN><<<dim3((unsigned)(plan->ntasks << shift)), dim3(kBlock), 0, s>>>(
-        plan->d_tensors, plan->d_tasks, plan->chunk, shift);
+    const dim3 grid((unsigned)(plan->ntasks << shift));
+    if (assign)
+        grad_accumulate_kernel<D, S, true><<<grid, dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, plan->chunk, shift);
+    else
+        grad_accumulate_kernel<D, S, false><<<grid, dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, plan->chunk, shift);
 }
 
 template <class D>
 static bool dispatch_source(int32_t src, const nt_plan *plan, hipStream_t s, bool assign) {
     switch (src) {
-        case NT_F32: assign ? launch_accumulate<D, TF32, true>(plan, s) : launch_accumulate<D, TF32, false>(plan, s); return true;
-        case NT_F16: assign ? launch_accumulate<D, TF16, true>(plan, s) : launch_accumulate<D, TF16, false>(plan, s); return true;
-        case NT_BF16:
-            assign ? launch_accumulate<D, TBF16, true>(plan, s) : launch_accumulate<D, TBF16, false>(plan, s);
-            return true;
+        case NT_F32: launch_accumulate<D, TF32>(plan, s, assign); return true;
+        case NT_F16: launch_accumulate<D, TF16>(plan, s, assign); return true;
+        case NT_BF16: launch_accumulate<D, TBF16>(plan, s, assign); return true;
         default: return false;
     }
 }

@@ -113,15 +113,16 @@ def _zeros_views(shapes, dtype: DType, device) -> list:
             for offset, count, shape in zip(offsets, counts, shapes)]
 
 
-def _pack_state_buffers(states, names) -> None:
-    """Move the device buffers `names` of every state dictionary into one
-    flat allocation per (name, device, dtype), values unchanged.  A buffer
-    object held under several names or states stays one object."""
+def _pack_state_buffers(states, names, keep=frozenset()) -> None:
+    """Move the buffers `names` of every state dictionary into one flat
+    allocation per (name, device, dtype), values unchanged; buffers whose id
+    is in `keep` stay where they are.  A buffer object held under several
+    names or states stays one object."""
     for name in names:
         groups: dict = {}
         for values in states:
             buffer = values.get(name)
-            if isinstance(buffer, Tensor) and not buffer._requires_grad:
+            if isinstance(buffer, Tensor) and not buffer._requires_grad and id(buffer) not in keep:
                 groups.setdefault((buffer._device, buffer._dtype), {})[id(buffer)] = buffer
         for (device, dtype), unique in groups.items():
             if len(unique) < 2:
@@ -161,8 +162,12 @@ class _FirstOrderOptimizer(Optimizer):
         super()._install_loaded_state(defaults, param_groups, state)
 
     def to(self, device):
+        # Buffers already on `device` are kept as they are (Tensor.to returns
+        # them); only the moved copies are packed.
+        before = [value for values in self.state.values() if isinstance(values, dict)
+                  for value in values.values() if isinstance(value, Tensor)]
         moved = super().to(device)
-        _pack_state_buffers(list(self.state.values()), self._state_buffers)
+        _pack_state_buffers(list(self.state.values()), self._state_buffers, keep={id(value) for value in before})
         return moved
 
     def _state_dtype(self, parameter: Tensor, name: str) -> DType:

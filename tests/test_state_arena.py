@@ -155,3 +155,39 @@ def test_a_single_fresh_parameter_keeps_its_own_allocation():
     optimizer.step()
     assert set(optimizer.state[id(params[4])]) == {"exp_avg", "exp_avg_sq", "step"}
     assert optimizer.state[id(params[4])]["exp_avg"]._storage.storage_offset() == 0
+
+
+def test_moving_to_the_same_device_keeps_every_buffer_object():
+    rng = np.random.default_rng(7)
+    params = _model(rng)
+    optimizer = AdamW(params, lr=1e-2)
+    for parameter in params:                                     # one allocation per buffer
+        optimizer._buffers(parameter, optimizer.state[id(parameter)])
+        optimizer.state[id(parameter)]["step"] = 1
+    before = {id(parameter): dict(optimizer.state[id(parameter)]) for parameter in params}
+    optimizer.to("cpu")
+    for parameter in params:
+        for name in ("exp_avg", "exp_avg_sq"):
+            assert optimizer.state[id(parameter)][name] is before[id(parameter)][name]
+
+
+@pytest.mark.gpu
+def test_state_moved_to_the_device_is_packed_with_values_kept():
+    rng = np.random.default_rng(8)
+    params = _model(rng, device=DEV)
+    optimizer = AdamW(params, lr=1e-2)
+    host = {}
+    for parameter in params:
+        values = {name: nt.Tensor(rng.standard_normal(parameter.shape).astype(np.float32))
+                  for name in ("exp_avg", "exp_avg_sq")}
+        values["exp_avg_sq"] = nt.Tensor(np.abs(values["exp_avg_sq"].numpy()))
+        values["step"] = 2
+        optimizer.state[id(parameter)] = values
+        host[id(parameter)] = {name: values[name].numpy().copy() for name in ("exp_avg", "exp_avg_sq")}
+    optimizer.to(DEV)
+    for name in ("exp_avg", "exp_avg_sq"):
+        assert len({_base(optimizer.state[id(parameter)][name]) for parameter in params}) == 1
+        for parameter in params:
+            moved = optimizer.state[id(parameter)][name]
+            assert moved.device == nt.Device(DEV)
+            assert np.array_equal(moved.numpy(), host[id(parameter)][name])
