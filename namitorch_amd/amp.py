@@ -18,6 +18,8 @@ from __future__ import annotations
 import ctypes
 import math
 import operator
+from collections import deque
+from itertools import repeat
 from operator import attrgetter, eq, is_, itemgetter
 from numbers import Real
 
@@ -450,11 +452,11 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     # unscale_ rewrites every gradient (one version bump); the clip may (one
     # more, undone on reconcile if the device decides not to clip).
     bumps = int(amp) + int(maximum is not None)
-    for gradient in gradients:
-        gradient._pending = transform
-        counter = gradient._version_counter
+    deque(map(setattr, gradients, repeat("_pending"), repeat(transform)), 0)
+    counters = tuple(map(_COUNTER, gradients))
+    for counter in counters:
         counter.value += bumps
-        gradient._finite_version = counter.value
+    deque(map(setattr, gradients, repeat("_finite_version"), map(_VALUE, counters)), 0)
     if maximum is not None:
         clip_bumps.extend(zip(gradients, map(_VALUE, map(_COUNTER, gradients))))
     plan = backend.grad_plan(gradients, dtype)

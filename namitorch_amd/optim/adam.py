@@ -386,7 +386,7 @@ class _Replay:
     __slots__ = ("registered_cache", "registered", "requires", "grads", "state", "ids", "dicts", "lens", "firsts",
                  "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
                  "second_counters", "fused_options", "enabled", "validate", "slots", "backend", "plan", "compute",
-                 "record_type", "moment_pairs", "move_counters", "member_groups", "bumped", "stream", "options_key",
+                 "record_type", "moment_buffers", "moment_counters", "move_counters", "member_groups", "bumped", "stream", "options_key",
                  "prepared", "adoptable", "spans", "sizes", "records")
 
     def __init__(self, optimizer, cached, group_index, backend, plan, compute, slot_specs, member_slots, bookkeeping):
@@ -423,9 +423,9 @@ class _Replay:
         self.compute = compute
         self.record_type = _native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs
         self.bumped = tuple(bool(not entry[6] or entry[0]._numel) for entry in bookkeeping)
-        self.moment_pairs = tuple((buffer, buffer._version_counter)
-                                  for entry, bumped in zip(bookkeeping, self.bumped) if bumped
-                                  for buffer in (entry[2], entry[3]))
+        self.moment_buffers = tuple(buffer for entry, bumped in zip(bookkeeping, self.bumped) if bumped
+                                    for buffer in (entry[2], entry[3]))
+        self.moment_counters = tuple(map(_COUNTER, self.moment_buffers))
         moving: list = [[] for _ in groups]
         for entry, bumped, group in zip(bookkeeping, self.bumped, self.member_groups):
             if bumped:
@@ -548,9 +548,9 @@ class _Replay:
                                  None if transform is None else make_xform(transform))
         # Bookkeeping of the full step: moments always, parameter (and master)
         # only for groups whose lr is nonzero, then the step counts.
-        for buffer, counter in self.moment_pairs:
+        for counter in self.moment_counters:
             counter.value += 1
-            buffer._clean_version = counter.value
+        deque(map(setattr, self.moment_buffers, repeat("_clean_version"), map(_VALUE, self.moment_counters)), 0)
         moves = [options["lr"] != 0 for options in prepared]
         for group, counters in enumerate(self.move_counters):
             if moves[group]:

@@ -142,10 +142,12 @@ _DTYPE = attrgetter("_dtype")
 def _device_groups(gradients) -> dict:
     """Gradients grouped by (backend, dtype), in order."""
     if gradients:
-        # Common case: one device and one dtype (C-level passes only).
-        devices = set(map(_DEVICE, gradients))
-        if len(set(map(_DTYPE, gradients))) == 1 and len(devices) == 1:
-            first = gradients[0]
+        # Common case: one device and one dtype, checked by identity in
+        # C-level passes (Tensors share one Device object per device, and
+        # dtypes are singletons).
+        first = gradients[0]
+        if (all(map(is_, map(_DEVICE, gradients), repeat(first._device)))
+                and all(map(is_, map(_DTYPE, gradients), repeat(first._dtype)))):
             return {(get_backend(first), first._dtype): list(gradients)}
     groups: dict = {}
     for gradient in gradients:
