@@ -191,3 +191,22 @@ def test_state_moved_to_the_device_is_packed_with_values_kept():
             moved = optimizer.state[id(parameter)][name]
             assert moved.device == nt.Device(DEV)
             assert np.array_equal(moved.numpy(), host[id(parameter)][name])
+
+
+def test_bulk_creation_groups_by_dtype():
+    rng = np.random.default_rng(12)
+    params = [nt.Parameter(rng.standard_normal(shape).astype(np.float32), dtype=dtype)
+              for shape, dtype in zip(SHAPES, ("float32", "float16", "float64", "float32", "float16", "float64"))]
+    bulk = AdamW(params, lr=1e-2)
+    bulk._create_buffers(params)
+    single = AdamW(params, lr=1e-2)
+    for parameter in params:
+        single._buffers(parameter, single.state[id(parameter)])
+    for name in ("exp_avg", "exp_avg_sq"):
+        for dtype in ("float32", "float16", "float64"):
+            members = [parameter for parameter in params if parameter.dtype.name == dtype]
+            assert len({_base(bulk.state[id(parameter)][name]) for parameter in members}) == 1
+        for parameter in params:
+            x, y = bulk.state[id(parameter)][name], single.state[id(parameter)][name]
+            assert x.dtype is y.dtype is parameter.dtype and x.shape == y.shape
+            assert np.array_equal(x.numpy().view(np.uint8), y.numpy().view(np.uint8))
