@@ -143,7 +143,8 @@ typedef struct nt_plan nt_plan; /* opaque multi-tensor plan */
 /* Thread-local message of the last failing call ("" if none). */
 const char *nt_last_error(void);
 
-/* ABI version of this library (bumped when a struct layout changes). */
+/* ABI version of this library (bumped when a struct layout or an entry
+ * point's signature changes). */
 int32_t nt_abi_version(void);
 
 /* Number of visible HIP devices. */
@@ -244,9 +245,13 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale,
  * sets skip = found_inf and scale_used = scale.  With
  * NT_FINALIZE_SCALER_UPDATE the GradScaler state machine of amp.py:225-233
  * then runs on the device, advancing ctrl->scale and ctrl->growth_tracker.
+ * `carry` (may be NULL; never equal to `ctrl`): the scaler state starts
+ * from *carry as nt_ctrl_carry(ctrl, carry) would set it, so a new
+ * iteration's block needs no carry launch; with NULL it starts from *ctrl.
+ * The pre-pass of such an iteration reads the scale from `carry`'s block.
  */
-int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type,
-                        double max_norm, int32_t flags,
+int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry,
+                        double norm_type, double max_norm, int32_t flags,
                         double growth_factor, double backoff_factor,
                         int32_t growth_interval, void *stream);
 

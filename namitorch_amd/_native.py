@@ -28,7 +28,7 @@ NT_F64 = 3
 NT_MAX_SLOTS = 16
 NT_FINALIZE_SCALER_UPDATE = 1
 NT_FINALIZE_CLIP_IF_FINITE = 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 c_void_p = ctypes.c_void_p
 c_int32 = ctypes.c_int32
@@ -129,7 +129,8 @@ SIGNATURES = {
     "nt_plan_info": (c_int32, [c_void_p, ctypes.POINTER(c_uint64), ctypes.POINTER(c_int32), ctypes.POINTER(c_int64)]),
     "nt_adamw_mt": (c_int32, [c_void_p, c_void_p, c_int32, ctypes.POINTER(GradXform), c_void_p]),
     "nt_amp_prepass": (c_int32, [c_void_p, c_float, c_int32, c_void_p, c_void_p]),
-    "nt_amp_finalize": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_int32, c_double, c_double, c_int32, c_void_p]),
+    "nt_amp_finalize": (c_int32, [c_void_p, c_void_p, c_void_p, c_double, c_double, c_int32, c_double, c_double, c_int32,
+                                  c_void_p]),
     "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_void_p]),
     "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
     "nt_grad_zero": (c_int32, [c_void_p, c_void_p]),

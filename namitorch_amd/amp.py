@@ -430,13 +430,16 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     (backend, dtype), _ = next(iter(groups.items()))
     if backend.adamw is None:
         backend._unsupported("Optimizer steps")
+    # This step's block is written whole by the finalize, which starts from
+    # the previous block's scaler state (or a neutral one without a scaler);
+    # the pre-pass reads the loss scale from the previous block.
     if amp:
         previous = scaler._device_blocks.get(backend)
         if previous is None or not scaler._device_steps:
             previous = backend.new_ctrl(scaler._scale, scaler._growth_tracker)
-        block = backend.carry_ctrl(previous)
     else:
-        block = backend.new_ctrl()
+        previous = backend.neutral_ctrl()
+    block = backend.empty_ctrl()
     clip_bumps: list = []
     device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps)
     device_step.clip_requested = maximum is not None
@@ -460,11 +463,11 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     if maximum is not None:
         clip_bumps.extend(zip(gradients, map(_VALUE, map(_COUNTER, gradients))))
     plan = backend.grad_plan(gradients, dtype)
-    backend.grad_prepass(plan, None, block.data_ptr(), unscale=amp)
+    backend.grad_prepass(plan, None, previous.data_ptr(), unscale=amp)
     flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)
     backend.grad_finalize(plan, block.data_ptr(), order, -1.0 if maximum is None else maximum, flags,
-                          growth, backoff, interval)
+                          growth, backoff, interval, carry_ptr=previous.data_ptr())
     device_step.capture()
     if amp:
         scaler._reconcile()                               # earlier fused steps: their finalize already ran

@@ -135,6 +135,7 @@ class HIPBackend:
         self._plans: OrderedDict = OrderedDict()
         self._lock = threading.RLock()
         self._side_stream = None
+        self._neutral_ctrl = None
         _backends_alive.add(self)
 
     def __repr__(self):
@@ -250,9 +251,12 @@ class HIPBackend:
                          int(unscale or scale is not None), ctrl_ptr, self.stream())
 
     def grad_finalize(self, plan: Plan, ctrl_ptr: int, norm_type: float = 2.0, max_norm: float = -1.0,
-                      flags: int = 0, growth: float = 2.0, backoff: float = 0.5, interval: int = 2000) -> None:
+                      flags: int = 0, growth: float = 2.0, backoff: float = 0.5, interval: int = 2000,
+                      carry_ptr: int | None = None) -> None:
+        """Finalize into `ctrl_ptr`; with `carry_ptr` the block starts from
+        that block's scaler state (no separate carry launch)."""
         with self.context():
-            _native.call("nt_amp_finalize", plan.handle, ctrl_ptr, norm_type, max_norm, int(flags),
+            _native.call("nt_amp_finalize", plan.handle, ctrl_ptr, carry_ptr, norm_type, max_norm, int(flags),
                          growth, backoff, interval, self.stream())
 
     def grad_norm_pow(self, plan: Plan, ctrl_ptr: int, norm_type: float, max_norm: float,
@@ -275,6 +279,21 @@ class HIPBackend:
     def reset_ctrl(self, block: torch.Tensor, scale: float, growth_tracker: int = 0) -> None:
         with self.context():
             _native.call("nt_ctrl_reset", block.data_ptr(), scale, growth_tracker, self.stream())
+
+    def empty_ctrl(self) -> torch.Tensor:
+        """Device memory for a control block that a finalize will write whole."""
+        return torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, device=self.device.torch)
+
+    def neutral_ctrl(self) -> torch.Tensor:
+        """A block with scale 1 and no history, kept per backend: the carry
+        source of steps without a GradScaler.  Nothing writes it after set-up."""
+        with self._lock:
+            if self._neutral_ctrl is None:
+                block = self.new_ctrl()
+                with self.context():
+                    torch.cuda.current_stream(self.device.index).synchronize()   # readable from any stream
+                self._neutral_ctrl = block
+            return self._neutral_ctrl
 
     def carry_ctrl(self, previous: torch.Tensor) -> torch.Tensor:
         """A new control block that continues `previous`'s scaler state."""

@@ -402,8 +402,25 @@ __device__ __forceinline__ void scaler_update(nt_amp_ctrl *c, int found, double 
     }
 }
 
+// A new iteration's block continuing `s`'s scaler state: scale,
+// growth_tracker, iterations and skipped carry over, every per-iteration
+// field starts cleared (clip_coef 1).
+__device__ __forceinline__ nt_amp_ctrl carried_ctrl(const nt_amp_ctrl &s) {
+    nt_amp_ctrl c{};
+    c.scale = s.scale;
+    c.scale_used = s.scale;
+    c.growth_tracker = s.growth_tracker;
+    c.iterations = s.iterations;
+    c.skipped = s.skipped;
+    c.clip_coef = 1.0;
+    return c;
+}
+
+// `carry` (optional): start from carried_ctrl(*carry) instead of *ctrl, so a
+// new iteration's block needs no separate carry kernel.
 __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restrict__ partials, int64_t n,
-                                                          nt_amp_ctrl *ctrl, double norm_type, double max_norm,
+                                                          nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry,
+                                                          double norm_type, double max_norm,
                                                           int32_t flags, double growth, double backoff,
                                                           int32_t interval) {
     Acc r = reduce_partials(partials, 0, n);
@@ -417,7 +434,7 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restr
     else if (r.inf) norm = infv;
     else if (r.amax == 0.0 || __builtin_isinf(norm_type)) norm = r.amax;
     else norm = __builtin_sqrt(r.sumsq);   // p == 2; other p: nt_grad_norm_pow
-    nt_amp_ctrl c = *ctrl;
+    nt_amp_ctrl c = carry != nullptr ? carried_ctrl(*carry) : *ctrl;
     c.sumsq = r.sumsq;
     c.amax = r.amax;
     c.norm = norm;
@@ -566,15 +583,7 @@ __global__ __launch_bounds__(kBlock) void grad_apply_f64_kernel(const DevTensor 
 
 __global__ void ctrl_carry_kernel(nt_amp_ctrl *dst, const nt_amp_ctrl *src) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    const nt_amp_ctrl s = *src;
-    nt_amp_ctrl c{};
-    c.scale = s.scale;
-    c.scale_used = s.scale;
-    c.growth_tracker = s.growth_tracker;
-    c.iterations = s.iterations;
-    c.skipped = s.skipped;
-    c.clip_coef = 1.0;
-    *dst = c;
+    *dst = carried_ctrl(*src);
 }
 
 __global__ void ctrl_reset_kernel(nt_amp_ctrl *ctrl, float scale, int32_t tracker) {
@@ -696,12 +705,14 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale, const nt_amp
     return NT_OK;
 }
 
-int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, double max_norm, int32_t flags,
-                        double growth_factor, double backoff_factor, int32_t growth_interval, void *stream) {
+int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry, double norm_type,
+                        double max_norm, int32_t flags, double growth_factor, double backoff_factor,
+                        int32_t growth_interval, void *stream) {
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
     if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
+    if (carry == ctrl) return fail(NT_ERR_VALUE, "nt_amp_finalize: carry and ctrl must be different blocks");
     if (!(norm_type > 0.0)) return fail(NT_ERR_VALUE, "norm_type must be positive or positive infinity.");
     if (flags & ~(NT_FINALIZE_SCALER_UPDATE | NT_FINALIZE_CLIP_IF_FINITE))
         return fail(NT_ERR_VALUE, "nt_amp_finalize: unknown flags");
@@ -713,7 +724,7 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, doub
     const Partial *src = plan->nstage2 > 0 ? plan->d_partials2 : plan->d_partials;
     const int64_t count = plan->nstage2 > 0 ? plan->nstage2 : plan->npartials;
     finalize_kernel<<<dim3(1), dim3(kBlock), 0, (hipStream_t)stream>>>(
-        src, count, ctrl, norm_type, max_norm, flags, growth_factor,
+        src, count, ctrl, carry, norm_type, max_norm, flags, growth_factor,
         backoff_factor, growth_interval);
     NT_LAUNCH_CHECK("finalize_kernel launch");
     return NT_OK;
