@@ -295,13 +295,6 @@ class HIPBackend:
                 self._neutral_ctrl = block
             return self._neutral_ctrl
 
-    def carry_ctrl(self, previous: torch.Tensor) -> torch.Tensor:
-        """A new control block that continues `previous`'s scaler state."""
-        block = torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, device=self.device.torch)
-        with self.context():
-            _native.call("nt_ctrl_carry", block.data_ptr(), previous.data_ptr(), self.stream())
-        return block
-
     def read_ctrl(self, block: torch.Tensor) -> _native.AmpCtrl:
         out = _native.AmpCtrl()
         with self.context():
