@@ -216,3 +216,39 @@ def test_comparison_detects_a_memo_that_ignores_option_changes(monkeypatch):
         patch.setattr(adam_mod, "_options_key", lambda groups: ("unchanging",))
         stale = _run(patch, memo=True)
     assert stale[0] != full[0]
+
+
+def test_next_coefficients_equal_a_full_computation():
+    """The replay rebuilds each coefficient record from the previous step's by
+    recomputing the two bias corrections; every field must equal what
+    ``_coefficients`` computes from scratch, and the same errors must rise."""
+    import ctypes
+    import random
+
+    from namitorch_amd import dtype as dtypes
+    from namitorch_amd.optim.adam import AdamW
+
+    optimizer = AdamW([nt.Parameter(np.zeros(4, np.float32))], lr=1e-3)
+    rng = random.Random(5)
+    for trial in range(300):
+        dtype = rng.choice([dtypes.float32, dtypes.float16, dtypes.float64])
+        options = {"lr": rng.choice([0.0, 1e-3, 3e-4, rng.random()]), "betas": (rng.random() * 0.999, rng.random() * 0.9999),
+                   "eps": rng.choice([1e-8, 1e-6, 1e-3]), "weight_decay": rng.choice([0.0, 0.1, 0.01]),
+                   "maximize": rng.random() < 0.2}
+        fused = rng.random() < 0.5
+        step = rng.choice([1, 2, 3, 10, 1000, 100000])
+        try:
+            previous = optimizer._coefficients(dtype, options, step, fused)
+        except ValueError:
+            continue
+        for later in (step + 1, step + 7):
+            try:
+                want = optimizer._coefficients(dtype, options, later, fused)
+            except ValueError as error:
+                with pytest.raises(ValueError, match=str(error)):
+                    optimizer._next_coefficients(dtype, options, later, fused, previous)
+                continue
+            got = optimizer._next_coefficients(dtype, options, later, fused, previous)
+            assert type(got) is type(want)
+            assert bytes(got) == bytes(want), (trial, dtype, options, later)
+            assert ctypes.addressof(got) != ctypes.addressof(previous)
