@@ -41,6 +41,7 @@ _FLOATING = attrgetter("_floating")
 _FIRST_OF = itemgetter(0)
 _SECOND_OF = itemgetter(1)
 _PARAMETER_AND_GRADIENT = itemgetter(1, 2)
+_THIRD_OF = itemgetter(2)
 _FINITE_VERSION = attrgetter("_finite_version")
 _VERSION_VALUE = attrgetter("_version_counter.value")
 
@@ -247,9 +248,18 @@ class GradScaler:
         entries = optimizer._grad_entries() if callable(getattr(optimizer, "_grad_entries", None)) \
             else tuple(optimizer._parameters_with_grad())
         gradients = tuple(map(_PARAMETER_AND_GRADIENT, entries))
-        if any(map(_REQUIRES, map(_SECOND_OF, gradients))) or not all(
-                map(_FLOATING, map(_DTYPE, map(_FIRST_OF, gradients)))):
+        if any(map(_REQUIRES, map(_THIRD_OF, entries))):
             raise RuntimeError("GradScaler requires detached floating gradients.")
+        # Parameter dtypes never change: the floating check is skipped while
+        # the entries come from the memo (which fixes the parameters) that
+        # passed it last.
+        attributes = getattr(optimizer, "__dict__", None)
+        served = attributes.get("_entries_served") if attributes is not None else None
+        if served is None or attributes.get("_floating_checked") is not served:
+            if not all(map(_FLOATING, map(_DTYPE, map(_SECOND_OF, entries)))):
+                raise RuntimeError("GradScaler requires detached floating gradients.")
+            if served is not None:
+                attributes["_floating_checked"] = served
         return gradients
 
     @staticmethod
@@ -418,7 +428,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     if order != 2.0 and not math.isinf(order):
         raise ValueError("fused_step supports norm_type 2 and inf; use clip_grad_norm_ for other norms.")
     pairs = GradScaler._gradients(optimizer)
-    gradients = [gradient for _, gradient in pairs]
+    gradients = list(map(_SECOND_OF, pairs))
     if not gradients:
         raise RuntimeError("No gradients were found for this optimizer.")
     groups = _device_groups(gradients)

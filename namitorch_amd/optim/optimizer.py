@@ -290,15 +290,18 @@ class Optimizer:
         memo = self.__dict__.get("_entries_memo")
         if (memo is not None and memo[0] is cache and memo[1] == requires and memo[2] == present
                 and all(map(is_, compress(grads, present), map(_CALL_REF, memo[3])))):
+            self.__dict__["_entries_served"] = memo    # these entries follow this memo
             return tuple(zip(memo[4], memo[5], compress(grads, memo[6])))
+        self.__dict__["_entries_served"] = None
         entries = self._bulk_entries(registered, requires, grads)
         if entries is None:
             entries = tuple(self._parameters_with_grad())
         if cache is not None and self.__dict__.get("_registered_cache") is cache:
             refs = tuple(map(weakref.ref, compress(grads, present)))
             mask = tuple(map(and_, requires, present))
-            self.__dict__["_entries_memo"] = (cache, requires, present, refs, tuple(map(_FIRST_OF, entries)),
-                                              tuple(map(_SECOND_OF, entries)), mask)
+            memo = (cache, requires, present, refs, tuple(map(_FIRST_OF, entries)),
+                    tuple(map(_SECOND_OF, entries)), mask)
+            self.__dict__["_entries_memo"] = self.__dict__["_entries_served"] = memo
         return entries
 
     def zero_grad(self, set_to_none: bool = True) -> None:
