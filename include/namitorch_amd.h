@@ -41,6 +41,16 @@ extern "C" {
 #define NT_FINALIZE_SCALER_UPDATE 1   /* advance scale/growth tracker (amp.py:225-233) */
 #define NT_FINALIZE_CLIP_IF_FINITE 2  /* clip only when no grad is non-finite (runner.py:249) */
 
+/* ---- nt_grad_norm_pow flags -------------------------------------------- */
+/* p = 2 only: run the prescaled sum only when max|g| lies outside
+ * [2^-480, 2^480], where the finalize's sqrt(sum g^2) can overflow or lose
+ * bits in fp64 (float64 gradients); otherwise leave the block unchanged. */
+#define NT_NORM_POW_GUARD 1
+
+/* ---- nt_tensor_scalar operations --------------------------------------- */
+#define NT_OP_MUL 0
+#define NT_OP_DIV 1
+
 /* ---- multi-tensor plan limits ------------------------------------------ */
 #define NT_MAX_SLOTS 16     /* coefficient sets per nt_adamw_mt launch */
 
@@ -256,15 +266,18 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *car
                         int32_t growth_interval, void *stream);
 
 /*
- * General p-norm (0 < p < inf, p != 2) of optim/clip_grad.py:70-79:
- * sum over grads of (|g'|/amax)^p in fp64, with amax from the previous
- * prepass already in `ctrl`; leaves the norm in ctrl->norm, the raw sum
- * in ctrl->sumsq and, with max_norm >= 0, the clip coefficient.  A
+ * General p-norm (0 < p < inf) of optim/clip_grad.py:70-79: sum over
+ * grads of (|g'|/amax)^p in fp64, with amax from the previous prepass
+ * already in `ctrl`; leaves the norm in ctrl->norm, the raw sum in
+ * ctrl->sumsq and, with max_norm >= 0, the clip coefficient.  A
  * non-finite or zero amax leaves the block as nt_amp_finalize wrote it.
+ * p = 2 is the finalize's own case except for float64 gradients whose
+ * squares leave the fp64 range: NT_NORM_POW_GUARD runs the pass only then,
+ * deciding on the device (no host round trip).
  */
 int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type,
                          double max_norm, float scale, int32_t unscale,
-                         int32_t scale_from_ctrl, void *stream);
+                         int32_t scale_from_ctrl, int32_t flags, void *stream);
 
 /*
  * Write the transformed grads back in place: the deferred form of
@@ -308,13 +321,22 @@ int32_t nt_grad_accumulate(nt_plan *plan, int32_t assign, void *stream);
 /* ---- small single-array kernels ---------------------------------------- */
 
 /*
- * out[i] = to_dtype(in[i] * scale) for a loss of `count` elements
- * (GradScaler.scale, amp.py:137-138: loss * self._scale); with
- * `ctrl != NULL` the scale is ctrl->scale.
+ * out[i] = in[i] * operand (NT_OP_MUL) or in[i] / operand (NT_OP_DIV),
+ * computed in `out_dtype` and rounded once to it: Tensor.__mul__ and
+ * Tensor.__truediv__ with a scalar operand (tensor.py:814-823 through
+ * _binary_operation, tensor.py:634-646, and binary_forward,
+ * _backend.py:54-72).  The caller promotes as the reference does
+ * (dtype.py:99-109, 204-208: a Python float is float32, so a float16 loss
+ * times the loss scale is float32) and passes the operand already rounded
+ * to `out_dtype`; `in_dtype` must widen exactly into `out_dtype`.  This is
+ * GradScaler.scale (amp.py:137-138: loss * self._scale) and the training
+ * loop's loss / grad_accum_steps (training/runner.py:246).  With
+ * `ctrl != NULL` the operand is ctrl->scale (the loss scale held on the
+ * device after a fused step).
  */
-int32_t nt_scale_array(const void *in, void *out, int32_t dtype,
-                       double scale, const nt_amp_ctrl *ctrl, uint64_t count,
-                       void *stream);
+int32_t nt_tensor_scalar(const void *in, int32_t in_dtype, void *out,
+                         int32_t out_dtype, double operand, int32_t op,
+                         const nt_amp_ctrl *ctrl, uint64_t count, void *stream);
 
 /*
  * *flag = 1 if any element of `array` is < 0 (the exp_avg_sq check of

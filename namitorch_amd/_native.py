@@ -28,7 +28,10 @@ NT_F64 = 3
 NT_MAX_SLOTS = 16
 NT_FINALIZE_SCALER_UPDATE = 1
 NT_FINALIZE_CLIP_IF_FINITE = 2
-ABI_VERSION = 2
+ABI_VERSION = 3
+NT_NORM_POW_GUARD = 1
+NT_OP_MUL = 0
+NT_OP_DIV = 1
 
 c_void_p = ctypes.c_void_p
 c_int32 = ctypes.c_int32
@@ -131,14 +134,14 @@ SIGNATURES = {
     "nt_amp_prepass": (c_int32, [c_void_p, c_float, c_int32, c_void_p, c_void_p]),
     "nt_amp_finalize": (c_int32, [c_void_p, c_void_p, c_void_p, c_double, c_double, c_int32, c_double, c_double, c_int32,
                                   c_void_p]),
-    "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_void_p]),
+    "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_int32, c_void_p]),
     "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
     "nt_grad_zero": (c_int32, [c_void_p, c_void_p]),
     "nt_plan_set_pointers": (c_int32, [c_void_p, c_int32, ctypes.POINTER(c_void_p), c_int32, c_void_p]),
     "nt_grad_accumulate": (c_int32, [c_void_p, c_int32, c_void_p]),
     "nt_ctrl_reset": (c_int32, [c_void_p, c_float, c_int32, c_void_p]),
     "nt_ctrl_carry": (c_int32, [c_void_p, c_void_p, c_void_p]),
-    "nt_scale_array": (c_int32, [c_void_p, c_void_p, c_int32, c_double, c_void_p, c_uint64, c_void_p]),
+    "nt_tensor_scalar": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_double, c_int32, c_void_p, c_uint64, c_void_p]),
     "nt_any_negative": (c_int32, [c_void_p, c_int32, c_uint64, c_void_p, c_void_p]),
     "nt_stream_probe": (c_int32, [ctypes.POINTER(c_void_p), c_int32, c_int32, ctypes.POINTER(c_void_p), c_int32, c_int32,
                                   c_uint64, c_void_p]),

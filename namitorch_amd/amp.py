@@ -28,8 +28,9 @@ import numpy as np
 from . import _native
 from .backends import get_backend
 from .backends._graph_capture import reject_during_capture
+from .dtype import float32, float64, promote_with_scalar
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
-from .tensor import GradTransform, is_grad_enabled
+from .tensor import GradTransform, _unsettled_steps, is_grad_enabled
 
 _REQUIRES = attrgetter("_requires_grad")
 _WRITABLE = attrgetter("_writable")
@@ -65,6 +66,22 @@ class DeviceStep:
         self._ctrl = None
         self._reconciled = False
         self.scheduler = None                 # advanced at reconciliation iff the step updated
+        self.ready = None                     # event after the finalize, on `stream`
+        self.stream = None
+
+    def block_for_current_stream(self):
+        """The control block, safe to read from work queued next on the
+        caller's current stream: a different stream first waits for this
+        step's finalize, and the block is kept from reuse until that stream's
+        work completes."""
+        current = self.backend.stream()
+        if self.stream is not None and current != self.stream:
+            import torch
+            with self.backend.context():
+                stream = torch.cuda.current_stream(self.backend.device.index)
+                stream.wait_event(self.ready)
+                self.block.record_stream(stream)
+        return self.block
 
     def capture(self) -> None:
         """Queue the copy of the control block to pinned host memory.  The
@@ -75,6 +92,9 @@ class DeviceStep:
         with self.backend.context():
             ready = torch.cuda.Event()
             ready.record()
+            # Work on another stream that reads this block waits on `ready`.
+            self.ready = ready
+            self.stream = self.backend.stream()
             side = self.backend.side_stream()
             side.wait_event(ready)
             with torch.cuda.stream(side):
@@ -113,6 +133,10 @@ class DeviceStep:
                         gradient._finite_version = version - 1
         self.records.clear()
         self._reconciled = True
+        for position, pending in enumerate(_unsettled_steps):
+            if pending is self:
+                del _unsettled_steps[position]
+                break
         if self.scheduler is not None and not (self.honor_skip and ctrl.skip):
             self.scheduler._advance()         # training/runner.py:252-253: only after an update
 
@@ -180,7 +204,7 @@ class GradScaler:
         self._growth_tracker = 0
         self._optimizer_states: dict = {}
         self._scale_used = False
-        self._device_blocks: dict = {}       # backend -> latest control block (scale lives there)
+        self._device_blocks: dict = {}       # backend -> latest DeviceStep (its block holds the scale)
         self._device_steps: list = []        # fused steps not yet reflected in the host mirror
 
     @staticmethod
@@ -232,10 +256,14 @@ class GradScaler:
         if self._optimizer_states:
             raise RuntimeError("Call update() before scaling another loss after unscale_ or step.")
         backend = get_backend(loss)
-        block = self._device_blocks.get(backend) if self._device_steps else None
+        latest = self._device_blocks.get(backend) if self._device_steps else None
+        block = None if latest is None else latest.block_for_current_stream()
         if block is not None:
-            # The current scale lives on the device after a fused step.
-            result = backend.scale_tensor(loss, 1.0, ctrl=block)
+            # The current scale lives on the device after a fused step; the
+            # result dtype is loss * <Python float>'s (amp.py:138), e.g.
+            # float32 for a float16 loss.
+            result = backend.scalar_arithmetic(loss, 1.0, _native.NT_OP_MUL,
+                                               promote_with_scalar(loss.dtype, float32), ctrl=block)
         else:
             result = loss * self._scale
         self._scale_used = True
@@ -444,9 +472,11 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     # the previous block's scaler state (or a neutral one without a scaler);
     # the pre-pass reads the loss scale from the previous block.
     if amp:
-        previous = scaler._device_blocks.get(backend)
-        if previous is None or not scaler._device_steps:
+        latest = scaler._device_blocks.get(backend) if scaler._device_steps else None
+        if latest is None:
             previous = backend.new_ctrl(scaler._scale, scaler._growth_tracker)
+        else:
+            previous = latest.block_for_current_stream()
     else:
         previous = backend.neutral_ctrl()
     block = backend.empty_ctrl()
@@ -478,14 +508,21 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)
     backend.grad_finalize(plan, block.data_ptr(), order, -1.0 if maximum is None else maximum, flags,
                           growth, backoff, interval, carry_ptr=previous.data_ptr())
+    if dtype is float64 and order == 2.0:
+        # fp64 squares can overflow or underflow: where max|g| says they may
+        # have, the device redoes the norm with the reference's max-abs
+        # prescale (clip_grad.py:73-78) and refreshes the clip decision.
+        backend.grad_norm_pow(plan, block.data_ptr(), 2.0, -1.0 if maximum is None else maximum, None,
+                              scale_from_ctrl=amp, flags=_native.NT_NORM_POW_GUARD)
     device_step.capture()
     if amp:
         scaler._reconcile()                               # earlier fused steps: their finalize already ran
-        scaler._device_blocks[backend] = block
+        scaler._device_blocks[backend] = device_step
         scaler._device_steps.append(device_step)
         scaler._scale_used = False
     optimizer.step()                                      # the AdamW pass reads the control block
     optimizer.__dict__.setdefault("_device_steps", []).append(device_step)
+    _unsettled_steps.append(device_step)                  # version reads settle it first
     return StepResult(device_step)
 
 

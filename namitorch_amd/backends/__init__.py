@@ -51,8 +51,8 @@ class CPUBackend:
     def apply_grad_transform(self, tensors, transform):
         self._unsupported("Gradient unscale/clip")
 
-    def scale_tensor(self, tensor, scale):
-        self._unsupported("Loss scaling")
+    def scalar_arithmetic(self, tensor, operand, op, dtype, ctrl=None):
+        self._unsupported("Tensor arithmetic")
 
     def __repr__(self):
         return "CPUBackend()"

@@ -260,11 +260,11 @@ class HIPBackend:
                          growth, backoff, interval, self.stream())
 
     def grad_norm_pow(self, plan: Plan, ctrl_ptr: int, norm_type: float, max_norm: float,
-                      scale: float | None, scale_from_ctrl: bool = False) -> None:
+                      scale: float | None, scale_from_ctrl: bool = False, flags: int = 0) -> None:
         with self.context():
             _native.call("nt_grad_norm_pow", plan.handle, ctrl_ptr, norm_type, max_norm,
                          1.0 if scale is None else scale, int(scale is not None or scale_from_ctrl),
-                         int(scale_from_ctrl), self.stream())
+                         int(scale_from_ctrl), int(flags), self.stream())
 
     def grad_apply(self, plan: Plan, xform: _native.GradXform) -> None:
         with self.context():
@@ -335,14 +335,20 @@ class HIPBackend:
             plan = self.grad_plan(group, dtype)
             self.grad_apply(plan, make_xform(transform))
 
-    def scale_tensor(self, tensor, scale: float, ctrl: torch.Tensor | None = None):
+    def scalar_arithmetic(self, tensor, operand: float, op: int, dtype, ctrl: torch.Tensor | None = None):
+        """``tensor * operand`` (NT_OP_MUL) or ``tensor / operand`` (NT_OP_DIV)
+        computed in `dtype`, a new Tensor of that dtype; `operand` is already
+        a value of `dtype`.  With `ctrl` the operand is the loss scale held in
+        that control block."""
         from ..tensor import Tensor
-        if tensor.dtype.code == _native.NT_DTYPE_NONE:
-            raise TypeError("Only floating Tensors can be scaled on the device.")
-        out = torch.empty_like(tensor._data)
+        if tensor.dtype.code == _native.NT_DTYPE_NONE or dtype.code == _native.NT_DTYPE_NONE:
+            raise TypeError("Only floating Tensors support scalar arithmetic on the device.")
+        source = tensor._data
+        out = torch.empty(tuple(source.shape), dtype=dtype.torch_dtype, device=self.device.torch)
         with self.context():
-            _native.call("nt_scale_array", tensor._data.data_ptr(), out.data_ptr(), tensor.dtype.code, float(scale),
-                         None if ctrl is None else ctrl.data_ptr(), tensor.size, self.stream())
+            _native.call("nt_tensor_scalar", source.data_ptr(), tensor.dtype.code, out.data_ptr(), dtype.code,
+                         float(operand), int(op), None if ctrl is None else ctrl.data_ptr(), tensor.size,
+                         self.stream())
         return Tensor._from_storage(out, tensor.requires_grad)
 
     def any_negative(self, array: torch.Tensor, code: int) -> bool:

@@ -456,15 +456,31 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restr
     *ctrl = c;
 }
 
-// General p-norm second pass: sum of (|g'|/amax)^p in fp64.
+// With `guard`, the p = 2 prescaled pass runs only when the finalize's
+// sqrt(sum of g^2) may have lost accuracy: fp64 squares overflow above 2^511
+// and fall below the normal range under 2^-511, so the direct sum is kept
+// while max|g'| lies in [2^-480, 2^480] (float32, float16 and bfloat16
+// gradients always do).
+__device__ __forceinline__ bool direct_norm_exact(double amax) {
+    return amax >= 0x1p-480 && amax <= 0x1p480;
+}
+
+// (|g'|/amax)^p: NumPy's power with exponent 2 is the plain square.
+__device__ __forceinline__ double pow_term(double a, double p) { return p == 2.0 ? a * a : pow(a, p); }
+
+// General p-norm second pass: sum of (|g'|/amax)^p in fp64
+// (optim/clip_grad.py:73-76).
 template <class G>
 __global__ __launch_bounds__(kBlock) void norm_pow_kernel(const DevTensor *__restrict__ tensors,
                                                           const Task *__restrict__ tasks, int64_t ntasks,
                                                           int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
-                                                          int32_t scale_from_ctrl, double p,
+                                                          int32_t scale_from_ctrl, double p, int32_t guard,
                                                           double *__restrict__ partials) {
-    if (scale_from_ctrl && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale_used, xf.unscale, xf.inv_scale);
     const double s = ctrl->amax;
+    // The finalize already holds the norm when the prescale is non-finite or
+    // zero (clip_grad.py:71-72), and with `guard` when the direct sum is exact.
+    if (ctrl->found_inf || !(s > 0.0) || (guard && direct_norm_exact(s))) return;
+    if (scale_from_ctrl && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale_used, xf.unscale, xf.inv_scale);
     double acc = 0.0;
     for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
         const Task task = tasks[t];
@@ -474,7 +490,36 @@ __global__ __launch_bounds__(kBlock) void norm_pow_kernel(const DevTensor *__res
         const auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
         for (uint64_t i = start + threadIdx.x; i < end; i += kBlock) {
             const double a = __builtin_fabs((double)unscale_one<G>(load1<G>(gp, i), xf)) / s;
-            acc += pow(a, p);
+            acc += pow_term(a, p);
+        }
+    }
+    Acc in;
+    in.sumsq = acc;
+    Acc r = block_reduce(in);
+    if (threadIdx.x == 0) partials[blockIdx.x] = r.sumsq;
+}
+
+// float64 gradients: unscale divides in fp64 (amp.py:190-191 on a float64
+// array), then the same prescaled terms.
+__global__ __launch_bounds__(kBlock) void norm_pow_f64_kernel(const DevTensor *__restrict__ tensors,
+                                                              const Task *__restrict__ tasks, int64_t ntasks,
+                                                              int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
+                                                              int32_t scale_from_ctrl, double p, int32_t guard,
+                                                              double *__restrict__ partials) {
+    const double s = ctrl->amax;
+    if (ctrl->found_inf || !(s > 0.0) || (guard && direct_norm_exact(s))) return;
+    const double scale = scale_from_ctrl ? (double)ctrl->scale_used : (double)xf.scale;
+    double acc = 0.0;
+    for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
+        const Task task = tasks[t];
+        const DevTensor d = tensors[task.tensor];
+        const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
+        const uint64_t end = min(start + (uint64_t)chunk, d.numel);
+        const double *gp = reinterpret_cast<const double *>(d.grad);
+        for (uint64_t i = start + threadIdx.x; i < end; i += kBlock) {
+            double g = gp[i];
+            if (xf.unscale) g = g / scale;
+            acc += pow_term(__builtin_fabs(g) / s, p);
         }
     }
     Acc in;
@@ -484,16 +529,19 @@ __global__ __launch_bounds__(kBlock) void norm_pow_kernel(const DevTensor *__res
 }
 
 __global__ __launch_bounds__(kBlock) void norm_pow_finalize_kernel(const double *__restrict__ partials, int32_t n,
-                                                                   nt_amp_ctrl *ctrl, double p, double max_norm) {
+                                                                   nt_amp_ctrl *ctrl, double p, double max_norm,
+                                                                   int32_t guard) {
+    {
+        // Same early exits as the pass (block-uniform, before any partial is read).
+        const double s = ctrl->amax;
+        if (ctrl->found_inf || !(s > 0.0) || (guard && direct_norm_exact(s))) return;
+    }
     Acc acc;
     for (int32_t i = threadIdx.x; i < n; i += kBlock) acc.sumsq += partials[i];
     Acc r = block_reduce(acc);
     if (threadIdx.x != 0) return;
     nt_amp_ctrl c = *ctrl;
     const double s = c.amax;
-    // A non-finite or zero max-abs prescale is the norm itself; finalize
-    // already stored it (optim/clip_grad.py:71-72).
-    if (c.found_inf || !(s > 0.0)) return;
     double total = r.sumsq;
     double result = s * pow(total, 1.0 / p);
     if (!__builtin_isfinite(result)) result = exp(log(s) + log(total) / p);
@@ -596,18 +644,35 @@ __global__ void ctrl_reset_kernel(nt_amp_ctrl *ctrl, float scale, int32_t tracke
     *ctrl = c;
 }
 
-template <class T>
-__global__ __launch_bounds__(kBlock) void scale_array_kernel(const typename T::raw *in, typename T::raw *out,
-                                                             double scale, const nt_amp_ctrl *ctrl, uint64_t n) {
-    const double s = ctrl != nullptr ? (double)ctrl->scale : scale;
-    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
-        out[i] = T::from_f64((double)T::to_f32(in[i]) * s);
+// out = to_O(widen(in) op operand).  The operand is already a value of the
+// output (compute) dtype, and the input widens exactly into it, so one fp64
+// operation followed by one rounding is the compute dtype's correctly
+// rounded product or quotient: a product of two values of at most 24
+// significant bits is exact in fp64, and a quotient rounded to fp64 and then
+// to a format of p <= 24 bits rounds innocuously (53 >= 2p + 2).
+template <class I, class O>
+__global__ __launch_bounds__(kBlock) void tensor_scalar_kernel(const typename I::raw *in, typename O::raw *out,
+                                                               double operand, const nt_amp_ctrl *ctrl,
+                                                               int32_t op, uint64_t n) {
+    const double s = ctrl != nullptr ? (double)ctrl->scale : operand;
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock) {
+        const double x = widen64<I>(in[i]);
+        out[i] = O::from_f64(op == NT_OP_DIV ? x / s : x * s);
+    }
 }
-__global__ __launch_bounds__(kBlock) void scale_array_f64_kernel(const double *in, double *out, double scale,
-                                                                 const nt_amp_ctrl *ctrl, uint64_t n) {
-    const double s = ctrl != nullptr ? (double)ctrl->scale : scale;
-    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
-        out[i] = in[i] * s;
+
+template <class I>
+static int32_t launch_tensor_scalar(const void *in, void *out, int32_t out_dtype, double operand,
+                                    const nt_amp_ctrl *ctrl, int32_t op, uint64_t n, dim3 grid, hipStream_t s) {
+    const auto *src = static_cast<const typename I::raw *>(in);
+    switch (out_dtype) {
+        case NT_F32: tensor_scalar_kernel<I, TF32><<<grid, dim3(kBlock), 0, s>>>(src, (float *)out, operand, ctrl, op, n); break;
+        case NT_F16: tensor_scalar_kernel<I, TF16><<<grid, dim3(kBlock), 0, s>>>(src, (uint16_t *)out, operand, ctrl, op, n); break;
+        case NT_BF16: tensor_scalar_kernel<I, TBF16><<<grid, dim3(kBlock), 0, s>>>(src, (uint16_t *)out, operand, ctrl, op, n); break;
+        case NT_F64: tensor_scalar_kernel<I, TF64><<<grid, dim3(kBlock), 0, s>>>(src, (double *)out, operand, ctrl, op, n); break;
+        default: return fail(NT_ERR_TYPE, "nt_tensor_scalar: unsupported output dtype");
+    }
+    return NT_OK;
 }
 
 __global__ void clear_flag_kernel(int32_t *flag) {
@@ -731,15 +796,16 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *car
 }
 
 int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, double max_norm, float scale,
-                         int32_t unscale, int32_t scale_from_ctrl, void *stream) {
+                         int32_t unscale, int32_t scale_from_ctrl, int32_t flags, void *stream) {
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
     if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
     if (!(norm_type > 0.0) || __builtin_isinf(norm_type))
         return fail(NT_ERR_VALUE, "nt_grad_norm_pow needs a finite positive norm_type");
-    if (plan->layout.grad_dtype == NT_F64)
-        return fail(NT_ERR_TYPE, "general p-norm of float64 gradients is not supported on the device");
+    if (flags & ~NT_NORM_POW_GUARD) return fail(NT_ERR_VALUE, "nt_grad_norm_pow: unknown flags");
+    const int32_t guard_on = (flags & NT_NORM_POW_GUARD) ? 1 : 0;
+    if (guard_on && norm_type != 2.0) return fail(NT_ERR_VALUE, "nt_grad_norm_pow: the guard applies to norm_type 2 only");
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     nt_grad_xform hx{};
@@ -749,13 +815,20 @@ int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, dou
     if (unscale && scale_from_ctrl) xf.unscale = 1;
     hipStream_t s = (hipStream_t)stream;
     dim3 grid((unsigned)plan->pow_grid);
-    rc = grad_dispatch<NormPowL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
-                                 (const Task *)plan->d_tasks, plan->ntasks, plan->chunk, xf,
-                                 (const nt_amp_ctrl *)ctrl, scale_from_ctrl, norm_type, plan->d_pow_partials);
-    if (rc != NT_OK) return rc;
+    if (plan->layout.grad_dtype == NT_F64) {
+        norm_pow_f64_kernel<<<grid, dim3(kBlock), 0, s>>>(plan->d_tensors, plan->d_tasks, plan->ntasks, plan->chunk,
+                                                          xf, ctrl, scale_from_ctrl, norm_type, guard_on,
+                                                          plan->d_pow_partials);
+    } else {
+        rc = grad_dispatch<NormPowL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
+                                     (const Task *)plan->d_tasks, plan->ntasks, plan->chunk, xf,
+                                     (const nt_amp_ctrl *)ctrl, scale_from_ctrl, norm_type, guard_on,
+                                     plan->d_pow_partials);
+        if (rc != NT_OK) return rc;
+    }
     NT_LAUNCH_CHECK("norm_pow_kernel launch");
     norm_pow_finalize_kernel<<<dim3(1), dim3(kBlock), 0, s>>>(plan->d_pow_partials, plan->pow_grid, ctrl,
-                                                              norm_type, max_norm);
+                                                              norm_type, max_norm, guard_on);
     NT_LAUNCH_CHECK("norm_pow_finalize_kernel launch");
     return NT_OK;
 }
@@ -799,21 +872,26 @@ int32_t nt_ctrl_carry(nt_amp_ctrl *dst, const nt_amp_ctrl *src, void *stream) {
     return NT_OK;
 }
 
-int32_t nt_scale_array(const void *in, void *out, int32_t dtype, double scale, const nt_amp_ctrl *ctrl,
-                       uint64_t count, void *stream) {
+int32_t nt_tensor_scalar(const void *in, int32_t in_dtype, void *out, int32_t out_dtype, double operand,
+                         int32_t op, const nt_amp_ctrl *ctrl, uint64_t count, void *stream) {
     clear_error();
+    if (op != NT_OP_MUL && op != NT_OP_DIV) return fail(NT_ERR_VALUE, "nt_tensor_scalar: unknown operation");
+    if (out_dtype != NT_F32 && out_dtype != NT_F16 && out_dtype != NT_BF16 && out_dtype != NT_F64)
+        return fail(NT_ERR_TYPE, "nt_tensor_scalar: unsupported output dtype");
     if (count == 0) return NT_OK;
-    if (in == nullptr || out == nullptr) return fail(NT_ERR_VALUE, "nt_scale_array: NULL array");
+    if (in == nullptr || out == nullptr) return fail(NT_ERR_VALUE, "nt_tensor_scalar: NULL array");
     hipStream_t s = (hipStream_t)stream;
     dim3 grid((unsigned)small_grid(count));
-    switch (dtype) {
-        case NT_F32: scale_array_kernel<TF32><<<grid, dim3(kBlock), 0, s>>>((const float *)in, (float *)out, scale, ctrl, count); break;
-        case NT_F16: scale_array_kernel<TF16><<<grid, dim3(kBlock), 0, s>>>((const uint16_t *)in, (uint16_t *)out, scale, ctrl, count); break;
-        case NT_BF16: scale_array_kernel<TBF16><<<grid, dim3(kBlock), 0, s>>>((const uint16_t *)in, (uint16_t *)out, scale, ctrl, count); break;
-        case NT_F64: scale_array_f64_kernel<<<grid, dim3(kBlock), 0, s>>>((const double *)in, (double *)out, scale, ctrl, count); break;
-        default: return fail(NT_ERR_TYPE, "nt_scale_array: unsupported dtype");
+    int32_t rc;
+    switch (in_dtype) {
+        case NT_F32: rc = launch_tensor_scalar<TF32>(in, out, out_dtype, operand, ctrl, op, count, grid, s); break;
+        case NT_F16: rc = launch_tensor_scalar<TF16>(in, out, out_dtype, operand, ctrl, op, count, grid, s); break;
+        case NT_BF16: rc = launch_tensor_scalar<TBF16>(in, out, out_dtype, operand, ctrl, op, count, grid, s); break;
+        case NT_F64: rc = launch_tensor_scalar<TF64>(in, out, out_dtype, operand, ctrl, op, count, grid, s); break;
+        default: return fail(NT_ERR_TYPE, "nt_tensor_scalar: unsupported input dtype");
     }
-    NT_LAUNCH_CHECK("scale_array_kernel launch");
+    if (rc != NT_OK) return rc;
+    NT_LAUNCH_CHECK("tensor_scalar_kernel launch");
     return NT_OK;
 }
 

@@ -91,6 +91,18 @@ struct TBF16 {
     __device__ static float round_f32(float x) { return bf16_to_f32(f32_to_bf16(x)); }
     __device__ static raw from_f64(double x) { return f32_to_bf16(f64_to_f32_odd(x)); }
 };
+struct TF64 {
+    using raw = double;
+    static constexpr int code = NT_F64;
+    __device__ static raw from_f64(double x) { return x; }
+};
+
+// Exact widening of a stored value to fp64.
+template <class T>
+__device__ __forceinline__ double widen64(typename T::raw x) {
+    if constexpr (T::code == NT_F64) return x;
+    else return (double)T::to_f32(x);
+}
 
 // ---- 4-element vector I/O ------------------------------------------------------
 // Loads/stores of 4 consecutive elements at a 4-element-aligned index: one

@@ -148,5 +148,56 @@ def from_torch_dtype(value: torch.dtype) -> DType:
     return _FROM_TORCH[value]
 
 
+# ---- promotion of a floating Tensor with a scalar operand ------------------------------
+# The reference wraps a Python scalar in a Tensor (bool -> bool, int -> int64,
+# float -> float32, a NumPy scalar keeps its dtype; dtype.py:177-188) and
+# promotes the two dtypes with its table (dtype.py:94-109, 204-208): for a
+# floating Tensor the result is the Tensor's dtype unless the scalar's dtype
+# is a wider float.  bfloat16 (no reference counterpart) ranks with float16:
+# integers keep it, float16 and float32 promote it to float32.
+_FLOAT_RANK = {float16: 1, bfloat16: 1, float32: 2, float64: 3}
+
+
+def scalar_dtype(value: object) -> DType:
+    """The dtype a scalar operand gets when the reference wraps it in a Tensor."""
+    if isinstance(value, np.generic):
+        return from_numpy_dtype(value.dtype)
+    if isinstance(value, bool):
+        return bool_
+    if isinstance(value, int):
+        if not -(1 << 63) <= value < (1 << 63):
+            raise OverflowError("Python integer is outside the supported int64 range.")
+        return int64
+    if isinstance(value, float):
+        return float32
+    raise TypeError(f"Unsupported scalar operand type {type(value).__name__}.")
+
+
+def promote_with_scalar(tensor_dtype: DType, operand: DType) -> DType:
+    """Result dtype of a floating Tensor combined with a scalar of `operand` dtype."""
+    mine = _FLOAT_RANK[tensor_dtype]
+    other = _FLOAT_RANK.get(operand, 0)
+    if other == 0 or (other == mine and operand is tensor_dtype):
+        return tensor_dtype
+    if other <= mine and mine >= 2:
+        return tensor_dtype
+    if other == mine:                      # float16 with bfloat16
+        return float32
+    return operand if other > mine else tensor_dtype
+
+
+def round_scalar(value: object, operand: DType, target: DType) -> float:
+    """The scalar as the reference computes with it: stored in its own dtype
+    (NumPy cast, round to nearest even), then cast to the compute dtype."""
+    with np.errstate(over="ignore", under="ignore", invalid="ignore"):
+        stored = np.asarray(value, dtype=operand.numpy_dtype)
+        if target is bfloat16:
+            # One correct rounding from the value widened to float64.
+            from .tensor import _bf16_bits_from_f64
+            bits = _bf16_bits_from_f64(stored.astype(np.float64).reshape(1))
+            return float((bits.astype(np.uint32) << 16).view(np.float32)[0])
+        return float(stored.astype(target.numpy_dtype))
+
+
 __all__ = ["DType", "UnsupportedDTypeError", "normalize_dtype", "from_numpy_dtype", "from_torch_dtype",
            "float16", "float32", "float64", "bfloat16"]

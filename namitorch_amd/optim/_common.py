@@ -246,14 +246,14 @@ class _FirstOrderOptimizer(Optimizer):
     @staticmethod
     def _has_negative(value) -> bool:
         if isinstance(value, Tensor):
-            if value._clean_version is not None and value._clean_version == value._version:
+            if value._clean_version is not None and value._clean_version == value._version_counter.value:
                 return False      # written only by this optimizer's kernels since the last check
             if value.device.type == "cpu":
                 result = bool((value._data.to(torch.float32) < 0).any())
             else:
                 result = get_backend(value).any_negative(value._data, value.dtype.code)
             if not result:
-                value._clean_version = value._version
+                value._clean_version = value._version_counter.value
             return result
         if isinstance(value, torch.Tensor):
             return bool((value.to(torch.float32) < 0).any())

@@ -5,11 +5,15 @@ errors and return value (a 0-d float64 Tensor on the gradients' device).
 The norm follows ``_total_norm`` (clip_grad.py:63-79): a non-finite or zero
 max-abs prescale is itself the result (and the result for norm_type=inf);
 otherwise the p-norm in float64.  For p = 2 the device reduces sum(g*g) in
-float64 in one pass (no max-abs prescale is needed: float64 cannot
-overflow or underflow on squares of float32/16 values), so the norm agrees
-with NumPy's to a few float64 ulps rather than bit for bit; other p use the
-prescaled form with a second pass.  The reduction order is fixed, so the
-result is deterministic.
+float64 in one pass: squares of float32/float16/bfloat16 values cannot
+overflow or underflow float64, and float64 gradients take the reference's
+prescaled form with a second pass whenever max|g| lies outside
+[2**-480, 2**480].  The norm therefore agrees with NumPy's to a few float64
+ulps rather than bit for bit: NumPy sums the prescaled squares pairwise and
+takes ``power(total, 0.5)``, whose last bit depends on the host (SVML's pow
+on AVX-512 CPUs, libm's elsewhere), so no device formula can match it on
+every host.  Other p use the prescaled form with a second pass.  The
+reduction order is fixed, so the result is deterministic.
 
 Clipping multiplies each gradient by ``max_norm / (norm + 1e-6)`` in
 float64 and rounds once to the gradient dtype (clip_grad.py:106-111).  The
@@ -32,6 +36,10 @@ from ..backends._graph_capture import reject_during_capture
 from ..tensor import GradTransform, Tensor, no_grad
 
 _NORM_EPS = 1e-6
+# max|g| range in which the direct float64 sum of squares neither overflows
+# nor loses small terms (the device's NT_NORM_POW_GUARD uses the same bounds).
+_DIRECT_L2_LOW = 2.0 ** -480
+_DIRECT_L2_HIGH = 2.0 ** 480
 
 
 def _nonnegative(value: object, name: str) -> float:
@@ -164,7 +172,12 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
         if backend.adamw is None:
             backend._unsupported("Gradient norms")
         transforms = {gradient._pending for gradient in members}
-        if len(transforms) > 1 or any(t is not None and t.clip is not None for t in transforms):
+        # The pre-pass applies at most one host-known unscale.  Anything else
+        # (mixed transforms, a pending clip, or a fused step's device-decided
+        # unscale/clip) is written back first, so the statistics are those of
+        # the values the reference would hold.
+        if len(transforms) > 1 or any(t is not None and (t.clip is not None or t.device is not None)
+                                      for t in transforms):
             for gradient in members:
                 gradient._materialize()
             scale = None
@@ -211,8 +224,10 @@ def _total_norm(gradients: list[Tensor], norm_type: float) -> float:
     scale = stats.prescale()
     if not math.isfinite(scale) or scale == 0 or math.isinf(norm_type):
         return scale
-    if norm_type == 2:
+    if norm_type == 2 and _DIRECT_L2_LOW <= scale <= _DIRECT_L2_HIGH:
         return math.sqrt(stats.sumsq)
+    # Other p, and p = 2 where squares of float64 gradients may leave the
+    # float64 range: the reference's prescaled sum (clip_grad.py:73-78).
     if blocks is None:
         stats, blocks = grad_stats(gradients)
     total = _pow_total(blocks, scale, norm_type)
@@ -261,7 +276,8 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
         unscaled_none = GradTransform()
         reject_during_capture("In-place Tensor updates")
         pendings = tuple(map(_PENDING, gradients))
-        if pendings and all(map(is_, pendings, repeat(pendings[0]))) and (pendings[0] is None or pendings[0].clip is None):
+        if pendings and all(map(is_, pendings, repeat(pendings[0]))) and (
+                pendings[0] is None or (pendings[0].clip is None and pendings[0].device is None)):
             # Common case, one shared prior transform (or none): the loop below
             # with C-level passes.  Inside no_grad only writability can fail the
             # in-place check, and _require_writable has checked it.
@@ -278,10 +294,10 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
             for gradient in gradients:
                 gradient._check_inplace()
                 pending = gradient._pending
-                if pending is not None and pending.clip is not None:
+                if pending is not None and (pending.clip is not None or pending.device is not None):
                     gradient._materialize()
                     pending = None
-                keep_finite = gradient._finite_version is not None and gradient._finite_version == gradient._version
+                keep_finite = gradient._finite_version is not None and gradient._finite_version == gradient._version_counter.value
                 base = unscaled_none if pending is None else pending
                 shared = clipped.get(id(base))
                 if shared is None:
@@ -289,7 +305,7 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
                 gradient._pending = shared[1]
                 gradient._version_counter.increment()
                 if keep_finite:
-                    gradient._finite_version = gradient._version
+                    gradient._finite_version = gradient._version_counter.value
     return _norm_tensor(norm, gradients)
 
 

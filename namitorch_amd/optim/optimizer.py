@@ -1,9 +1,27 @@
 """Optimizer base class.
 
-Same public behaviour as ``namitorch/optim/optimizer.py:120-315``: parameter
-groups, the gradient iterator and its checks (181-195), ``zero_grad``
-(197-206), the versioned ``state_dict`` (211-233), ``load_state_dict``
-(235-312) and ``to`` (288-309), with the same exception classes and messages.
+The public contract is ``namitorch/optim/optimizer.py:120-315``: parameter
+groups and their validation, the gradient iterator with its device, shape
+and dtype checks (181-195), ``zero_grad`` (197-206), the versioned
+``state_dict`` (211-233), ``load_state_dict`` (235-312) and ``to``
+(288-309), raising the same exception classes with the same messages in the
+same order, so callers that catch them or persist these dictionaries work
+unchanged.
+
+How it is built here:
+
+* one walker (:class:`_StateTree`) validates and rebuilds nested optimizer
+  state for all three consumers — copying into and out of a state dict, and
+  moving state to another device — with the array leaf handled by a
+  per-use function;
+* the registered-parameter list and the ``(group, parameter, gradient)``
+  entries are memoized on object identity (a Tensor's device, shape and
+  dtype never change), with the per-item iterator as the path that raises;
+* ``state`` is a property: a step whose skip decision was taken on the device
+  (``namitorch_amd.amp.fused_step``) leaves the host's step counts
+  optimistic until its outcome is read back, and reading ``state`` settles
+  that first, so ``optimizer.state[id(p)]["step"]`` is always the
+  reference's value.
 """
 
 from __future__ import annotations
@@ -33,188 +51,259 @@ _FIRST_OF = itemgetter(0)
 _SECOND_OF = itemgetter(1)
 _CALL_REF = weakref.ReferenceType.__call__
 
+_ARRAY_TYPES = (Tensor, np.ndarray, torch.Tensor)
+_PASS_THROUGH = (bool, int, float, str, bytes)
+_KEY_TYPES = (str, int)
 
-def _copy_value(value, path: str, parameter_shape=None, active=None):
-    if isinstance(value, (Tensor, np.ndarray, torch.Tensor)):
+
+class _StateTree:
+    """Validating rebuild of one optimizer-state value.
+
+    Array leaves (Tensors and storage arrays) go to ``leaf(value, path)``;
+    NumPy scalars become Python scalars after their dtype is checked; None
+    and plain Python scalars are kept; dicts, lists and tuples are rebuilt
+    (keys must be strings or integers, cycles are rejected); anything else
+    is a TypeError.  ``keys_first`` checks all keys of a dictionary before
+    any of its values (the migration order), otherwise each key just before
+    its value (the copy order)."""
+
+    __slots__ = ("leaf", "keys_first", "open")
+
+    def __init__(self, leaf, keys_first: bool):
+        self.leaf = leaf
+        self.keys_first = keys_first
+        self.open: set = set()
+
+    def rebuild(self, value, path: str):
+        if isinstance(value, _ARRAY_TYPES):
+            return self.leaf(value, path)
+        if isinstance(value, np.generic):
+            from_numpy_dtype(value.dtype)
+            return value.item()
+        if value is None or type(value) in _PASS_THROUGH:
+            return value
+        if not isinstance(value, (dict, list, tuple)):
+            raise TypeError(f"{path} contains unsupported optimizer state type {type(value).__name__}.")
+        marker = id(value)
+        if marker in self.open:
+            raise ValueError(f"{path} contains a cyclic optimizer state container.")
+        self.open.add(marker)
+        try:
+            if isinstance(value, dict):
+                return self._mapping(value, path)
+            rebuilt = [self.rebuild(item, f"{path}[{position}]") for position, item in enumerate(value)]
+            return tuple(rebuilt) if isinstance(value, tuple) else rebuilt
+        finally:
+            self.open.discard(marker)
+
+    def _mapping(self, value: dict, path: str) -> dict:
+        if self.keys_first and not all(type(key) in _KEY_TYPES for key in value):
+            raise TypeError(f"{path} dictionary keys must be strings or integers.")
+        rebuilt = {}
+        for key, item in value.items():
+            if type(key) not in _KEY_TYPES:
+                raise TypeError(f"{path} dictionary keys must be strings or integers.")
+            rebuilt[key] = self.rebuild(item, f"{path}[{key!r}]")
+        return rebuilt
+
+
+def _copy_leaf(parameter_shape):
+    """Leaf function of a state copy: an independent copy of every array,
+    optionally checked to be a scalar or of the parameter's shape."""
+    expected = None if parameter_shape is None else tuple(parameter_shape)
+
+    def copy(value, path):
         shape = tuple(value.shape)
-        if parameter_shape is not None and shape not in ((), tuple(parameter_shape)):
-            raise ValueError(f"{path} has shape {shape}; expected scalar state or parameter shape {tuple(parameter_shape)}.")
+        if expected is not None and shape != () and shape != expected:
+            raise ValueError(f"{path} has shape {shape}; expected scalar state or parameter shape {expected}.")
         if isinstance(value, Tensor):
             return Tensor(value, device=value.device)
         if isinstance(value, np.ndarray):
             from_numpy_dtype(value.dtype)
             return value.copy()
         return value.clone()
-    if isinstance(value, np.generic):
-        from_numpy_dtype(value.dtype)
-        return value.item()
-    if value is None or type(value) in (bool, int, float, str, bytes):
-        return value
-    if not isinstance(value, (dict, list, tuple)):
-        raise TypeError(f"{path} contains unsupported optimizer state type {type(value).__name__}.")
-    active = set() if active is None else active
-    identity = id(value)
-    if identity in active:
-        raise ValueError(f"{path} contains a cyclic optimizer state container.")
-    active.add(identity)
-    try:
-        if isinstance(value, dict):
-            copied = {}
-            for key, item in value.items():
-                if type(key) not in (str, int):
-                    raise TypeError(f"{path} dictionary keys must be strings or integers.")
-                copied[key] = _copy_value(item, f"{path}[{key!r}]", parameter_shape, active)
-            return copied
-        copied = [_copy_value(item, f"{path}[{index}]", parameter_shape, active) for index, item in enumerate(value)]
-        return tuple(copied) if isinstance(value, tuple) else copied
-    finally:
-        active.remove(identity)
+
+    return copy
 
 
-def _move_state(value, device: Device, shape, path, memo, active):
-    identity = id(value)
-    if isinstance(value, (Tensor, np.ndarray, torch.Tensor)):
-        if tuple(value.shape) not in ((), tuple(shape)):
-            raise ValueError(f"{path} has incompatible optimizer state shape {tuple(value.shape)}; expected {tuple(shape)}.")
-        if identity not in memo:
+def _copy_state(value, path: str, parameter_shape=None):
+    return _StateTree(_copy_leaf(parameter_shape), keys_first=False).rebuild(value, path)
+
+
+def _move_leaf(device: Device, shape, memo: dict):
+    """Leaf function of a migration: each array object moves once (``memo``
+    by identity, so buffers shared between entries stay shared)."""
+    expected = tuple(shape)
+
+    def move(value, path):
+        found = tuple(value.shape)
+        if found != () and found != expected:
+            raise ValueError(f"{path} has incompatible optimizer state shape {found}; expected {expected}.")
+        key = id(value)
+        if key not in memo:
             if isinstance(value, Tensor):
                 if value.requires_grad:
                     raise RuntimeError(f"{path} must be detached from autograd before migration.")
-                memo[identity] = value.to(device)
+                memo[key] = value.to(device)
             else:
-                memo[identity] = Tensor(value, device=device)
-        return memo[identity]
-    if isinstance(value, np.generic):
-        from_numpy_dtype(value.dtype)
-        return value.item()
-    if value is None or type(value) in (bool, int, float, str, bytes):
-        return value
-    if not isinstance(value, (dict, list, tuple)):
-        raise TypeError(f"{path} contains unsupported optimizer state type {type(value).__name__}.")
-    if identity in active:
-        raise ValueError(f"{path} contains a cyclic optimizer state container.")
-    active.add(identity)
-    try:
-        if isinstance(value, dict):
-            if any(type(key) not in (str, int) for key in value):
-                raise TypeError(f"{path} dictionary keys must be strings or integers.")
-            return {key: _move_state(item, device, shape, f"{path}[{key!r}]", memo, active) for key, item in value.items()}
-        result = [_move_state(item, device, shape, f"{path}[{index}]", memo, active) for index, item in enumerate(value)]
-        return tuple(result) if isinstance(value, tuple) else result
-    finally:
-        active.remove(identity)
+                memo[key] = Tensor(value, device=device)
+        return memo[key]
+
+    return move
 
 
-def _copy_options(options: dict, path: str) -> dict:
+def _checked_options(options, path: str) -> dict:
+    """A validated copy of a group's (or the defaults') options."""
     if not isinstance(options, dict):
         raise TypeError(f"{path} must be a dictionary.")
-    if any(not isinstance(key, str) or not key for key in options):
-        raise TypeError(f"{path} option names must be nonempty strings.")
+    for name in options:
+        if not isinstance(name, str) or not name:
+            raise TypeError(f"{path} option names must be nonempty strings.")
     if "params" in options:
         raise ValueError(f"{path} cannot contain the reserved option 'params'.")
-    return _copy_value(options, path)
+    return _copy_state(options, path)
 
 
-def _parameter_list(params, path: str, allow_single: bool = False) -> list:
+def _collect_parameters(params, path: str, allow_single: bool = False) -> list:
+    """The Parameters of one group, in order: leaves, each object once."""
     if allow_single and isinstance(params, Parameter):
-        values = [params]
+        collected = [params]
+    elif isinstance(params, (Tensor, dict, str, bytes, set, frozenset)):
+        raise TypeError(f"{path} must be an ordered iterable of Parameters.")
     else:
-        if isinstance(params, (Tensor, dict, str, bytes, set, frozenset)):
-            raise TypeError(f"{path} must be an ordered iterable of Parameters.")
         try:
-            values = list(params)
+            collected = list(params)
         except TypeError:
             raise TypeError(f"{path} must be an ordered iterable of Parameters.") from None
-    if not values:
+    if not collected:
         raise ValueError(f"{path} cannot be empty.")
-    identities = set()
-    for parameter in values:
+    seen: set = set()
+    for parameter in collected:
         if not isinstance(parameter, Parameter):
             raise TypeError(f"{path} must contain only NamiTorch Parameters, got {type(parameter).__name__}.")
         if not parameter.is_leaf:
             raise ValueError(f"{path} must contain only leaf Parameters.")
-        if id(parameter) in identities:
+        if id(parameter) in seen:
             raise ValueError(f"{path} contains a duplicate Parameter object.")
-        identities.add(id(parameter))
-    return values
+        seen.add(id(parameter))
+    return collected
+
+
+def _valid_shape(shape) -> bool:
+    return isinstance(shape, (list, tuple)) and all(type(size) is int and size >= 0 for size in shape)
 
 
 class Optimizer:
     def __init__(self, params, defaults: dict | None = None):
         self.defaults = self._prepare_options({} if defaults is None else defaults, "defaults")
-        self.state: dict[int, dict] = defaultdict(dict)
+        self.state = defaultdict(dict)
         self.param_groups: list[dict] = []
+        for group in self._initial_groups(params):
+            self.add_param_group(group)
+
+    @staticmethod
+    def _initial_groups(params) -> list:
+        described = "Optimizer params must be an ordered iterable of Parameters or parameter-group dictionaries."
         if isinstance(params, (Tensor, dict, str, bytes, set, frozenset)):
-            raise TypeError("Optimizer params must be an ordered iterable of Parameters or parameter-group dictionaries.")
+            raise TypeError(described)
         try:
             entries = list(params)
         except TypeError:
-            raise TypeError("Optimizer params must be an ordered iterable of Parameters or parameter-group dictionaries.") from None
+            raise TypeError(described) from None
         if not entries:
             raise ValueError("Optimizer cannot receive an empty parameter list.")
-        if all(isinstance(entry, dict) for entry in entries):
-            groups = entries
-        elif any(isinstance(entry, dict) for entry in entries):
+        dictionaries = sum(isinstance(entry, dict) for entry in entries)
+        if dictionaries == len(entries):
+            return entries
+        if dictionaries:
             raise TypeError("Optimizer params cannot mix Parameters and parameter-group dictionaries.")
-        else:
-            groups = [{"params": entries}]
-        for group in groups:
-            self.add_param_group(group)
+        return [{"params": entries}]
 
+    # ---- per-parameter state ------------------------------------------------------------
+    @property
+    def state(self):
+        """Per-parameter state keyed by ``id(parameter)``; steps decided on the
+        device are settled before it is handed out."""
+        if self.__dict__.get("_device_steps"):
+            self._reconcile_device_steps()
+        return self.__dict__["_state"]
+
+    @state.setter
+    def state(self, value) -> None:
+        self.__dict__["_state"] = value
+
+    def _reconcile_device_steps(self) -> None:
+        """Settle host state (step counts, version counters) of steps whose
+        skip decision was taken on the device (``namitorch_amd.amp.fused_step``)."""
+        pending = self.__dict__.get("_device_steps")
+        if pending:
+            for device_step in pending:
+                device_step.reconcile()
+            pending.clear()
+
+    # ---- hooks for subclasses ------------------------------------------------------------
     def _prepare_options(self, options: dict, path: str) -> dict:
-        return _copy_options(options, path)
+        return _checked_options(options, path)
 
     def _prepare_state(self, values: dict, parameter: Parameter, path: str) -> dict:
-        return _copy_value(values, path, parameter.shape)
+        return _copy_state(values, path, parameter.shape)
 
-    def _registered_parameters(self) -> list:
-        if not self.param_groups:
-            raise ValueError("Optimizer must contain at least one parameter group.")
-        # The structure check below is a pure function of which objects the
-        # groups hold; skip it when that is unchanged since the last call.
+    # ---- parameter groups --------------------------------------------------------------------
+    def _group_fingerprint(self):
+        """Which objects the groups hold (None when a group is not a plain
+        dict with a list of params: the full check then runs)."""
         try:
-            fingerprint = tuple(
+            return tuple(
                 (id(group), id(group["params"]), tuple(map(id, group["params"])))
                 if type(group) is dict and type(group.get("params")) is list else None
                 for group in self.param_groups
             )
         except TypeError:
-            fingerprint = None
+            return None
+
+    def _registered_parameters(self) -> list:
+        if not self.param_groups:
+            raise ValueError("Optimizer must contain at least one parameter group.")
+        # The structure check is a pure function of which objects the groups
+        # hold; it is skipped while that is unchanged since the last call.
+        fingerprint = self._group_fingerprint()
         cached = self.__dict__.get("_registered_cache")
         if fingerprint is not None and cached is not None and cached[0] == fingerprint:
             return list(cached[1])
-        parameters = []
-        identities = set()
-        for index, group in enumerate(self.param_groups):
+        registered: list = []
+        owners: set = set()
+        for position, group in enumerate(self.param_groups):
             if not isinstance(group, dict) or "params" not in group:
-                raise TypeError(f"Parameter group {index} must be a dictionary containing 'params'.")
+                raise TypeError(f"Parameter group {position} must be a dictionary containing 'params'.")
             if not isinstance(group["params"], list):
-                raise TypeError(f"Parameter group {index} params must remain a materialized list.")
-            current = _parameter_list(group["params"], f"param_groups[{index}]['params']")
-            for parameter in current:
-                if id(parameter) in identities:
+                raise TypeError(f"Parameter group {position} params must remain a materialized list.")
+            for parameter in _collect_parameters(group["params"], f"param_groups[{position}]['params']"):
+                if id(parameter) in owners:
                     raise ValueError("A Parameter object cannot belong to more than one parameter group.")
-                identities.add(id(parameter))
-            parameters.extend(current)
+                owners.add(id(parameter))
+                registered.append(parameter)
         if fingerprint is not None and None not in fingerprint:
-            self._registered_cache = (fingerprint, tuple(parameters))
-        return parameters
+            self._registered_cache = (fingerprint, tuple(registered))
+        return registered
 
     def add_param_group(self, param_group: dict) -> None:
         if not isinstance(param_group, dict):
             raise TypeError("add_param_group requires a dictionary.")
         if "params" not in param_group:
             raise ValueError("A parameter group must contain 'params'.")
-        parameters = _parameter_list(param_group["params"], "param_group['params']", allow_single=True)
-        existing = {id(parameter) for parameter in self._registered_parameters()} if self.param_groups else set()
-        if any(id(parameter) in existing for parameter in parameters):
-            raise ValueError("A Parameter object cannot belong to more than one parameter group.")
-        options = _copy_options(self.defaults, "defaults")
-        options.update(_copy_options({key: value for key, value in param_group.items() if key != "params"}, "param_group"))
-        options = self._prepare_options(options, "param_group")
-        options["params"] = parameters
-        self.param_groups.append(options)
+        members = _collect_parameters(param_group["params"], "param_group['params']", allow_single=True)
+        if self.param_groups:
+            taken = set(map(id, self._registered_parameters()))
+            if not taken.isdisjoint(map(id, members)):
+                raise ValueError("A Parameter object cannot belong to more than one parameter group.")
+        merged = _checked_options(self.defaults, "defaults")
+        merged.update(_checked_options({name: value for name, value in param_group.items() if name != "params"},
+                                       "param_group"))
+        group = self._prepare_options(merged, "param_group")
+        group["params"] = members
+        self.param_groups.append(group)
 
+    # ---- gradients ----------------------------------------------------------------------------
     def _gradient_dtype_ok(self, parameter: Tensor, gradient: Tensor) -> bool:
         """Gradients must have the parameter's dtype (optimizer.py:193-194)."""
         return gradient.dtype is parameter.dtype
@@ -250,25 +339,24 @@ class Optimizer:
         checked = self.__dict__.setdefault("_checked_grads", {})
         for group in self.param_groups:
             for parameter in group["params"]:
-                if not parameter._requires_grad:
+                if not parameter._requires_grad or parameter._grad is None:
                     continue
                 gradient = parameter._grad
-                if gradient is None:
-                    continue
-                seen = checked.get(id(parameter))
-                if seen is not None and seen[0] is parameter and seen[1]() is gradient:
-                    yield group, parameter, gradient
-                    continue
-                if not isinstance(gradient, Tensor):
-                    raise TypeError("Parameter gradients must be NamiTorch Tensors.")
-                if gradient._device is not parameter._device and gradient._device != parameter._device:
-                    ensure_same_device(parameter, gradient)       # raises the device mismatch
-                if gradient._storage.shape != parameter._storage.shape:
-                    raise ValueError(f"Gradient shape {gradient.shape} does not match parameter shape {parameter.shape}.")
-                if not self._gradient_dtype_ok(parameter, gradient):
-                    raise TypeError(f"Gradient dtype {gradient.dtype} does not match parameter dtype {parameter.dtype}.")
-                checked[id(parameter)] = (parameter, weakref.ref(gradient))
+                known = checked.get(id(parameter))
+                if known is None or known[0] is not parameter or known[1]() is not gradient:
+                    self._check_gradient(parameter, gradient)
+                    checked[id(parameter)] = (parameter, weakref.ref(gradient))
                 yield group, parameter, gradient
+
+    def _check_gradient(self, parameter: Tensor, gradient) -> None:
+        if not isinstance(gradient, Tensor):
+            raise TypeError("Parameter gradients must be NamiTorch Tensors.")
+        if gradient._device is not parameter._device and gradient._device != parameter._device:
+            ensure_same_device(parameter, gradient)       # raises the device mismatch
+        if gradient._storage.shape != parameter._storage.shape:
+            raise ValueError(f"Gradient shape {gradient.shape} does not match parameter shape {parameter.shape}.")
+        if not self._gradient_dtype_ok(parameter, gradient):
+            raise TypeError(f"Gradient dtype {gradient.dtype} does not match parameter dtype {parameter.dtype}.")
 
     def _grad_entries(self) -> tuple:
         """``tuple(self._parameters_with_grad())``, memoized.
@@ -319,92 +407,96 @@ class Optimizer:
     def step(self, closure=None):
         raise RuntimeError("Optimizer subclass must implement step.")
 
-    def _reconcile_device_steps(self) -> None:
-        """Settle host state (step counts, version counters) of steps whose
-        skip decision was taken on the device (``namitorch_amd.amp.fused_step``)."""
-        pending = self.__dict__.get("_device_steps")
-        if pending:
-            for device_step in pending:
-                device_step.reconcile()
-            pending.clear()
-
+    # ---- state dictionaries ---------------------------------------------------------------------
     def state_dict(self) -> dict:
-        self._reconcile_device_steps()
         parameters = self._registered_parameters()
-        indices = {id(parameter): index for index, parameter in enumerate(parameters)}
-        state = {}
-        for identity, values in self.state.items():
-            if type(identity) is not int or identity not in indices:
+        position = {id(parameter): index for index, parameter in enumerate(parameters)}
+        saved_state = {}
+        for key, values in self.state.items():
+            index = position.get(key) if type(key) is int else None
+            if index is None:
                 raise ValueError("Optimizer state keys must be identities of registered Parameters.")
             if not isinstance(values, dict):
                 raise TypeError("Each parameter's optimizer state must be a dictionary.")
-            index = indices[identity]
-            state[index] = self._prepare_state(values, parameters[index], f"state[{index}]")
-        groups = []
-        for index, group in enumerate(self.param_groups):
-            copied = self._prepare_options({key: value for key, value in group.items() if key != "params"}, f"param_groups[{index}]")
-            copied["params"] = [indices[id(parameter)] for parameter in group["params"]]
-            groups.append(copied)
+            saved_state[index] = self._prepare_state(values, parameters[index], f"state[{index}]")
+        saved_groups = []
+        for number, group in enumerate(self.param_groups):
+            options = self._prepare_options({name: value for name, value in group.items() if name != "params"},
+                                            f"param_groups[{number}]")
+            options["params"] = [position[id(parameter)] for parameter in group["params"]]
+            saved_groups.append(options)
         return {
             "version": 1,
             "defaults": self._prepare_options(self.defaults, "defaults"),
-            "param_groups": groups,
+            "param_groups": saved_groups,
             "param_shapes": [list(parameter.shape) for parameter in parameters],
-            "state": state,
+            "state": saved_state,
         }
 
     def _prepare_load_state_dict(self, state_dict: dict):
-        if not isinstance(state_dict, dict):
-            raise TypeError("Optimizer state_dict must be a dictionary.")
-        expected_keys = {"version", "defaults", "param_groups", "param_shapes", "state"}
-        if set(state_dict) != expected_keys:
-            raise ValueError("Optimizer state_dict must contain version, defaults, param_groups, param_shapes and state.")
-        if type(state_dict["version"]) is not int or state_dict["version"] != 1:
-            raise ValueError("Unsupported optimizer state_dict version.")
+        """Validate a saved state against this optimizer and build the
+        replacement (defaults, groups, state) without changing anything."""
+        self._check_saved_layout(state_dict)
         parameters = self._registered_parameters()
-        groups = state_dict["param_groups"]
+        groups, shapes = state_dict["param_groups"], state_dict["param_shapes"]
         if not isinstance(groups, list) or len(groups) != len(self.param_groups):
             raise ValueError("Loaded optimizer must have the same number of parameter groups.")
-        shapes = state_dict["param_shapes"]
         if not isinstance(shapes, list) or len(shapes) != len(parameters):
             raise ValueError("Loaded optimizer must contain one shape for each parameter.")
         defaults = self._prepare_options(state_dict["defaults"], "defaults")
-        restored_groups = []
-        index_to_parameter = {}
-        for group_index, (saved, current) in enumerate(zip(groups, self.param_groups)):
-            if not isinstance(saved, dict) or "params" not in saved:
-                raise ValueError(f"Loaded parameter group {group_index} must contain 'params'.")
-            saved_indices = saved["params"]
-            if not isinstance(saved_indices, list) or len(saved_indices) != len(current["params"]):
-                raise ValueError(f"Loaded parameter group {group_index} has a different number of parameters.")
-            options = self._prepare_options({key: value for key, value in saved.items() if key != "params"}, f"param_groups[{group_index}]")
-            if not defaults.keys() <= options.keys():
-                raise ValueError(f"Loaded parameter group {group_index} is missing default options.")
-            for index, parameter in zip(saved_indices, current["params"]):
-                if type(index) is not int or not 0 <= index < len(parameters):
-                    raise ValueError("Loaded parameter indices must be integers in the registered parameter range.")
-                if index in index_to_parameter:
-                    raise ValueError("Loaded parameter groups contain duplicate parameter indices.")
-                shape = shapes[index]
-                if not isinstance(shape, (list, tuple)) or any(type(dimension) is not int or dimension < 0 for dimension in shape):
-                    raise ValueError(f"Invalid saved parameter shape for index {index}.")
-                if tuple(shape) != parameter.shape:
-                    raise ValueError(f"Saved parameter {index} shape {tuple(shape)} does not match current shape {parameter.shape}.")
-                index_to_parameter[index] = parameter
-            options["params"] = list(current["params"])
-            restored_groups.append(options)
-        saved_state = state_dict["state"]
+        owner_of: dict = {}
+        restored_groups = [self._restore_group(number, saved, current, defaults, shapes, len(parameters), owner_of)
+                           for number, (saved, current) in enumerate(zip(groups, self.param_groups))]
+        return defaults, restored_groups, self._restore_state(state_dict["state"], owner_of)
+
+    @staticmethod
+    def _check_saved_layout(state_dict) -> None:
+        if not isinstance(state_dict, dict):
+            raise TypeError("Optimizer state_dict must be a dictionary.")
+        if set(state_dict) != {"version", "defaults", "param_groups", "param_shapes", "state"}:
+            raise ValueError("Optimizer state_dict must contain version, defaults, param_groups, param_shapes and state.")
+        if type(state_dict["version"]) is not int or state_dict["version"] != 1:
+            raise ValueError("Unsupported optimizer state_dict version.")
+
+    def _restore_group(self, number: int, saved, current: dict, defaults: dict, shapes: list, count: int,
+                       owner_of: dict) -> dict:
+        """One saved group matched to the current one; records which current
+        parameter each saved index now names in `owner_of`."""
+        if not isinstance(saved, dict) or "params" not in saved:
+            raise ValueError(f"Loaded parameter group {number} must contain 'params'.")
+        indices = saved["params"]
+        if not isinstance(indices, list) or len(indices) != len(current["params"]):
+            raise ValueError(f"Loaded parameter group {number} has a different number of parameters.")
+        options = self._prepare_options({name: value for name, value in saved.items() if name != "params"},
+                                        f"param_groups[{number}]")
+        if not defaults.keys() <= options.keys():
+            raise ValueError(f"Loaded parameter group {number} is missing default options.")
+        for index, parameter in zip(indices, current["params"]):
+            if type(index) is not int or not 0 <= index < count:
+                raise ValueError("Loaded parameter indices must be integers in the registered parameter range.")
+            if index in owner_of:
+                raise ValueError("Loaded parameter groups contain duplicate parameter indices.")
+            shape = shapes[index]
+            if not _valid_shape(shape):
+                raise ValueError(f"Invalid saved parameter shape for index {index}.")
+            if tuple(shape) != parameter.shape:
+                raise ValueError(f"Saved parameter {index} shape {tuple(shape)} does not match current shape {parameter.shape}.")
+            owner_of[index] = parameter
+        options["params"] = list(current["params"])
+        return options
+
+    def _restore_state(self, saved_state, owner_of: dict):
         if not isinstance(saved_state, dict):
             raise TypeError("Loaded optimizer state must be a dictionary keyed by parameter indices.")
-        restored_state = defaultdict(dict)
+        restored = defaultdict(dict)
         for index, values in saved_state.items():
-            if type(index) is not int or index not in index_to_parameter:
+            parameter = owner_of.get(index) if type(index) is int else None
+            if parameter is None:
                 raise ValueError("Loaded state keys must be registered parameter indices.")
             if not isinstance(values, dict):
                 raise TypeError(f"Loaded state[{index}] must be a dictionary.")
-            parameter = index_to_parameter[index]
-            restored_state[id(parameter)] = self._prepare_state(values, parameter, f"state[{index}]")
-        return defaults, restored_groups, restored_state
+            restored[id(parameter)] = self._prepare_state(values, parameter, f"state[{index}]")
+        return restored
 
     def _install_loaded_state(self, defaults: dict, param_groups: list, state) -> None:
         """Replace options and state with a prepared load; device-side steps
@@ -415,27 +507,29 @@ class Optimizer:
     def load_state_dict(self, state_dict: dict) -> None:
         self._install_loaded_state(*self._prepare_load_state_dict(state_dict))
 
+    # ---- migration --------------------------------------------------------------------------------
     def to(self, device):
         reject_during_capture("Moving optimizer state")
         target = Device(device)
-        parameters = {id(parameter): parameter for parameter in self._registered_parameters()}
-        if any(parameter.device != target for parameter in parameters.values()):
+        by_identity = {id(parameter): parameter for parameter in self._registered_parameters()}
+        if any(parameter.device != target for parameter in by_identity.values()):
             raise RuntimeError(f"Move all optimizer parameters to {target} first with model.to(device); optimizer.to(device) moves only optimizer state.")
-        staged = defaultdict(dict)
-        memo = {}
+        moved_state = defaultdict(dict)
+        moved_arrays: dict = {}
+        validate = getattr(self, "_check_state", None)
         with no_grad():
-            for identity, values in self.state.items():
-                if type(identity) is not int or identity not in parameters:
+            for key, values in self.state.items():
+                parameter = by_identity.get(key) if type(key) is int else None
+                if parameter is None:
                     raise ValueError("Optimizer state keys must identify registered Parameters.")
                 if not isinstance(values, dict):
                     raise TypeError("Each parameter's optimizer state must be a dictionary.")
-                parameter = parameters[identity]
-                moved = _move_state(values, target, parameter.shape, "optimizer state", memo, set())
-                validate = getattr(self, "_check_state", None)
+                tree = _StateTree(_move_leaf(target, parameter.shape, moved_arrays), keys_first=True)
+                moved = tree.rebuild(values, "optimizer state")
                 if validate is not None:
                     validate(moved, parameter, "optimizer state", runtime=True)
-                staged[identity] = moved
-        self.state = staged
+                moved_state[key] = moved
+        self.state = moved_state
         return self
 
     def __repr__(self) -> str:

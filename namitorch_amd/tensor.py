@@ -42,6 +42,9 @@ from .dtype import (
     from_torch_dtype,
     int64,
     normalize_dtype,
+    promote_with_scalar,
+    round_scalar,
+    scalar_dtype,
 )
 
 
@@ -53,6 +56,17 @@ class _VersionCounter:
 
     def increment(self) -> None:
         self.value += 1
+
+
+# Device-decided optimizer steps (namitorch_amd.amp.fused_step) whose host
+# bookkeeping (version counters, step counts) is still optimistic, oldest
+# first; each removes itself when reconciled.
+_unsettled_steps: list = []
+
+
+def _settle_device_steps() -> None:
+    while _unsettled_steps:
+        _unsettled_steps[0].reconcile()
 
 
 # ---- grad mode (namitorch/autograd.py:15-42) -----------------------------------------
@@ -314,6 +328,11 @@ class Tensor:
 
     @property
     def _version(self) -> int:
+        """In-place version (tensor.py:71-76).  A fused step decided on the
+        device bumps versions before its outcome is known; reading a version
+        settles such steps first, so a skipped step reads as never taken."""
+        if _unsettled_steps:
+            _settle_device_steps()
         return self._version_counter.value
 
     # ---- in-place updates (tensor.py:1252-1287) ------------------------------------------
@@ -404,19 +423,34 @@ class Tensor:
             return self
         return Tensor(self, dtype=kind, device=target)
 
-    def __mul__(self, other):
-        if isinstance(other, builtins.bool) or not isinstance(other, Real):
+    def _scalar_arithmetic(self, other, op: int) -> "Tensor":
+        """``self * other`` or ``self / other`` for a scalar ``other``, with the
+        reference's promotion (tensor.py:585-646: the scalar becomes a Tensor of
+        its own dtype, both operands are cast to the promoted dtype and one
+        NumPy ufunc computes the result in it)."""
+        if isinstance(other, Tensor):
             return NotImplemented
+        if not isinstance(other, (builtins.bool, builtins.int, builtins.float, np.generic)):
+            raise TypeError(
+                f"Operators require Tensor, Python scalar or NumPy scalar operands, got {type(other).__name__}. "
+                "Convert sequences and ndarrays explicitly with tensor() or as_tensor()."
+            )
+        if not self._dtype.is_floating_point:
+            raise TypeError("Only floating Tensors support scalar arithmetic on the device.")
+        operand = scalar_dtype(other)
+        result = promote_with_scalar(self._dtype, operand)
         from .backends import get_backend
-        return get_backend(self).scale_tensor(self, float(other))
+        return get_backend(self).scalar_arithmetic(self, round_scalar(other, operand, result), op, result)
+
+    def __mul__(self, other):
+        from ._native import NT_OP_MUL
+        return self._scalar_arithmetic(other, NT_OP_MUL)
 
     __rmul__ = __mul__
 
     def __truediv__(self, other):
-        if isinstance(other, builtins.bool) or not isinstance(other, Real):
-            return NotImplemented
-        from .backends import get_backend
-        return get_backend(self).scale_tensor(self, 1.0 / float(other))
+        from ._native import NT_OP_DIV
+        return self._scalar_arithmetic(other, NT_OP_DIV)
 
     def __len__(self) -> int:
         if self.ndim == 0:

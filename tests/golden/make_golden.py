@@ -442,9 +442,75 @@ def error_texts(nt):
     return texts
 
 
-def main(reference: str) -> None:
+SCALAR_LOSSES = [3.0, -2.5, 1.0, 0.0, -0.0, 65504.0, 1e-5, 6.1e-5, 1e30, np.inf, -np.inf, np.nan, 0.1, 1.0 / 3.0]
+
+
+def scalar_cases(nt):
+    """GradScaler.scale (amp.py:137-138) and the runner's loss / accum
+    (runner.py:246): Tensor-by-scalar arithmetic with the reference's dtype
+    promotion, for float16/32/64 losses."""
+    out = {}
+    rng = np.random.Generator(np.random.PCG64(61))
+    for dtype in (np.float16, np.float32, np.float64):
+        with np.errstate(over="ignore", invalid="ignore"):
+            loss = np.concatenate([np.asarray(SCALAR_LOSSES, dtype=np.float64),
+                                   rng.standard_normal(50) * 4.0]).astype(dtype)
+        name = np.dtype(dtype).name
+        out[f"{name}_loss"] = loss
+        for scale in (65536.0, 3000.0, 0.125):
+            scaler = nt.amp.GradScaler(init_scale=scale)
+            out[f"{name}_scale_{scale:g}"] = scaler.scale(nt.Tensor(loss.copy()))._data.copy()
+        for label, divisor in (("int3", 3), ("int7", 7), ("int1000", 1000), ("float3", 3.0), ("float0.1", 0.1),
+                               ("f16_3", np.float16(3.0)), ("f64_3", np.float64(3.0))):
+            with np.errstate(over="ignore", invalid="ignore", divide="ignore", under="ignore"):
+                out[f"{name}_div_{label}"] = (nt.Tensor(loss.copy()) / divisor)._data.copy()
+        for label, factor in (("int3", 3), ("float0.1", 0.1), ("f64_0.1", np.float64(0.1))):
+            with np.errstate(over="ignore", invalid="ignore", under="ignore"):
+                out[f"{name}_mul_{label}"] = (nt.Tensor(loss.copy()) * factor)._data.copy()
+    np.savez(HERE / "scalar_ops.npz", **out)
+    return sorted(out)
+
+
+def clip_f64_cases(nt):
+    """clip_grad_norm_ on float64 gradients whose squares leave the float64
+    range (|g| ~ 1e200 and 1e-200) and at ordinary magnitudes, p = 2 and 3."""
+    rng = np.random.Generator(np.random.PCG64(67))
+    shapes = [(37,), (8, 16), (1000,)]
+    out = {}
+    records = []
+    for label, magnitude, max_norm in (("huge", 1e200, 1e199), ("tiny", 1e-200, 1e-210), ("unit", 1.0, 1.0)):
+        for norm_type in (2.0, 3.0):
+            grads = [rng.standard_normal(s) * magnitude for s in shapes]
+            params = [nt.nn.Parameter(np.zeros(s, dtype=np.float64)) for s in shapes]
+            for param, grad in zip(params, grads):
+                param._grad = nt.Tensor(grad.copy())
+            with np.errstate(under="ignore"):
+                norm = nt.optim.clip_grad_norm_(params, max_norm, norm_type=norm_type)
+            key = f"clip64_{label}_{norm_type:g}"
+            for index, (grad, param) in enumerate(zip(grads, params)):
+                out[f"{key}_in{index}"] = grad
+                out[f"{key}_out{index}"] = param.grad._data.copy()
+            records.append(dict(key=key, norm_type=norm_type, max_norm=max_norm, norm=float(norm._data),
+                                count=len(shapes)))
+    out["records"] = np.asarray(json.dumps(records))
+    np.savez(HERE / "clip_f64.npz", **out)
+    return [record["key"] for record in records]
+
+
+# Fixture sets that write their own files (and keep their records there);
+# `--only name,...` regenerates just those.
+STANDALONE = {"scalar_ops": scalar_cases, "clip_f64": clip_f64_cases}
+
+
+def main(reference: str, only: list[str] | None = None) -> None:
     sys.path.insert(0, reference)
     import namitorch as nt  # the reference, on its NumPy (CPU) backend
+    if only:
+        for name in only:
+            print(name, STANDALONE[name](nt))
+        return
+    for function in STANDALONE.values():
+        function(nt)
     golden = {
         "source": "renderityai/NamiTorch NumPy backend (optim/adam.py, optim/clip_grad.py, amp.py)",
         "numpy": np.__version__,
@@ -464,4 +530,6 @@ def main(reference: str) -> None:
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    arguments = [argument for argument in sys.argv[1:] if not argument.startswith("--only=")]
+    selected = [argument.split("=", 1)[1] for argument in sys.argv[1:] if argument.startswith("--only=")]
+    main(arguments[0] if arguments else "/root/reference", selected[0].split(",") if selected else None)

@@ -211,13 +211,14 @@ def test_prepass_finalize_norm_and_apply(plans):
         with pytest.raises(ValueError, match="growth/backoff"):
             _call("nt_amp_finalize", plan, c, None, 2.0, -1.0, update, growth, backoff, interval, _stream())
     with pytest.raises(ValueError, match="control block is NULL"):
-        _call("nt_grad_norm_pow", plan, None, 3.0, -1.0, 1.0, 0, 0, _stream())
+        _call("nt_grad_norm_pow", plan, None, 3.0, -1.0, 1.0, 0, 0, 0, _stream())
     for norm_type in (float("inf"), 0.0):
         with pytest.raises(ValueError, match="finite positive norm_type"):
-            _call("nt_grad_norm_pow", plan, c, norm_type, -1.0, 1.0, 0, 0, _stream())
-    f64 = plans((NONE, F64, NONE, NONE), [64])
-    with pytest.raises(TypeError, match="float64 gradients"):
-        _call("nt_grad_norm_pow", f64, c, 3.0, -1.0, 1.0, 0, 0, _stream())
+            _call("nt_grad_norm_pow", plan, c, norm_type, -1.0, 1.0, 0, 0, 0, _stream())
+    with pytest.raises(ValueError, match="unknown flags"):
+        _call("nt_grad_norm_pow", plan, c, 2.0, -1.0, 1.0, 0, 0, 4, _stream())
+    with pytest.raises(ValueError, match="norm_type 2 only"):
+        _call("nt_grad_norm_pow", plan, c, 3.0, -1.0, 1.0, 0, 0, _native.NT_NORM_POW_GUARD, _stream())
     with pytest.raises(ValueError, match="plan is NULL"):
         _call("nt_grad_apply", None, None, _stream())
     _call("nt_grad_apply", plan, None, _stream())                         # no transform: nothing to do
@@ -233,11 +234,16 @@ def test_control_blocks_and_small_kernels():
     with pytest.raises(ValueError, match="alias"):
         _call("nt_ctrl_carry", ctrl.data_ptr(), ctrl.data_ptr(), _stream())
     x = torch.ones(8, device=DEV)
+    mul, div = _native.NT_OP_MUL, _native.NT_OP_DIV
     with pytest.raises(ValueError, match="NULL array"):
-        _call("nt_scale_array", None, x.data_ptr(), F32, 2.0, None, 8, _stream())
-    with pytest.raises(TypeError, match="unsupported dtype"):
-        _call("nt_scale_array", x.data_ptr(), x.data_ptr(), 9, 2.0, None, 8, _stream())
-    _call("nt_scale_array", None, None, F32, 2.0, None, 0, _stream())      # empty loss
+        _call("nt_tensor_scalar", None, F32, x.data_ptr(), F32, 2.0, mul, None, 8, _stream())
+    with pytest.raises(TypeError, match="unsupported input dtype"):
+        _call("nt_tensor_scalar", x.data_ptr(), 9, x.data_ptr(), F32, 2.0, mul, None, 8, _stream())
+    with pytest.raises(TypeError, match="unsupported output dtype"):
+        _call("nt_tensor_scalar", x.data_ptr(), F32, x.data_ptr(), 9, 2.0, div, None, 8, _stream())
+    with pytest.raises(ValueError, match="unknown operation"):
+        _call("nt_tensor_scalar", x.data_ptr(), F32, x.data_ptr(), F32, 2.0, 7, None, 8, _stream())
+    _call("nt_tensor_scalar", None, F32, None, F32, 2.0, mul, None, 0, _stream())      # empty loss
     flag = torch.ones(1, dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError, match="NULL flag"):
         _call("nt_any_negative", x.data_ptr(), F32, 8, None, _stream())

@@ -181,3 +181,47 @@ def test_schedule_follows_updates_like_reference(mode):
         assert state["exp_avg"].numpy().tobytes() == data[f"m{i}"].tobytes(), i
         assert state["exp_avg_sq"].numpy().tobytes() == data[f"v{i}"].tobytes(), i
         assert state["step"] == int(data[f"step{i}"])
+
+
+@pytest.mark.parametrize("first_read", ["state", "version"])
+def test_reads_right_after_a_skipped_fused_step(first_read):
+    """The last step of a fused run is skipped on the device (non-finite
+    gradients) and read back at once, with no other synchronizing call:
+    ``optimizer.state[...]["step"]`` and the version counters must be those
+    of the reference call sequence at the same point, where the skipped step
+    never happened (amp.py:211-217)."""
+    golden = json.loads((GOLDEN / "golden.json").read_text())["schedule_runner"]
+    data = np.load(GOLDEN / "schedule_runner.npz")
+    last = golden["updated"].index(False)             # first skipped step of the reference run
+    assert last > 0
+
+    def run(mode):
+        params = [nt.Parameter(data["p0_0"], device=DEV), nt.Parameter(data["p0_1"], device=DEV)]
+        optimizer = nt.optim.AdamW([{"params": [params[0]], "weight_decay": 0.1},
+                                    {"params": [params[1]], "weight_decay": 0.0}], lr=2e-3, betas=(0.9, 0.95))
+        scaler = nt.GradScaler(init_scale=4096.0, growth_interval=3)
+        for k in range(last + 1):
+            for i, p in enumerate(params):
+                p.grad = nt.Tensor(data[f"grad{i}_{k}"], device=DEV)
+            scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+            if mode == "api":
+                if scaler.unscale_(optimizer):
+                    nt.optim.clip_grad_norm_(params, 1.0)
+                scaler.step(optimizer)
+                scaler.update()
+            else:
+                nt.amp.fused_step(optimizer, scaler, max_norm=1.0)
+        if first_read == "version":
+            versions = [(p._version, optimizer.state[id(p)]["exp_avg"]._version) for p in params]
+            steps = [optimizer.state[id(p)]["step"] for p in params]
+        else:
+            steps = [optimizer.state[id(p)]["step"] for p in params]
+            versions = [(p._version, optimizer.state[id(p)]["exp_avg"]._version) for p in params]
+        return steps, versions, [p.grad._version for p in params], [p.numpy().tobytes() for p in params]
+
+    api = run("api")
+    fused = run("fused")
+    assert fused[0] == api[0] == [sum(golden["updated"][:last + 1])] * 2
+    assert fused[1] == api[1]
+    assert fused[2] == api[2]
+    assert fused[3] == api[3]

@@ -1,0 +1,243 @@
+"""The benchmark configurations as composed 10-step runs against the oracle.
+
+Each run goes through the reference's call sequence (``unscale_`` ->
+``clip_grad_norm_`` -> ``step`` -> ``update``, training/runner.py:248-251)
+and through ``amp.fused_step``, and is compared with the oracle's
+``scaler.unscale`` -> ``clip.clip_grad_norm`` -> ``adam.master_step`` /
+``adam.adam_step`` composed on the host (evaluated slice-wise on a thread
+pool by ``oracle.parallel``, which gives the oracle's bits):
+
+* C2: the full GPT-2-124M list (148 tensors, 124,439,808 parameters), float32
+  AdamW in the two ``decay_parameter_groups`` groups (runner.py:83-90);
+* C3: the full GPT-2-124M list with AMP: bfloat16 model + float32 master,
+  float16 gradients f16(N(0, 1e-3) * 65536), one +inf (or NaN) at a seeded
+  (step, tensor, element), GradScaler(65536, x2, x0.5, 2000) and a
+  growth_interval 3 variant that grows within the run;
+* C4: the GPT-1.3B layout at its real width (d 2048, vocab 50304, ctx 2048)
+  with 2 layers (207.8 M parameters): float32 master, bfloat16
+  parameters/moments/gradients, clip_grad_norm_ at 1.0 (active every step).
+
+Bars: found_inf flags, skip decisions and the
+loss-scale sequence bit-exact; norms within 1e-12 relative; float32 master,
+parameters and moments bit-exact, and model copies and bfloat16 moments
+equal to the oracle's RNE values.  A clip coefficient one float64 ulp away
+from the oracle's can move a clipped gradient across a rounding boundary;
+for bfloat16 gradients that has a probability of about 2**-43 per element, so
+any such element is allowed only within one unit of the storage type and at
+a rate below 1e-6.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import namitorch_amd as nt
+from namitorch_amd.param_lists import decay_mask, gpt2_shapes, total_params
+from oracle import clip as oclip
+from oracle import parallel
+from oracle import scaler as oscaler
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+STEPS = 10
+NORM_RTOL = 1e-12
+OPTIONS = dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8)
+
+
+@pytest.fixture(scope="module")
+def pool():
+    with parallel.Pool() as threads:
+        yield threads
+
+
+def _normals(pool, shapes, seed, sigma):
+    """float32 N(0, sigma) per tensor, each from its own PCG64 stream
+    (SeedSequence(seed).spawn), drawn in parallel."""
+    streams = np.random.SeedSequence(seed).spawn(len(shapes))
+
+    def draw(shape, stream):
+        values = np.random.Generator(np.random.PCG64(stream)).standard_normal(shape, dtype=np.float32)
+        values *= np.float32(sigma)
+        return values
+
+    return pool.run([lambda s=s, q=q: draw(s, q) for s, q in zip(shapes, streams)])
+
+
+def _say(message):
+    print(message, flush=True)
+
+
+def _compare(label, got, want, unit_bits=None, allow_rate=0.0):
+    """Bit-exact, or (allow_rate > 0) mismatches within one unit of the
+    storage type (unit_bits: 16 for bfloat16 values held as float32) at a
+    rate below allow_rate."""
+    got = np.ascontiguousarray(got).reshape(-1)
+    want = np.ascontiguousarray(want).reshape(-1)
+    assert got.shape == want.shape and got.dtype == want.dtype, label
+    bad = np.flatnonzero(got.view(np.uint32 if got.itemsize == 4 else np.uint16)
+                         != want.view(np.uint32 if want.itemsize == 4 else np.uint16))
+    if bad.size == 0:
+        return 0
+    assert bad.size <= allow_rate * got.size, f"{label}: {bad.size} of {got.size} elements differ"
+    step = 1 << (32 - unit_bits) if unit_bits else 1
+    distance = np.abs(got.view(np.int32)[bad].astype(np.int64) - want.view(np.int32)[bad].astype(np.int64))
+    assert np.all(distance <= step), f"{label}: differences beyond one unit"
+    return int(bad.size)
+
+
+def _groups(params, shapes, weight_decay=0.1):
+    mask = decay_mask(shapes)
+    return [{"params": [p for p, m in zip(params, mask) if m], "weight_decay": weight_decay},
+            {"params": [p for p, m in zip(params, mask) if not m], "weight_decay": 0.0}]
+
+
+# ---- C2 --------------------------------------------------------------------------------------------
+def test_c2_full_gpt2_fp32_ten_steps(pool):
+    shapes = gpt2_shapes()
+    assert len(shapes) == 148 and total_params(shapes) == 124_439_808
+    host = _normals(pool, shapes, 1337, 0.02)
+    params = [nt.Parameter(h, device=DEV) for h in host]
+    optimizer = nt.optim.AdamW(_groups(params, shapes), **OPTIONS)
+    ref_p = [h.copy() for h in host]
+    ref_m = [np.zeros_like(h) for h in host]
+    ref_v = [np.zeros_like(h) for h in host]
+    decays = [0.1 if m else 0.0 for m in decay_mask(shapes)]
+    for step in range(1, STEPS + 1):
+        grads = _normals(pool, shapes, 1337 + 1000 + step, 1e-3)
+        for p, g in zip(params, grads):
+            p.grad = nt.Tensor(g, device=DEV)
+        optimizer.step()
+        for i, g in enumerate(grads):
+            parallel.adam_step(pool, ref_p[i], g, ref_m[i], ref_v[i], step, weight_decay=decays[i], **OPTIONS)
+        _say(f"C2 step {step} done")
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        _compare(f"p[{i}]", p.numpy(), ref_p[i])
+        _compare(f"m[{i}]", state["exp_avg"].numpy(), ref_m[i])
+        _compare(f"v[{i}]", state["exp_avg_sq"].numpy(), ref_v[i])
+        assert state["step"] == STEPS
+
+
+# ---- C3 --------------------------------------------------------------------------------------------
+def _c3_oracle(pool, shapes, host, grads16, growth_interval):
+    """Oracle trajectory of the C3 recipe: flags, scales and final state."""
+    master = [h.copy() for h in host]
+    m = [np.zeros_like(h) for h in host]
+    v = [np.zeros_like(h) for h in host]
+    decays = [0.1 if k else 0.0 for k in decay_mask(shapes)]
+    scaler = oscaler.Scaler(65536.0, 2.0, 0.5, growth_interval)
+    finite_flags, scales, count = [], [], 0
+    for grads in grads16:
+        unscaled = [parallel.unscale(pool, g, scaler.scale, "float16") for g in grads]
+        finite = parallel.finite(pool, unscaled)
+        if finite:
+            count += 1
+            for i, u in enumerate(unscaled):
+                parallel.master_step(pool, master[i], u, m[i], v[i], count, weight_decay=decays[i], **OPTIONS)
+        scaler.update(not finite)
+        finite_flags.append(finite)
+        scales.append(scaler.scale)
+    copies = [parallel.round_bf16(pool, x) for x in master]
+    return finite_flags, scales, master, m, v, copies, count
+
+
+@pytest.mark.parametrize("poison,growth_interval", [(np.inf, 2000), (np.nan, 3)])
+def test_c3_gpt2_amp_ten_steps(pool, poison, growth_interval):
+    shapes = gpt2_shapes()
+    host = [parallel.round_bf16(pool, h) for h in _normals(pool, shapes, 1337, 0.02)]
+    pick = np.random.Generator(np.random.PCG64(7))
+    bad_step, bad_tensor = int(pick.integers(1, STEPS)), int(pick.integers(0, len(shapes)))
+    bad_element = int(pick.integers(0, int(np.prod(shapes[bad_tensor]))))
+    grads16 = []
+    for step in range(STEPS):
+        values = _normals(pool, shapes, 1337 + 1000 + step, 1e-3)
+        step_grads = pool.run([lambda g=g: (g * np.float32(65536.0)).astype(np.float16) for g in values])
+        if step == bad_step:
+            step_grads[bad_tensor].reshape(-1)[bad_element] = poison
+        grads16.append(step_grads)
+    finite_flags, scales, master, m, v, copies, count = _c3_oracle(pool, shapes, host, grads16, growth_interval)
+    assert finite_flags.count(False) == 1 and not finite_flags[bad_step]
+    if growth_interval == 3:
+        assert max(scales) > 65536.0              # the run grows the scale
+    _say(f"C3 oracle done: skip at step {bad_step}, scales {scales}")
+    for mode in ("api", "fused"):
+        params = [nt.Parameter(h, dtype="bfloat16", device=DEV) for h in host]
+        optimizer = nt.optim.AdamW(_groups(params, shapes), master_weights=True, **OPTIONS)
+        scaler = nt.GradScaler(init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5,
+                               growth_interval=growth_interval)
+        for step, grads in enumerate(grads16):
+            scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+            for p, g in zip(params, grads):
+                p.grad = nt.Tensor(g, device=DEV)
+            if mode == "api":
+                finite = scaler.unscale_(optimizer)
+                updated = scaler.step(optimizer)
+                scaler.update()
+            else:
+                result = nt.amp.fused_step(optimizer, scaler)
+                finite, updated = result.finite, result.updated
+            assert finite == finite_flags[step] and updated == finite_flags[step], (mode, step)
+            assert scaler.get_scale() == scales[step], (mode, step)
+        for i, p in enumerate(params):
+            state = optimizer.state[id(p)]
+            assert state["step"] == count
+            _compare(f"{mode} master[{i}]", state["master"].numpy(), master[i])
+            _compare(f"{mode} m[{i}]", state["exp_avg"].numpy(), m[i])
+            _compare(f"{mode} v[{i}]", state["exp_avg_sq"].numpy(), v[i])
+            _compare(f"{mode} copy[{i}]", p.numpy(), copies[i])
+        _say(f"C3 {mode} matches the oracle")
+        del params, optimizer
+
+
+# ---- C4 --------------------------------------------------------------------------------------------
+def test_c4_gpt1p3b_width_bf16_clip_ten_steps(pool):
+    shapes = gpt2_shapes(vocab=50304, ctx=2048, d=2048, layers=2, ffn=8192)
+    assert total_params(shapes) == 207_757_312
+    host = [parallel.round_bf16(pool, h) for h in _normals(pool, shapes, 1337, 0.02)]
+    grads = []
+    for step in range(STEPS):
+        grads.append([parallel.round_bf16(pool, g) for g in _normals(pool, shapes, 1337 + 1000 + step, 1e-3)])
+    # Oracle: clip at 1.0 (always active here), then the master step with bfloat16 moments.
+    master = [h.copy() for h in host]
+    m = [np.zeros_like(h) for h in host]
+    v = [np.zeros_like(h) for h in host]
+    decays = [0.1 if k else 0.0 for k in decay_mask(shapes)]
+    norms = []
+    for step, step_grads in enumerate(grads, start=1):
+        norm = parallel.total_norm(pool, step_grads)
+        coefficient = oclip.clip_coefficient(1.0, norm)
+        assert coefficient < 1
+        clipped = [parallel.clip_apply(pool, g, coefficient, "bfloat16") for g in step_grads]
+        for i, g in enumerate(clipped):
+            parallel.master_step(pool, master[i], g, m[i], v[i], step, weight_decay=decays[i], state_bf16=True,
+                                 **OPTIONS)
+        norms.append(norm)
+    copies = [parallel.round_bf16(pool, x) for x in master]
+    _say(f"C4 oracle done: norms {norms[0]:.6g} .. {norms[-1]:.6g}")
+    for mode in ("api", "fused"):
+        params = [nt.Parameter(h, dtype="bfloat16", device=DEV) for h in host]
+        optimizer = nt.optim.AdamW(_groups(params, shapes), master_weights=True, state_dtype="bfloat16", **OPTIONS)
+        for step, step_grads in enumerate(grads):
+            for p, g in zip(params, step_grads):
+                # bfloat16-valued float32 -> bfloat16 is exact; converted on the device.
+                p.grad = nt.Tensor(torch.from_numpy(g).to(DEV).to(torch.bfloat16))
+            if mode == "api":
+                norm = nt.optim.clip_grad_norm_(params, 1.0).item()
+                optimizer.step()
+            else:
+                norm = nt.amp.fused_step(optimizer, None, max_norm=1.0).norm
+            assert abs(norm - norms[step]) <= NORM_RTOL * norms[step], (mode, step, norm, norms[step])
+        flips = 0
+        for i, p in enumerate(params):
+            state = optimizer.state[id(p)]
+            assert state["step"] == STEPS
+            flips += _compare(f"{mode} master[{i}]", state["master"].numpy(), master[i], unit_bits=32, allow_rate=1e-6)
+            flips += _compare(f"{mode} m[{i}]", state["exp_avg"].numpy(), m[i], unit_bits=16, allow_rate=1e-6)
+            flips += _compare(f"{mode} v[{i}]", state["exp_avg_sq"].numpy(), v[i], unit_bits=16, allow_rate=1e-6)
+            flips += _compare(f"{mode} copy[{i}]", p.numpy(), copies[i], unit_bits=16, allow_rate=1e-6)
+        _say(f"C4 {mode} matches the oracle ({flips} elements one unit away)")
+        del params, optimizer

@@ -188,3 +188,32 @@ def test_host_bf16_conversion_matches_torch():
     assert np.array_equal(t.bits(), lowp.f64_to_bf16(x))
     agree = np.mean(t.bits() == want.view(torch.int16).numpy().view(np.uint16))
     assert agree > 0.999
+
+
+def test_scalar_promotion_matches_reference_fixture_dtypes(golden_dir):
+    """The host's promotion and operand rounding (what nt_tensor_scalar is
+    given) agree with the reference's result dtypes and with the oracle's
+    operand values for every scalar_ops.npz case."""
+    from namitorch_amd.dtype import from_numpy_dtype, promote_with_scalar, round_scalar, scalar_dtype
+    from oracle import arith
+    from test_oracle import scalar_fixture_cases
+    data = np.load(golden_dir / "scalar_ops.npz")
+    for key, loss, operand, op in scalar_fixture_cases(data):
+        tensor_dtype = from_numpy_dtype(loss.dtype)
+        kind = scalar_dtype(operand)
+        result = promote_with_scalar(tensor_dtype, kind)
+        assert result.numpy_dtype == data[key].dtype, key
+        want = np.asarray(operand, dtype=arith.operand_dtype(operand)).astype(data[key].dtype)
+        assert round_scalar(operand, kind, result) == float(want), key
+
+
+def test_scalar_promotion_bfloat16_extension():
+    from namitorch_amd.dtype import bfloat16, float16, float32, float64, int64, promote_with_scalar, round_scalar
+    assert promote_with_scalar(bfloat16, int64) is bfloat16
+    assert promote_with_scalar(bfloat16, float16) is float32
+    assert promote_with_scalar(bfloat16, float32) is float32
+    assert promote_with_scalar(bfloat16, float64) is float64
+    assert promote_with_scalar(float16, float32) is float32
+    assert round_scalar(3, int64, bfloat16) == 3.0
+    assert round_scalar(257, int64, bfloat16) == 256.0        # ties to even at 8 significant bits
+    assert round_scalar(259, int64, bfloat16) == 260.0

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import adam, clip, grads, lowp, scaler
+from oracle import adam, arith, clip, grads, lowp, scaler
 
 GOLDEN_CASES = ["adamw_f32", "adamw_f32_maximize", "adamw_f32_lr0", "adamw_f32_wd0", "adamw_f32_defaults",
                 "adam_f32_coupled", "adamw_f32_bfgrads", "adamw_f32_special", "adamw_f16", "adamw_f64"]
@@ -289,3 +289,129 @@ def test_accumulate_oracle_bf16_against_torch_and_exact_sums():
     exact = a.astype(np.float64) + b.astype(np.float64)
     assert np.array_equal((a + b).astype(np.float64), exact)
     assert grads.accumulate(None, incoming, "bfloat16").tobytes() == t_in.numpy().tobytes()
+
+
+# ---- Tensor-by-scalar arithmetic (GradScaler.scale, loss / accum) -------------------------
+SCALAR_OPERANDS = {"int3": 3, "int7": 7, "int1000": 1000, "float3": 3.0, "float0.1": 0.1,
+                   "f16_3": np.float16(3.0), "f64_3": np.float64(3.0), "f64_0.1": np.float64(0.1)}
+
+
+def scalar_fixture_cases(data):
+    """(key, loss, operand, op) for every entry of scalar_ops.npz."""
+    cases = []
+    for key in sorted(data):
+        if key.endswith("_loss"):
+            continue
+        dtype, op, label = key.split("_", 2)
+        if op == "scale":
+            operand = float(label)
+            op = "mul"
+        else:
+            operand = SCALAR_OPERANDS[label]
+        cases.append((key, data[f"{dtype}_loss"], operand, op))
+    return cases
+
+
+def test_scalar_oracle_matches_reference_golden(golden_dir):
+    data = np.load(golden_dir / "scalar_ops.npz")
+    cases = scalar_fixture_cases(data)
+    assert len(cases) == 39
+    for key, loss, operand, op in cases:
+        got = arith.scalar_op(loss, operand, op)
+        assert got.dtype == data[key].dtype, key
+        assert got.tobytes() == data[key].tobytes(), key
+
+
+def test_scalar_oracle_promotion_closed_form():
+    """float16 loss times the loss scale is float32 and exact for powers of
+    two; division is IEEE true division in the promoted dtype."""
+    loss = np.float16([3.0, -2.5, 65504.0, 1e-5])
+    scaled = arith.scale_loss(loss, 65536.0)
+    assert scaled.dtype == np.float32
+    assert np.array_equal(scaled, loss.astype(np.float32) * np.float32(65536.0))
+    assert np.isfinite(scaled).all()                   # float16 itself would overflow
+    q = arith.scalar_op(np.float32([1.0, 2.0, 10.0]), 3, "div")
+    assert [float(x) for x in q] == [float(np.float32(Fraction(n, 3))) for n in (1, 2, 10)]
+
+
+# ---- float64 gradient norms whose squares leave the float64 range -------------------------
+def test_clip_oracle_float64_extremes_match_reference_golden(golden_dir):
+    data = np.load(golden_dir / "clip_f64.npz")
+    records = json.loads(str(data["records"]))
+    assert len(records) == 6
+    for record in records:
+        key = record["key"]
+        grads = [data[f"{key}_in{i}"] for i in range(record["count"])]
+        with np.errstate(under="ignore"):
+            norm, clipped = clip.clip_grad_norm(grads, record["max_norm"], record["norm_type"])
+        assert norm == record["norm"], key
+        for i, g in enumerate(clipped):
+            assert g.tobytes() == data[f"{key}_out{i}"].tobytes(), (key, i)
+
+
+def test_clip_float64_direct_sum_fails_where_prescale_is_needed(golden_dir):
+    """The reference's max-abs prescale matters for float64: sqrt(sum g^2)
+    overflows at |g| ~ 1e200 and underflows at 1e-200, while the prescaled
+    norm is finite and positive (the device switches to the prescaled pass
+    there)."""
+    data = np.load(golden_dir / "clip_f64.npz")
+    for key, bad in (("clip64_huge_2", math.inf), ("clip64_tiny_2", 0.0)):
+        grads = [data[f"{key}_in{i}"] for i in range(3)]
+        with np.errstate(over="ignore", under="ignore"):
+            direct = math.sqrt(sum(float(np.sum(g * g)) for g in grads))
+        assert direct == bad
+        assert 0 < clip.total_norm(grads) < math.inf
+
+
+def test_clip_norm_formulations_round_differently():
+    """sqrt(sum g^2) and the reference's amax*power(sum (g/amax)^2, 0.5) are
+    different roundings of the same real number: on ordinary data they differ
+    in the last bits but stay within 1e-12 relative, the tolerance the device
+    norm is held to."""
+    rng = np.random.default_rng(5)
+    differ = 0
+    for trial in range(200):
+        grads = [(rng.standard_normal(int(rng.integers(1, 400))) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32)
+                 for _ in range(3)]
+        direct = math.sqrt(sum(float(np.sum(g.astype(np.float64) ** 2)) for g in grads))
+        reference = clip.total_norm(grads)
+        differ += direct != reference
+        assert abs(direct - reference) <= 1e-12 * reference
+    assert differ > 0
+
+
+# ---- chunked evaluation (oracle.parallel) -----------------------------------------------
+def test_parallel_oracle_equals_plain_oracle():
+    """Slice-wise, threaded evaluation gives the plain oracle's bits: sizes
+    straddle the 1 Mi-element slice boundary; moments in float32 and bfloat16;
+    norms with the per-tensor order kept."""
+    from oracle import parallel
+    rng = np.random.default_rng(77)
+    sizes = [parallel.SLICE + 4097, 3, parallel.SLICE, 70001]
+    options = dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
+    with parallel.Pool(4) as pool:
+        for n in sizes:
+            p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+            g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+            m = (rng.standard_normal(n) * 1e-4).astype(np.float32)
+            v = np.abs(rng.standard_normal(n) * 1e-6).astype(np.float32)
+            a = [x.copy() for x in (p, g, m, v)]
+            b = [x.copy() for x in (p, g, m, v)]
+            adam.adam_step(*a, 3, **options)
+            parallel.adam_step(pool, *b, 3, **options)
+            assert all(x.tobytes() == y.tobytes() for x, y in zip(a, b))
+            mb, vb = lowp.round_bf16(m), lowp.round_bf16(v)
+            a = [p.copy(), lowp.round_bf16(g), mb.copy(), vb.copy()]
+            b = [x.copy() for x in a]
+            adam.master_step(*a, 3, state_bf16=True, **options)
+            parallel.master_step(pool, *b, 3, state_bf16=True, **options)
+            assert all(x.tobytes() == y.tobytes() for x, y in zip(a, b))
+            g16 = (g * 65536).astype(np.float16)
+            assert parallel.unscale(pool, g16, 65536.0, "float16").tobytes() == scaler.unscale(g16, 65536.0, "float16").tobytes()
+            assert parallel.clip_apply(pool, g, 0.3, "bfloat16").tobytes() == clip.clip_apply(g, 0.3, "bfloat16").tobytes()
+            assert parallel.round_bf16(pool, p).tobytes() == lowp.round_bf16(p).tobytes()
+        grads = [(rng.standard_normal(n) * 1e-3).astype(np.float32) for n in sizes]
+        for order in (2.0, 3.0, np.inf):
+            assert parallel.total_norm(pool, grads, order) == clip.total_norm(grads, order)
+        grads[1][1] = np.nan
+        assert math.isnan(parallel.total_norm(pool, grads)) and not parallel.finite(pool, grads)
