@@ -14,7 +14,7 @@ pool by ``oracle.parallel``, which gives the oracle's bits):
   (step, tensor, element), GradScaler(65536, x2, x0.5, 2000) and a
   growth_interval 3 variant that grows within the run;
 * C4: the GPT-1.3B layout at its real width (d 2048, vocab 50304, ctx 2048)
-  with 2 layers (207.8 M parameters): float32 master, bfloat16
+  with 2 layers (207.9 M parameters): float32 master, bfloat16
   parameters/moments/gradients, clip_grad_norm_ at 1.0 (active every step).
 
 Bars: found_inf flags, skip decisions and the
@@ -196,7 +196,7 @@ def test_c3_gpt2_amp_ten_steps(pool, poison, growth_interval):
 # ---- C4 --------------------------------------------------------------------------------------------
 def test_c4_gpt1p3b_width_bf16_clip_ten_steps(pool):
     shapes = gpt2_shapes(vocab=50304, ctx=2048, d=2048, layers=2, ffn=8192)
-    assert total_params(shapes) == 207_757_312
+    assert total_params(shapes) == 207_937_536
     host = [parallel.round_bf16(pool, h) for h in _normals(pool, shapes, 1337, 0.02)]
     grads = []
     for step in range(STEPS):
