@@ -112,7 +112,8 @@ typedef struct nt_adamw_coefs64 {
  * nt_amp_finalize(); read by nt_adamw_mt() when a grad transform points at it.
  */
 typedef struct nt_amp_ctrl {
-    double sumsq;          /* sum of squares of the (unscaled) grads, fp64 */
+    double sumsq;          /* sum of squares of the (unscaled) grads, fp64;
+                              undefined when found_inf is set */
     double amax;           /* max |g| over finite grads, fp64 */
     double norm;           /* global grad norm (fp64), reference semantics */
     double clip_coef;      /* max_norm / (norm + 1e-6) */
@@ -317,6 +318,30 @@ int32_t nt_grad_zero(nt_plan *plan, void *stream);
  * gradient of a leaf).
  */
 int32_t nt_grad_accumulate(nt_plan *plan, int32_t assign, void *stream);
+
+/*
+ * nt_amp_prepass followed by nt_amp_finalize over one flat gradient buffer
+ * grad[count] of `grad_dtype` (NT_F32, NT_F16, NT_BF16) on `device`,
+ * allocating nothing: no plan, no hipMalloc, no library allocation.  No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation), e.g. over a flat gradient bucket.  Arguments and the block
+ * written to `ctrl` mean what they mean for that pair (unscale by `scale`,
+ * or by carry->scale when `carry` is given; norm_type 2 or +inf only).  The
+ * per-workgroup partials live in a fixed 64 KiB device array of the library
+ * (4096 partials), one per GPU, held until the process ends; count is at
+ * most 2**40 elements (NT_ERR_VALUE beyond, nothing launched).  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (on different
+ * streams, or from several threads) race and must be serialized by the
+ * caller.  Nothing in it needs clearing between calls: each call writes all
+ * the partials it reads.
+ */
+int32_t nt_amp_flat_stats_noalloc(int32_t device, const void *grad, int32_t grad_dtype,
+                                  uint64_t count, float scale, int32_t unscale,
+                                  nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry,
+                                  double norm_type, double max_norm, int32_t flags,
+                                  double growth_factor, double backoff_factor,
+                                  int32_t growth_interval, void *stream);
 
 /* ---- small single-array kernels ---------------------------------------- */
 

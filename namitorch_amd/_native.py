@@ -143,6 +143,8 @@ SIGNATURES = {
     "nt_ctrl_carry": (c_int32, [c_void_p, c_void_p, c_void_p]),
     "nt_tensor_scalar": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_double, c_int32, c_void_p, c_uint64, c_void_p]),
     "nt_any_negative": (c_int32, [c_void_p, c_int32, c_uint64, c_void_p, c_void_p]),
+    "nt_amp_flat_stats_noalloc": (c_int32, [c_int32, c_void_p, c_int32, c_uint64, c_float, c_int32, c_void_p, c_void_p,
+                                            c_double, c_double, c_int32, c_double, c_double, c_int32, c_void_p]),
     "nt_stream_probe": (c_int32, [ctypes.POINTER(c_void_p), c_int32, c_int32, ctypes.POINTER(c_void_p), c_int32, c_int32,
                                   c_uint64, c_void_p]),
 }

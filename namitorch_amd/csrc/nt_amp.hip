@@ -7,6 +7,8 @@
 // atomics are used.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "nt_internal.hpp"
 
 namespace nt {
@@ -731,6 +733,82 @@ static uint64_t small_grid(uint64_t n) {
     return b ? b : 1;
 }
 
+// ---- plan-free pre-pass over one flat gradient buffer, allocating nothing ----------
+// nt_amp_flat_stats_noalloc's per-workgroup partials live in `scratch`, a
+// fixed device array of this file: every GPU holds its own copy for the life
+// of the process.  Host code never uses the array's name as an address; it
+// resolves the device address once per device (hipGetSymbolAddress, with that
+// device current) and passes that pointer to the kernels.
+constexpr int kFlatPartials = 4096;                          // 64 KiB of partials
+constexpr int kFlatUnroll = 4;                               // 4-element groups per lane per iteration
+constexpr uint64_t kFlatMaxCount = uint64_t(1) << 40;
+constexpr int kFlatMaxDevices = 64;
+static __device__ __align__(256) Partial scratch[kFlatPartials];
+
+static std::mutex g_scratch_lock;
+static Partial *g_scratch_address[kFlatMaxDevices] = {};
+
+// Device address of `scratch` on `device` (which must be current).
+static int32_t flat_scratch(int32_t device, Partial **out) {
+    std::lock_guard<std::mutex> lock(g_scratch_lock);
+    if (g_scratch_address[device] == nullptr) {
+        void *address = nullptr;
+        NT_HIP_TRY(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_scratch_address[device] = static_cast<Partial *>(address);
+    }
+    *out = g_scratch_address[device];
+    return NT_OK;
+}
+
+// Grid-stride pass over grad[0, count): each workgroup writes one partial
+// (fp64 sum of squares of the finite unscaled values, max |g'| with inf/NaN
+// encoded) to partials[blockIdx.x]; the grid never exceeds kFlatPartials.
+template <class G>
+__global__ __launch_bounds__(kBlock) void flat_prepass_kernel(const typename G::raw *__restrict__ grad, uint64_t count,
+                                                              int32_t aligned, Xform xf, const nt_amp_ctrl *carry,
+                                                              Partial *__restrict__ partials) {
+    __shared__ WaveJoin join;
+    wave_join_init(join);
+    if (carry != nullptr && xf.unscale) xf.scale = ctrl_scale_inv(carry->scale, xf.unscale, xf.inv_scale);
+    PAcc acc;
+    uint64_t scalar_from = 0;
+    if (aligned) {
+        const uint64_t vend = count & ~(uint64_t)(kVec - 1);
+        const uint64_t stride = (uint64_t)gridDim.x * kBlock * kVec * kFlatUnroll;
+        for (uint64_t base = (uint64_t)blockIdx.x * kBlock * kVec * kFlatUnroll + (uint64_t)threadIdx.x * kVec;
+             base < vend; base += stride) {
+            float g[kFlatUnroll][kVec];
+#pragma unroll
+            for (int u = 0; u < kFlatUnroll; ++u) {
+                const uint64_t i = base + (uint64_t)u * kBlock * kVec;
+                if (i < vend) {
+                    Vec4IO<G, true>::load(grad, i, g[u]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < kVec; ++k) g[u][k] = 0.0f;     // adds nothing to either statistic
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kFlatUnroll; ++u)
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) pacc_wide(acc, unscale_one<G>(g[u][k], xf));
+        }
+        scalar_from = vend;
+    }
+    for (uint64_t i = scalar_from + (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < count;
+         i += (uint64_t)gridDim.x * kBlock)
+        pacc_wide(acc, unscale_one<G>(load1<G>(grad, i), xf));
+    const Partial mine{wave_sum(acc.sumsq), amax_from_bits(wave_max_u32(acc.amax_bits))};
+    wave_join_finish(join, mine, partials + blockIdx.x);
+}
+
+template <class G>
+static void launch_flat_prepass(dim3 grid, hipStream_t s, const void *grad, uint64_t count, int32_t aligned,
+                                Xform xf, const nt_amp_ctrl *carry, Partial *partials) {
+    flat_prepass_kernel<G><<<grid, dim3(kBlock), 0, s>>>(static_cast<const typename G::raw *>(grad), count, aligned,
+                                                         xf, carry, partials);
+}
+
 }  // namespace nt
 
 using namespace nt;
@@ -912,6 +990,64 @@ int32_t nt_any_negative(const void *array, int32_t dtype, uint64_t count, int32_
         default: return fail(NT_ERR_TYPE, "nt_any_negative: unsupported dtype");
     }
     NT_LAUNCH_CHECK("any_negative_kernel launch");
+    return NT_OK;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int32_t nt_amp_flat_stats_noalloc(int32_t device, const void *grad, int32_t grad_dtype, uint64_t count, float scale,
+                                  int32_t unscale, nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry, double norm_type,
+                                  double max_norm, int32_t flags, double growth_factor, double backoff_factor,
+                                  int32_t growth_interval, void *stream) {
+    clear_error();
+    if (device < 0 || device >= kFlatMaxDevices) return fail(NT_ERR_VALUE, "nt_amp_flat_stats_noalloc: invalid device");
+    if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
+    if (carry == ctrl) return fail(NT_ERR_VALUE, "nt_amp_flat_stats_noalloc: carry and ctrl must be different blocks");
+    if (!(norm_type == 2.0 || (__builtin_isinf(norm_type) && norm_type > 0.0)))
+        return fail(NT_ERR_VALUE, "nt_amp_flat_stats_noalloc: norm_type must be 2 or +inf");
+    if (flags & ~(NT_FINALIZE_SCALER_UPDATE | NT_FINALIZE_CLIP_IF_FINITE))
+        return fail(NT_ERR_VALUE, "nt_amp_flat_stats_noalloc: unknown flags");
+    if ((flags & NT_FINALIZE_SCALER_UPDATE) &&
+        (growth_interval <= 0 || !(growth_factor > 1.0) || !(backoff_factor > 0.0 && backoff_factor < 1.0)))
+        return fail(NT_ERR_VALUE, "invalid GradScaler growth/backoff settings");
+    if (grad_dtype != NT_F32 && grad_dtype != NT_F16 && grad_dtype != NT_BF16)
+        return fail(NT_ERR_TYPE, "nt_amp_flat_stats_noalloc: gradients must be float32, float16 or bfloat16");
+    if (count > kFlatMaxCount)
+        return fail(NT_ERR_VALUE, "nt_amp_flat_stats_noalloc: count " + std::to_string(count) +
+                                      " exceeds the maximum of 2**40 elements");
+    if (count > 0 && grad == nullptr) return fail(NT_ERR_VALUE, "nt_amp_flat_stats_noalloc: NULL gradient buffer");
+    if (unscale && carry == nullptr && !(scale > 0.0f && __builtin_isfinite(scale)))
+        return fail(NT_ERR_VALUE, "loss scale must be finite and positive");
+    DeviceGuard guard(device);
+    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
+    Partial *partials = nullptr;
+    int32_t rc = flat_scratch(device, &partials);
+    if (rc != NT_OK) return rc;
+    nt_grad_xform hx{};
+    hx.scale = unscale ? scale : 1.0f;
+    hx.unscale = unscale ? 1 : 0;
+    Xform xf = make_xform(unscale && carry == nullptr ? &hx : nullptr);
+    if (unscale && carry != nullptr) xf.unscale = 1;   // scale read from the carry block on the device
+    const uint64_t per_group = (uint64_t)kBlock * kVec * kFlatUnroll;
+    uint64_t groups = (count + per_group - 1) / per_group;
+    if (groups > (uint64_t)kFlatPartials) groups = kFlatPartials;
+    const uintptr_t alignment = grad_dtype == NT_F32 ? 16u : 8u;
+    const int32_t aligned = ((uintptr_t)grad % alignment) == 0 ? 1 : 0;
+    hipStream_t s = (hipStream_t)stream;
+    if (groups > 0) {
+        const dim3 grid((unsigned)groups);
+        switch (grad_dtype) {
+            case NT_F32: launch_flat_prepass<TF32>(grid, s, grad, count, aligned, xf, carry, partials); break;
+            case NT_F16: launch_flat_prepass<TF16>(grid, s, grad, count, aligned, xf, carry, partials); break;
+            default: launch_flat_prepass<TBF16>(grid, s, grad, count, aligned, xf, carry, partials); break;
+        }
+        NT_LAUNCH_CHECK("flat_prepass_kernel launch");
+    }
+    finalize_kernel<<<dim3(1), dim3(kBlock), 0, s>>>(partials, (int64_t)groups, ctrl, carry, norm_type, max_norm,
+                                                     flags, growth_factor, backoff_factor, growth_interval);
+    NT_LAUNCH_CHECK("finalize_kernel launch");
     return NT_OK;
 }
 
