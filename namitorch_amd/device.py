@@ -1,49 +1,93 @@
-"""Devices: ``cpu`` and ``cuda[:N]`` (HIP devices keep the reference's
-``cuda`` name, as PyTorch-ROCm does).  Mirrors ``namitorch/device.py``:
-the same accepted spellings and the same errors."""
+"""Devices: ``cpu`` and ``cuda[:N]``.
+
+HIP devices keep the reference's ``cuda`` name, as PyTorch-ROCm does.  The
+accepted spellings and the errors for everything else are those of
+``namitorch/device.py``: ``"cpu"``, ``"cuda"`` (device 0), ``"cuda:N"`` with
+N written without leading zeros, ``Device(...)`` copies, and an ``index``
+argument for a bare ``"cuda"``.
+
+Devices are immutable and interned: every spelling of one device yields the
+same object, so device comparisons on the hot path are identity checks.
+"""
 
 from __future__ import annotations
 
 import operator
-import re
 from numbers import Integral
+from threading import Lock
+
+_KINDS = ("cpu", "cuda")
+_ASCII_DIGITS = frozenset("0123456789")
+
+
+def _split(spec: str):
+    """(kind, index written in the string or None) of a device string."""
+    kind, colon, written = spec.partition(":")
+    if kind not in _KINDS:
+        return None
+    if not colon:
+        return kind, None
+    if not written or not set(written) <= _ASCII_DIGITS or (written[0] == "0" and written != "0"):
+        return None
+    return kind, int(written)
+
+
+def _ordinal(kind: str, index):
+    """The index a device of `kind` ends up with, checked."""
+    if kind == "cpu":
+        if index is not None:
+            raise ValueError("CPU devices do not have an index.")
+        return None
+    if index is None:
+        return 0
+    if isinstance(index, bool) or not isinstance(index, Integral):
+        raise TypeError("Device index must be a nonnegative integer.")
+    try:
+        index = operator.index(index)
+    except TypeError:
+        raise TypeError("Device index must be a nonnegative integer.") from None
+    if index < 0:
+        raise ValueError("Device index must be nonnegative.")
+    return index
 
 
 class Device:
     __slots__ = ("type", "index", "_hash")
 
-    def __init__(self, value="cpu", index=None):
+    _interned: dict = {}
+    _intern_lock = Lock()
+
+    def __new__(cls, value="cpu", index=None):
         if isinstance(value, Device):
             if index is not None:
                 raise ValueError("A Device cannot be combined with an index override.")
-            kind, ordinal = value.type, value.index
-        elif isinstance(value, str):
-            match = re.fullmatch(r"(cpu|cuda)(?::(0|[1-9][0-9]*))?", value)
-            if match is None:
-                raise ValueError(f"Unsupported device {value!r}; expected cpu, cuda or cuda:N.")
-            kind, embedded = match.groups()
-            if embedded is not None and index is not None:
-                raise ValueError("Specify the device index only once.")
-            ordinal = int(embedded) if embedded is not None else index
-            if kind == "cpu":
-                if ordinal is not None:
-                    raise ValueError("CPU devices do not have an index.")
-            else:
-                if ordinal is None:
-                    ordinal = 0
-                if isinstance(ordinal, bool) or not isinstance(ordinal, Integral):
-                    raise TypeError("Device index must be a nonnegative integer.")
-                ordinal = operator.index(ordinal)
-                if ordinal < 0:
-                    raise ValueError("Device index must be nonnegative.")
-        else:
+            return value
+        if not isinstance(value, str):
             raise TypeError("Device expects a device string or another Device.")
-        object.__setattr__(self, "type", kind)
-        object.__setattr__(self, "index", ordinal)
-        object.__setattr__(self, "_hash", hash((kind, ordinal)))
+        parsed = _split(value)
+        if parsed is None:
+            raise ValueError(f"Unsupported device {value!r}; expected cpu, cuda or cuda:N.")
+        kind, written = parsed
+        if written is not None and index is not None:
+            raise ValueError("Specify the device index only once.")
+        key = (kind, _ordinal(kind, written if written is not None else index))
+        found = cls._interned.get(key)
+        if found is None:
+            with cls._intern_lock:
+                found = cls._interned.get(key)
+                if found is None:
+                    found = object.__new__(cls)
+                    object.__setattr__(found, "type", key[0])
+                    object.__setattr__(found, "index", key[1])
+                    object.__setattr__(found, "_hash", hash(key))
+                    cls._interned[key] = found
+        return found
 
     def __setattr__(self, name, value):
         raise AttributeError("Device is immutable.")
+
+    def __reduce__(self):
+        return (Device, (str(self),))
 
     def __eq__(self, other):
         return self is other or (isinstance(other, Device) and self.type == other.type and self.index == other.index)

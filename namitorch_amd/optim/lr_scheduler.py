@@ -1,11 +1,18 @@
 """Learning-rate schedules over optimizer parameter groups.
 
-Same classes, arguments, learning rates and messages as
-``namitorch/optim/lr_scheduler.py:37-272`` (LRScheduler, StepLR, MultiStepLR,
-ExponentialLR, CosineAnnealingLR, LinearLR, WarmupCosine).  Each rate is a
-Python float computed on the host with the reference's expression, operation
-for operation, because AdamW rounds ``lr`` and ``1 - lr * weight_decay`` to
-the parameter dtype from exactly that float.
+Contract: the classes, arguments, rates, state dictionaries and messages of
+``namitorch/optim/lr_scheduler.py:37-272`` (LRScheduler, StepLR,
+MultiStepLR, ExponentialLR, CosineAnnealingLR, LinearLR, WarmupCosine).
+Each rate is a Python float computed on the host with the reference's
+expression, operation for operation, because AdamW rounds ``lr`` and
+``1 - lr * weight_decay`` to the parameter dtype from exactly that float.
+
+Structure: each schedule declares its configuration as an ordered list of
+field rules (``_FIELDS``: a name and its validator, or a check across the
+fields validated so far) and a rate rule — a factor applied to every base
+rate, or a fraction of the way from a floor to each base rate.  The base
+class does the rest: validation in rule order, the rate checks, applying
+rates to the groups, and the state dictionary.
 
 Device-side skips: after ``amp.fused_step`` the host does not yet know
 whether the step updated (the skip is decided on the GPU).  A scheduler
@@ -28,6 +35,7 @@ from numbers import Integral, Real
 from .optimizer import Optimizer
 
 
+# ---- value rules -------------------------------------------------------------------------
 def _integer(value, name: str, minimum: int = 0) -> int:
     if isinstance(value, bool) or not isinstance(value, Integral):
         raise TypeError(f"{name} must be an integer.")
@@ -49,16 +57,37 @@ def _rate(value, name: str) -> float:
     return value
 
 
-def _between(base_lrs, floor: float, fraction: float) -> list:
-    """floor + (base - floor) * fraction per group (the cosine families)."""
+def _count(minimum: int):
+    return lambda value, name: _integer(value, name, minimum)
+
+
+def _milestones(value, name):
+    if not isinstance(value, (list, tuple)):
+        raise TypeError("milestones must be a list or tuple of integers.")
+    return sorted(_integer(item, "milestone") for item in value)
+
+
+def _toward(base_lrs, floor: float, fraction: float) -> list:
+    """floor + (base - floor) * fraction for every group (cosine families)."""
     if any(floor > base for base in base_lrs):
         raise ValueError("Minimum learning rate cannot exceed a group's base learning rate.")
     return [floor + (base - floor) * fraction for base in base_lrs]
 
 
+def _half_cosine(progress: float) -> float:
+    return (1 + math.cos(math.pi * progress)) / 2
+
+
 class LRScheduler:
-    """Base schedule: constant rates.  Subclasses list their configuration
-    keys in ``_config_keys`` and compute rates in ``_compute_lrs``."""
+    """Constant schedule; subclasses add field rules and a rate rule."""
+
+    # (name, validator(value, name)) in validation order; a rule whose name
+    # is None is a check over the fields validated before it.
+    _FIELDS: tuple = ()
+
+    def __init_subclass__(cls, **kwargs):
+        super().__init_subclass__(**kwargs)
+        cls._config_keys = tuple(name for name, _ in cls._FIELDS if name is not None)
 
     _config_keys: tuple = ()
 
@@ -68,33 +97,40 @@ class LRScheduler:
         optimizer._registered_parameters()
         step = _integer(last_step, "last_step")
         config = self._normalize_config(configuration)
-        bases = []
-        for group in optimizer.param_groups:
-            if "lr" not in group:
-                raise ValueError("Every optimizer parameter group must define lr.")
-            _rate(group["lr"], "lr")
-            bases.append(_rate(group.get("initial_lr", group["lr"]), "initial_lr"))
+        bases = [self._group_base(group) for group in optimizer.param_groups]
         rates = self._checked_lrs(step, bases, config)
         self.optimizer = optimizer
         self.base_lrs = bases
         self.last_step = step
         self._group_signature = self._signature()
-        for name, value in config.items():
-            setattr(self, name, value)
+        self.__dict__.update(config)
         self._apply(rates)
 
-    # ---- configuration -------------------------------------------------------------------
+    @staticmethod
+    def _group_base(group: dict) -> float:
+        if "lr" not in group:
+            raise ValueError("Every optimizer parameter group must define lr.")
+        _rate(group["lr"], "lr")
+        return _rate(group.get("initial_lr", group["lr"]), "initial_lr")
+
+    # ---- configuration ------------------------------------------------------------------
     @classmethod
     def _normalize_config(cls, config: dict) -> dict:
         if not isinstance(config, dict) or set(config) != set(cls._config_keys):
             raise ValueError(f"{cls.__name__} configuration must contain {cls._config_keys}.")
-        return deepcopy(config)
+        checked = deepcopy(config)
+        for name, rule in cls._FIELDS:
+            if name is None:
+                rule(checked)
+            else:
+                checked[name] = rule(checked[name], name)
+        return checked
 
     def _configuration(self) -> dict:
         return self._normalize_config({name: getattr(self, name) for name in self._config_keys})
 
     def _signature(self):
-        return tuple(tuple(id(parameter) for parameter in group["params"]) for group in self.optimizer.param_groups)
+        return tuple(tuple(map(id, group["params"])) for group in self.optimizer.param_groups)
 
     def _validate_groups(self) -> None:
         self.optimizer._registered_parameters()
@@ -112,6 +148,9 @@ class LRScheduler:
             raise ValueError("Scheduled learning rate exceeds the finite supported range.") from None
         return [_rate(value, "scheduled lr") for value in rates]
 
+    def _bases(self) -> list:
+        return [_rate(value, "base_lr") for value in self.base_lrs]
+
     def _apply(self, rates: list) -> None:
         for group, base, value in zip(self.optimizer.param_groups, self.base_lrs, rates):
             group["initial_lr"] = base
@@ -125,8 +164,7 @@ class LRScheduler:
     def get_lr(self) -> list:
         self._settle()
         self._validate_groups()
-        bases = [_rate(value, "base_lr") for value in self.base_lrs]
-        return self._checked_lrs(_integer(self.last_step, "last_step"), bases, self._configuration())
+        return self._checked_lrs(_integer(self.last_step, "last_step"), self._bases(), self._configuration())
 
     def get_last_lr(self) -> list:
         self._settle()
@@ -138,11 +176,9 @@ class LRScheduler:
 
     def _advance(self) -> None:
         self._validate_groups()
-        step = _integer(self.last_step, "last_step") + 1
-        bases = [_rate(value, "base_lr") for value in self.base_lrs]
-        rates = self._checked_lrs(step, bases, self._configuration())
-        self._apply(rates)
-        self.last_step = step
+        following = _integer(self.last_step, "last_step") + 1
+        self._apply(self._checked_lrs(following, self._bases(), self._configuration()))
+        self.last_step = following
 
     # ---- state ----------------------------------------------------------------------------
     def state_dict(self) -> dict:
@@ -151,7 +187,7 @@ class LRScheduler:
             "version": 1,
             "scheduler": type(self).__name__,
             "last_step": int(self.last_step),
-            "base_lrs": [_rate(value, "base_lr") for value in self.base_lrs],
+            "base_lrs": self._bases(),
             "config": self._configuration(),
         }
 
@@ -167,9 +203,10 @@ class LRScheduler:
         if state["scheduler"] != type(self).__name__:
             raise ValueError("Saved scheduler type does not match the current scheduler.")
         step = _integer(state["last_step"], "last_step")
-        if not isinstance(state["base_lrs"], list) or len(state["base_lrs"]) != len(self.optimizer.param_groups):
+        saved_bases = state["base_lrs"]
+        if not isinstance(saved_bases, list) or len(saved_bases) != len(self.optimizer.param_groups):
             raise ValueError("Saved base_lrs must match the optimizer parameter group count.")
-        bases = [_rate(value, "base_lr") for value in state["base_lrs"]]
+        bases = [_rate(value, "base_lr") for value in saved_bases]
         config = self._normalize_config(state["config"])
         return step, bases, config, self._checked_lrs(step, bases, config)
 
@@ -177,38 +214,40 @@ class LRScheduler:
         step, bases, config, rates = prepared
         self.base_lrs = bases
         self.last_step = step
-        for name, value in config.items():
-            setattr(self, name, value)
+        self.__dict__.update(config)
         self._apply(rates)
 
     def load_state_dict(self, state: dict) -> None:
         self._apply_loaded_state(self._prepare_load_state_dict(state))
 
 
-class StepLR(LRScheduler):
+class _ScaledSchedule(LRScheduler):
+    """Rates are base * factor(step) for every group."""
+
+    def _factor(self, step: int, config: dict) -> float:
+        raise NotImplementedError
+
+    def _compute_lrs(self, step, base_lrs, config):
+        factor = self._factor(step, config)
+        return [base * factor for base in base_lrs]
+
+
+class StepLR(_ScaledSchedule):
     """base * gamma ** (step // step_size)."""
 
-    _config_keys = ("step_size", "gamma")
+    _FIELDS = (("step_size", _count(1)), ("gamma", _rate))
 
     def __init__(self, optimizer: Optimizer, step_size: int, gamma: float = 0.1, last_step: int = 0):
         super().__init__(optimizer, last_step, step_size=step_size, gamma=gamma)
 
-    @classmethod
-    def _normalize_config(cls, config: dict) -> dict:
-        config = super()._normalize_config(config)
-        config["step_size"] = _integer(config["step_size"], "step_size", 1)
-        config["gamma"] = _rate(config["gamma"], "gamma")
-        return config
-
-    def _compute_lrs(self, step, base_lrs, config):
-        factor = config["gamma"] ** (step // config["step_size"])
-        return [base * factor for base in base_lrs]
+    def _factor(self, step, config):
+        return config["gamma"] ** (step // config["step_size"])
 
 
-class MultiStepLR(LRScheduler):
-    """base * gamma ** (milestones passed)."""
+class MultiStepLR(_ScaledSchedule):
+    """base * gamma ** (number of milestones <= step)."""
 
-    _config_keys = ("milestones", "gamma")
+    _FIELDS = (("milestones", _milestones), ("gamma", _rate))
 
     def __init__(self, optimizer: Optimizer, milestones, gamma: float = 0.1, last_step: int = 0):
         if isinstance(milestones, (str, bytes, dict, set, frozenset)):
@@ -219,109 +258,70 @@ class MultiStepLR(LRScheduler):
             raise TypeError("milestones must be an ordered iterable of integers.") from None
         super().__init__(optimizer, last_step, milestones=milestones, gamma=gamma)
 
-    @classmethod
-    def _normalize_config(cls, config: dict) -> dict:
-        config = super()._normalize_config(config)
-        if not isinstance(config["milestones"], (list, tuple)):
-            raise TypeError("milestones must be a list or tuple of integers.")
-        config["milestones"] = sorted(_integer(value, "milestone") for value in config["milestones"])
-        config["gamma"] = _rate(config["gamma"], "gamma")
-        return config
-
-    def _compute_lrs(self, step, base_lrs, config):
-        factor = config["gamma"] ** bisect_right(config["milestones"], step)
-        return [base * factor for base in base_lrs]
+    def _factor(self, step, config):
+        return config["gamma"] ** bisect_right(config["milestones"], step)
 
 
-class ExponentialLR(LRScheduler):
+class ExponentialLR(_ScaledSchedule):
     """base * gamma ** step."""
 
-    _config_keys = ("gamma",)
+    _FIELDS = (("gamma", _rate),)
 
     def __init__(self, optimizer: Optimizer, gamma: float, last_step: int = 0):
         super().__init__(optimizer, last_step, gamma=gamma)
 
-    @classmethod
-    def _normalize_config(cls, config: dict) -> dict:
-        config = super()._normalize_config(config)
-        config["gamma"] = _rate(config["gamma"], "gamma")
-        return config
-
-    def _compute_lrs(self, step, base_lrs, config):
-        factor = config["gamma"] ** step
-        return [base * factor for base in base_lrs]
+    def _factor(self, step, config):
+        return config["gamma"] ** step
 
 
-class CosineAnnealingLR(LRScheduler):
-    """eta_min + (base - eta_min) * (1 + cos(pi * min(step, T_max) / T_max)) / 2."""
-
-    _config_keys = ("T_max", "eta_min")
-
-    def __init__(self, optimizer: Optimizer, T_max: int, eta_min: float = 0.0, last_step: int = 0):
-        super().__init__(optimizer, last_step, T_max=T_max, eta_min=eta_min)
-
-    @classmethod
-    def _normalize_config(cls, config: dict) -> dict:
-        config = super()._normalize_config(config)
-        config["T_max"] = _integer(config["T_max"], "T_max", 1)
-        config["eta_min"] = _rate(config["eta_min"], "eta_min")
-        return config
-
-    def _compute_lrs(self, step, base_lrs, config):
-        progress = min(step, config["T_max"]) / config["T_max"]
-        return _between(base_lrs, config["eta_min"], (1 + math.cos(math.pi * progress)) / 2)
-
-
-class LinearLR(LRScheduler):
+class LinearLR(_ScaledSchedule):
     """base * (start * (1 - p) + end * p), p = min(step, total_iters) / total_iters."""
 
-    _config_keys = ("start_factor", "end_factor", "total_iters")
+    _FIELDS = (("start_factor", _rate), ("end_factor", _rate), ("total_iters", _count(1)))
 
     def __init__(self, optimizer: Optimizer, start_factor: float = 1 / 3, end_factor: float = 1.0,
                  total_iters: int = 5, last_step: int = 0):
         super().__init__(optimizer, last_step, start_factor=start_factor, end_factor=end_factor, total_iters=total_iters)
 
-    @classmethod
-    def _normalize_config(cls, config: dict) -> dict:
-        config = super()._normalize_config(config)
-        config["start_factor"] = _rate(config["start_factor"], "start_factor")
-        config["end_factor"] = _rate(config["end_factor"], "end_factor")
-        config["total_iters"] = _integer(config["total_iters"], "total_iters", 1)
-        return config
+    def _factor(self, step, config):
+        progress = min(step, config["total_iters"]) / config["total_iters"]
+        return config["start_factor"] * (1 - progress) + config["end_factor"] * progress
+
+
+class CosineAnnealingLR(LRScheduler):
+    """eta_min + (base - eta_min) * (1 + cos(pi * min(step, T_max) / T_max)) / 2."""
+
+    _FIELDS = (("T_max", _count(1)), ("eta_min", _rate))
+
+    def __init__(self, optimizer: Optimizer, T_max: int, eta_min: float = 0.0, last_step: int = 0):
+        super().__init__(optimizer, last_step, T_max=T_max, eta_min=eta_min)
 
     def _compute_lrs(self, step, base_lrs, config):
-        progress = min(step, config["total_iters"]) / config["total_iters"]
-        factor = config["start_factor"] * (1 - progress) + config["end_factor"] * progress
-        return [base * factor for base in base_lrs]
+        return _toward(base_lrs, config["eta_min"], _half_cosine(min(step, config["T_max"]) / config["T_max"]))
+
+
+def _warmup_before_total(config: dict) -> None:
+    if config["warmup_steps"] >= config["total_steps"]:
+        raise ValueError("warmup_steps must be smaller than total_steps.")
 
 
 class WarmupCosine(LRScheduler):
     """Linear warm-up to the base rate over warmup_steps, then cosine decay
     to min_lr at total_steps (the training runner's schedule)."""
 
-    _config_keys = ("warmup_steps", "total_steps", "min_lr")
+    _FIELDS = (("warmup_steps", _count(0)), ("total_steps", _count(1)), (None, _warmup_before_total),
+               ("min_lr", _rate))
 
     def __init__(self, optimizer: Optimizer, warmup_steps: int, total_steps: int, min_lr: float = 0.0,
                  last_step: int = 0):
         super().__init__(optimizer, last_step, warmup_steps=warmup_steps, total_steps=total_steps, min_lr=min_lr)
 
-    @classmethod
-    def _normalize_config(cls, config: dict) -> dict:
-        config = super()._normalize_config(config)
-        config["warmup_steps"] = _integer(config["warmup_steps"], "warmup_steps")
-        config["total_steps"] = _integer(config["total_steps"], "total_steps", 1)
-        if config["warmup_steps"] >= config["total_steps"]:
-            raise ValueError("warmup_steps must be smaller than total_steps.")
-        config["min_lr"] = _rate(config["min_lr"], "min_lr")
-        return config
-
     def _compute_lrs(self, step, base_lrs, config):
-        _between(base_lrs, config["min_lr"], 1.0)
-        warmup, total = config["warmup_steps"], config["total_steps"]
+        floor, warmup, total = config["min_lr"], config["warmup_steps"], config["total_steps"]
+        _toward(base_lrs, floor, 1.0)                 # every base at least the floor
         if step < warmup:
             return [base * (step / warmup) for base in base_lrs]
-        progress = (min(step, total) - warmup) / (total - warmup)
-        return _between(base_lrs, config["min_lr"], (1 + math.cos(math.pi * progress)) / 2)
+        return _toward(base_lrs, floor, _half_cosine((min(step, total) - warmup) / (total - warmup)))
 
 
 __all__ = ["LRScheduler", "StepLR", "MultiStepLR", "ExponentialLR", "CosineAnnealingLR", "LinearLR", "WarmupCosine"]

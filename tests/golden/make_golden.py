@@ -497,9 +497,33 @@ def clip_f64_cases(nt):
     return [record["key"] for record in records]
 
 
+DEVICE_SPELLINGS = ["cpu", "cuda", "cuda:0", "cuda:1", "cuda:01", "cuda:", "cpu:0", "gpu", "cuda:12", "CUDA",
+                    "cuda:१", "cuda: 1", " cuda", "cuda:-1", 5, None]
+DEVICE_INDICES = [None, 0, 1, -1, True, 1.0, 2]
+
+
+def device_cases(nt):
+    """Device(value, index) outcomes (namitorch/device.py): the string or the
+    exception class and message, for spellings x index arguments, and for
+    Device copies."""
+    from namitorch.device import Device
+
+    def outcome(value, index):
+        try:
+            made = Device(value, index)
+            return ["ok", str(made), repr(made)]
+        except Exception as error:            # the outcome is the fixture
+            return [type(error).__name__, str(error)]
+
+    records = [[value, index, outcome(value, index)] for value in DEVICE_SPELLINGS for index in DEVICE_INDICES]
+    copies = [[value, index, outcome(Device(value), index)] for value in ("cpu", "cuda:3") for index in DEVICE_INDICES]
+    (HERE / "devices.json").write_text(json.dumps({"spellings": records, "copies": copies}, indent=1) + "\n")
+    return len(records) + len(copies)
+
+
 # Fixture sets that write their own files (and keep their records there);
 # `--only name,...` regenerates just those.
-STANDALONE = {"scalar_ops": scalar_cases, "clip_f64": clip_f64_cases}
+STANDALONE = {"scalar_ops": scalar_cases, "clip_f64": clip_f64_cases, "devices": device_cases}
 
 
 def main(reference: str, only: list[str] | None = None) -> None:

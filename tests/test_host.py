@@ -217,3 +217,24 @@ def test_scalar_promotion_bfloat16_extension():
     assert round_scalar(3, int64, bfloat16) == 3.0
     assert round_scalar(257, int64, bfloat16) == 256.0        # ties to even at 8 significant bits
     assert round_scalar(259, int64, bfloat16) == 260.0
+
+
+def test_device_spellings_match_reference(golden_dir):
+    """Every Device(value, index) outcome — the device or the exception class
+    and message — is the reference's (tests/golden/devices.json)."""
+    from namitorch_amd.device import Device
+    data = json.loads((golden_dir / "devices.json").read_text())
+
+    def outcome(make):
+        try:
+            made = make()
+            return ["ok", str(made), repr(made)]
+        except Exception as error:
+            return [type(error).__name__, str(error)]
+
+    for value, index, want in data["spellings"]:
+        assert outcome(lambda: Device(value, index)) == want, (value, index)
+    for value, index, want in data["copies"]:
+        assert outcome(lambda: Device(Device(value), index)) == want, (value, index)
+    assert Device("cuda") is Device("cuda:0") is Device("cuda", 0)
+    assert Device("cpu") == Device(Device("cpu")) and hash(Device("cuda:2")) == hash(Device("cuda", 2))
