@@ -63,6 +63,8 @@ def parse_args():
     parser.add_argument("--kernel-only", action="store_true", help="only the C2 kernel loop (for profilers)")
     parser.add_argument("--calibrate", action="store_true",
                         help="with --kernel-only: also run 3 plain 1 GiB device copies (known bytes, for PMC scaling)")
+    parser.add_argument("--profile", default=None, choices=sorted(MIXED),
+                        help="only this config's fused step (for profilers): --warmup untimed, --steps timed")
     return parser.parse_args()
 
 
@@ -98,6 +100,14 @@ def event_pair(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
+def median_interval(marks) -> float:
+    """Median of the intervals between consecutive recorded events (ms): the
+    per-step times on the device timeline, launch gaps included."""
+    intervals = sorted(a.elapsed_time(b) for a, b in zip(marks, marks[1:]))
+    middle = len(intervals) // 2
+    return intervals[middle] if len(intervals) % 2 else 0.5 * (intervals[middle - 1] + intervals[middle])
+
+
 # ---- C2: the headline ----------------------------------------------------------------------------
 def bench_c2(nt, torch, steps, warmup):
     from namitorch_amd.param_lists import gpt2_shapes, total_params
@@ -108,18 +118,22 @@ def bench_c2(nt, torch, steps, warmup):
     optimizer = nt.optim.AdamW(decay_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8)
     for _ in range(warmup):
         optimizer.step()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     torch.cuda.synchronize()
     start = time.perf_counter()
-    for _ in range(steps):
+    for k in range(steps):
+        marks[k].record()
         optimizer.step()
+    marks[steps].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
     ms_per_step = elapsed * 1e3 / steps
+    median_ms = median_interval(marks)
     # Dominant kernel: re-launch the cached plan back to back between HIP events
     # on the launch stream (torch's current stream, where the library launches).
     kernel_ms = kernel_time_c2(nt, torch, optimizer, params, steps)
     result = dict(params=n, tensors=len(shapes), ms_per_step=ms_per_step, params_per_s=n / (ms_per_step / 1e3),
-                  kernel_ms=kernel_ms, bytes_per_param=28)
+                  median_ms_per_step=median_ms, kernel_ms=kernel_ms, bytes_per_param=28)
     del optimizer, params
     torch.cuda.empty_cache()
     return result
@@ -226,17 +240,22 @@ def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype
 
         for _ in range(warmup):
             one_step()
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
         torch.cuda.synchronize()
         start_wall = time.perf_counter()
-        for _ in range(steps):
+        for k in range(steps):
+            marks[k].record()
             one_step()
+        marks[steps].record()
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - start_wall) * 1e3 / steps
-        result[mode] = dict(ms_per_step=wall_ms, params_per_s=n / (wall_ms / 1e3),
+        median_ms = median_interval(marks)
+        result[mode] = dict(ms_per_step=wall_ms, median_ms_per_step=median_ms, params_per_s=n / (wall_ms / 1e3),
                             GBps=bytes_per_param * n / wall_ms / 1e6,
                             pct_hbm_peak=100 * bytes_per_param * n / wall_ms / 1e6 / HBM_PEAK_GBPS,
+                            median_pct_hbm_peak=100 * bytes_per_param * n / median_ms / 1e6 / HBM_PEAK_GBPS,
                             scale=None if scaler is None else scaler.get_scale())
-        log(f"{name} {mode}: {wall_ms:.3f} ms/step")
+        log(f"{name} {mode}: {wall_ms:.3f} ms/step (median {median_ms:.3f})")
         for p in params:
             p._grad = None
         del optimizer, scaler
@@ -422,26 +441,20 @@ def bench_chunks(nt, torch, launches=20, reps=4):
 
 
 # ---- CPU baseline ---------------------------------------------------------------------------------------
-def cpu_baseline(min_seconds=10.0, max_steps=40):
-    """NumPy oracle AdamW (the reference's NumPy path restated op for op) over
-    the whole GPT-2-124M list (the C2 workload): one untimed step, then timed
-    steps until `min_seconds` have elapsed (at least two, at most `max_steps`)."""
-    import numpy as np
-    from namitorch_amd.param_lists import gpt2_shapes
-    from oracle import adam as oadam
-    shapes = gpt2_shapes()
-    total = sum(int(np.prod(s)) for s in shapes)
-    rng = np.random.Generator(np.random.PCG64(1337))
-    params = [(rng.standard_normal(int(np.prod(s)), dtype=np.float32) * np.float32(0.02)) for s in shapes]
-    grads = [(rng.standard_normal(p.size, dtype=np.float32) * np.float32(1e-3)) for p in params]
-    ms = [np.zeros_like(p) for p in params]
-    vs = [np.zeros_like(p) for p in params]
-    wds = [0.1 if len(s) >= 2 else 0.0 for s in shapes]
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else what platform reports."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-    def step(k):
-        for p, g, m, v, wd in zip(params, grads, ms, vs, wds):
-            oadam.adam_step(p, g, m, v, k, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
 
+def _timed_steps(step, min_seconds, max_steps):
+    """One untimed step, then timed steps until `min_seconds` have passed
+    (at least two, at most `max_steps`); (steps, seconds)."""
     step(1)
     steps = 0
     start = time.perf_counter()
@@ -450,13 +463,152 @@ def cpu_baseline(min_seconds=10.0, max_steps=40):
         steps += 1
         elapsed = time.perf_counter() - start
         if steps >= max_steps or (steps >= 2 and elapsed >= min_seconds):
-            break
+            return steps, elapsed
+
+
+def _host_tensors(shapes, seed, sigma, dtype="float32"):
+    import numpy as np
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return [(rng.standard_normal(int(np.prod(s)), dtype=np.float32) * np.float32(sigma)).astype(dtype) for s in shapes]
+
+
+def _baseline_record(total, steps, elapsed, bytes_per_param, sample, *, extrapolated_to=None):
     value = total * steps / elapsed
-    return dict(value=value, unit="params/s", cores=1, kind="port",
-                sample=f"NumPy oracle AdamW over the full GPT-2-124M list ({len(shapes)} tensors, {total} params), "
-                       f"{steps} timed steps after 1 untimed step; {elapsed:.2f} s; host {platform.processor() or platform.machine()}, "
-                       f"os.cpu_count()={os.cpu_count()} (NumPy ufuncs are single-threaded)",
-                GBps=28 * value / 1e9)
+    record = dict(value=value, unit="params/s", cores=1, kind="port", GBps=bytes_per_param * value / 1e9,
+                  sample=f"{sample}; {steps} timed steps after 1 untimed step, {elapsed:.2f} s; host CPU {cpu_model()}, "
+                         f"os.cpu_count()={os.cpu_count()}, 1 thread (NumPy ufuncs are single-threaded)")
+    if extrapolated_to is not None:
+        record["extrapolated"] = True
+        record["sample"] += (f"; extrapolated linearly by parameter count to the full list ({extrapolated_to} params): "
+                             f"{extrapolated_to / value:.1f} s per step")
+    return record
+
+
+def cpu_baseline(min_seconds=10.0, max_steps=40):
+    """C2 (the headline): NumPy oracle AdamW — the reference's NumPy path
+    (optim/adam.py:27-42) restated op for op — over the whole GPT-2-124M
+    list."""
+    import numpy as np
+    from namitorch_amd.param_lists import gpt2_shapes
+    from oracle import adam as oadam
+    shapes = gpt2_shapes()
+    total = sum(int(np.prod(s)) for s in shapes)
+    params = _host_tensors(shapes, 1337, 0.02)
+    grads = _host_tensors(shapes, 2337, 1e-3)
+    ms = [np.zeros_like(p) for p in params]
+    vs = [np.zeros_like(p) for p in params]
+    wds = [0.1 if len(s) >= 2 else 0.0 for s in shapes]
+
+    def step(k):
+        for p, g, m, v, wd in zip(params, grads, ms, vs, wds):
+            oadam.adam_step(p, g, m, v, k, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+
+    steps, elapsed = _timed_steps(step, min_seconds, max_steps)
+    return _baseline_record(total, steps, elapsed, 28,
+                            f"NumPy oracle AdamW over the full GPT-2-124M list ({len(shapes)} tensors, {total} params)")
+
+
+def cpu_baselines_other(min_seconds=3.0):
+    """The other configs through the oracle on this host, one thread each:
+    C1 whole; C3 (unscale_ -> finite -> master step -> bf16 copy -> scaler
+    update, amp.py:169-234 over the fp32-master extension), C4 and C5 on a
+    prefix of about 15 M parameters of their lists (the step is per-element
+    work, so params/s carries over to the full list, stated as
+    extrapolated)."""
+    import numpy as np
+    from namitorch_amd.param_lists import gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes, total_params
+    from oracle import adam as oadam
+    from oracle import clip as oclip
+    from oracle import lowp
+    from oracle import scaler as oscaler
+    options = dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8)
+    out = {}
+
+    # C1: one flat 4,194,304-element fp32 tensor.
+    p, = _host_tensors([(4_194_304,)], 1337, 0.02)
+    g, = _host_tensors([(4_194_304,)], 2337, 1e-3)
+    m, v = np.zeros_like(p), np.zeros_like(p)
+    steps, elapsed = _timed_steps(lambda k: oadam.adam_step(p, g, m, v, k, weight_decay=0.1, **options), min_seconds, 200)
+    out["c1"] = _baseline_record(p.size, steps, elapsed, 28, "NumPy oracle AdamW, one flat fp32 tensor of 4,194,304")
+    del p, g, m, v
+
+    # C3 prefix: the first two GPT-2-124M layers, AMP: fp16 grads x 65536, fp32 master, bf16 model copy.
+    full = gpt2_shapes()
+    shapes = full[2:26]
+    masters = [lowp.round_bf16(x) for x in _host_tensors(shapes, 1337, 0.02)]
+    grads16 = [(x * np.float32(65536.0)).astype(np.float16) for x in _host_tensors(shapes, 2337, 1e-3)]
+    ms = [np.zeros_like(x) for x in masters]
+    vs = [np.zeros_like(x) for x in masters]
+    wds = [0.1 if len(s) >= 2 else 0.0 for s in shapes]
+    scaler = oscaler.Scaler()
+
+    def c3_step(k):
+        unscaled = [oscaler.unscale(x, scaler.scale, "float16") for x in grads16]
+        finite = oscaler.finite(unscaled) and oscaler.finite(unscaled)     # unscale_ and step both check
+        if finite:
+            for master, u, m_, v_, wd in zip(masters, unscaled, ms, vs, wds):
+                oadam.master_step(master, u, m_, v_, k, weight_decay=wd, **options)
+                lowp.round_bf16(master)                                      # the bf16 model copy
+        scaler.update(not finite)
+
+    steps, elapsed = _timed_steps(c3_step, min_seconds, 40)
+    out["c3"] = _baseline_record(total_params(shapes), steps, elapsed, 30,
+                                 f"NumPy oracle AMP step over layers 0-1 of the GPT-2-124M list "
+                                 f"({len(shapes)} tensors, {total_params(shapes)} params)",
+                                 extrapolated_to=total_params(full))
+    del masters, grads16, ms, vs
+
+    # C4 prefix: the attention tensors of GPT-1.3B layer 0, bf16 grads/m/v, clip 1.0.
+    full = gpt_1p3b_shapes()
+    shapes = full[2:8]
+    masters = [lowp.round_bf16(x) for x in _host_tensors(shapes, 1337, 0.02)]
+    grads = [lowp.round_bf16(x) for x in _host_tensors(shapes, 2337, 1e-3)]
+    ms = [np.zeros_like(x) for x in masters]
+    vs = [np.zeros_like(x) for x in masters]
+    wds = [0.1 if len(s) >= 2 else 0.0 for s in shapes]
+
+    def c4_step(k):
+        norm = oclip.total_norm(grads)
+        coefficient = oclip.clip_coefficient(1.0, norm)
+        clipped = [oclip.clip_apply(x, coefficient, "bfloat16") for x in grads] if coefficient < 1 else grads
+        for master, x, m_, v_, wd in zip(masters, clipped, ms, vs, wds):
+            oadam.master_step(master, x, m_, v_, k, weight_decay=wd, state_bf16=True, **options)
+            lowp.round_bf16(master)
+
+    steps, elapsed = _timed_steps(c4_step, min_seconds, 40)
+    out["c4"] = _baseline_record(total_params(shapes), steps, elapsed, 22,
+                                 f"NumPy oracle bf16 clip + master step over the attention tensors of GPT-1.3B "
+                                 f"layer 0 ({len(shapes)} tensors, {total_params(shapes)} params)",
+                                 extrapolated_to=total_params(full))
+    del masters, grads, ms, vs
+
+    # C5 prefix: the q projection of Llama-7B layer 0, AMP + clip.
+    full = llama7b_shapes()
+    shapes = full[2:3]
+    masters = [x for x in _host_tensors(shapes, 1337, 0.02)]
+    grads = [lowp.round_bf16(x * np.float32(65536.0)) for x in _host_tensors(shapes, 2337, 1e-3)]
+    ms = [np.zeros_like(x) for x in masters]
+    vs = [np.zeros_like(x) for x in masters]
+    scaler = oscaler.Scaler()
+
+    def c5_step(k):
+        unscaled = [oscaler.unscale(x, scaler.scale, "bfloat16") for x in grads]
+        finite = oscaler.finite(unscaled) and oscaler.finite(unscaled)
+        if finite:
+            norm = oclip.total_norm(unscaled)
+            coefficient = oclip.clip_coefficient(1.0, norm)
+            clipped = [oclip.clip_apply(x, coefficient, "bfloat16") for x in unscaled] if coefficient < 1 else unscaled
+            for master, x, m_, v_ in zip(masters, clipped, ms, vs):
+                oadam.master_step(master, x, m_, v_, k, weight_decay=0.1, **options)
+                lowp.round_bf16(master)
+        scaler.update(not finite)
+
+    steps, elapsed = _timed_steps(c5_step, min_seconds, 40)
+    out["c5"] = _baseline_record(total_params(shapes), steps, elapsed, 30,
+                                 f"NumPy oracle AMP + clip + master step over the q projection of Llama-7B "
+                                 f"layer 0 ({len(shapes)} tensor, {total_params(shapes)} params)",
+                                 extrapolated_to=total_params(full))
+    return out
 
 
 def pmc_traffic():
@@ -469,6 +621,28 @@ def pmc_traffic():
     except (OSError, ValueError):
         return None
     return None
+
+
+def _mixed_configs(nt):
+    """(result key, bench_mixed keyword arguments) of the mixed-precision configs."""
+    from namitorch_amd.param_lists import decay_mask, gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes, shard_shapes
+    return {
+        "c3": ("c3_gpt2_amp", dict(shapes=gpt2_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.float16,
+                                   state_dtype=None, amp=True, max_norm=None, bytes_per_param=30)),
+        "c4": ("c4_gpt1p3b_bf16_clip", dict(shapes=gpt_1p3b_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.bfloat16,
+                                            state_dtype=nt.bfloat16, amp=False, max_norm=1.0, bytes_per_param=22)),
+        "c5": ("c5_llama7b_amp_clip", dict(shapes=llama7b_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.bfloat16,
+                                           state_dtype=None, amp=True, max_norm=1.0, bytes_per_param=30)),
+        "c4s8": ("c4_shard8", dict(shapes=shard_shapes(gpt_1p3b_shapes(), 8), param_dtype=nt.bfloat16,
+                                   grad_dtype=nt.bfloat16, state_dtype=nt.bfloat16, amp=False, max_norm=1.0,
+                                   bytes_per_param=22, modes=("fused",), mask=decay_mask(gpt_1p3b_shapes()))),
+        "c5s8": ("c5_shard8", dict(shapes=shard_shapes(llama7b_shapes(), 8), param_dtype=nt.bfloat16,
+                                   grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
+                                   bytes_per_param=30, modes=("fused",), mask=decay_mask(llama7b_shapes()))),
+    }
+
+
+MIXED = ("c3", "c4", "c5", "c4s8", "c5s8")
 
 
 def main():
@@ -484,6 +658,14 @@ def main():
     log(f"device {torch.cuda.get_device_name(0)}")
     wanted = [c.strip() for c in args.configs.split(",") if c.strip()]
     extra = {}
+    if args.profile:
+        key, spec = _mixed_configs(nt)[args.profile]
+        spec = dict(spec, modes=("fused",))
+        shapes = spec.pop("shapes")
+        log(f"{args.profile} fused step only ({args.warmup} untimed, {args.steps} timed)")
+        print(json.dumps({key: bench_mixed(nt, torch, args.profile, shapes, steps=args.steps, warmup=args.warmup,
+                                           **spec)}), flush=True)
+        return
     log("C2 gpt2-124m fp32 multi-tensor AdamW")
     c2 = bench_c2(nt, torch, args.steps, args.warmup)
     log(f"C2: {c2['ms_per_step']:.3f} ms/step, kernel {c2['kernel_ms']:.3f} ms")
@@ -497,42 +679,26 @@ def main():
             c2["calibration_copy_bytes"] = {"read": source.numel() * 4, "write": target.numel() * 4, "launches": 3}
         print(json.dumps(c2))
         return
-    from namitorch_amd.param_lists import decay_mask, gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes, shard_shapes
+    from namitorch_amd.param_lists import gpt_1p3b_shapes
     if "c1" in wanted:
         log("C1 flat 4M fp32")
         extra["c1_flat4m_fp32"] = bench_c1(nt, torch, args.steps, args.warmup)
-    if "c3" in wanted:
-        log("C3 gpt2-124m AMP (bf16 model, fp32 master, fp16 grads x65536)")
-        extra["c3_gpt2_amp"] = bench_mixed(nt, torch, "c3", gpt2_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.float16,
-                                           state_dtype=None, amp=True, max_norm=None, bytes_per_param=30,
-                                           steps=args.steps, warmup=args.warmup)
-    if "c4" in wanted:
-        log("C4 gpt-1.3b bf16 params/m/v/grads, fp32 master, clip 1.0")
-        extra["c4_gpt1p3b_bf16_clip"] = bench_mixed(nt, torch, "c4", gpt_1p3b_shapes(), param_dtype=nt.bfloat16,
-                                                    grad_dtype=nt.bfloat16, state_dtype=nt.bfloat16, amp=False,
-                                                    max_norm=1.0, bytes_per_param=22,
-                                                    steps=max(5, args.steps // 2), warmup=args.warmup)
-    if "c5" in wanted:
-        log("C5 llama-7b fp32 master/m/v, bf16 grads/params, AMP + clip")
-        extra["c5_llama7b_amp_clip"] = bench_mixed(nt, torch, "c5", llama7b_shapes(), param_dtype=nt.bfloat16,
-                                                   grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
-                                                   bytes_per_param=30, steps=max(5, args.steps // 5),
-                                                   warmup=min(args.warmup, 3))
-    # One GPU's share of an 8-way sharded step (every tensor split into 8
-    # contiguous slices, ZeRO-1 style): the local pre-pass + AdamW pass that
-    # each rank would run between the collectives.
-    if "c4s8" in wanted:
-        log("C4/8 shard: gpt-1.3b list, 1/8 of every tensor, bf16 + clip")
-        extra["c4_shard8"] = bench_mixed(nt, torch, "c4s8", shard_shapes(gpt_1p3b_shapes(), 8), param_dtype=nt.bfloat16,
-                                         grad_dtype=nt.bfloat16, state_dtype=nt.bfloat16, amp=False, max_norm=1.0,
-                                         bytes_per_param=22, steps=args.steps, warmup=args.warmup, modes=("fused",),
-                                         mask=decay_mask(gpt_1p3b_shapes()))
-    if "c5s8" in wanted:
-        log("C5/8 shard: llama-7b list, 1/8 of every tensor, AMP + clip")
-        extra["c5_shard8"] = bench_mixed(nt, torch, "c5s8", shard_shapes(llama7b_shapes(), 8), param_dtype=nt.bfloat16,
-                                         grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
-                                         bytes_per_param=30, steps=max(5, args.steps // 2), warmup=args.warmup,
-                                         modes=("fused",), mask=decay_mask(llama7b_shapes()))
+    # C3 GPT-2 AMP (bf16 model, fp32 master, fp16 grads x65536); C4 GPT-1.3B
+    # bf16 params/m/v/grads, fp32 master, clip 1.0; C5 Llama-7B fp32
+    # master/m/v, bf16 grads/params, AMP + clip; and one GPU's share of an
+    # 8-way sharded C4 and C5 step (every tensor split into 8 contiguous
+    # slices, ZeRO-1 style: the local pre-pass + AdamW pass each rank runs
+    # between the collectives).
+    counts = {"c3": args.steps, "c4": max(5, args.steps // 2), "c5": max(5, args.steps // 5), "c4s8": args.steps,
+              "c5s8": max(5, args.steps // 2)}
+    for name, (key, spec) in _mixed_configs(nt).items():
+        if name not in wanted:
+            continue
+        spec = dict(spec)
+        shapes = spec.pop("shapes")
+        log(f"{name}: {key}")
+        extra[key] = bench_mixed(nt, torch, name, shapes, steps=counts[name],
+                                 warmup=min(args.warmup, 3) if name == "c5" else args.warmup, **spec)
     if "chunks" in wanted:
         log("AdamW pass task size: 4096 against 2048 elements, same buffers")
         extra["pass_chunks"] = bench_chunks(nt, torch)
@@ -548,6 +714,10 @@ def main():
     if not args.no_cpu:
         log("CPU baseline (NumPy oracle)")
         baseline = cpu_baseline()
+        log(f"CPU C2: {baseline['value']:.3g} params/s")
+        extra["cpu_baselines"] = cpu_baselines_other()
+        for name, record in extra["cpu_baselines"].items():
+            log(f"CPU {name}: {record['value']:.3g} params/s")
     achieved = 28 * c2["params"] / (c2["kernel_ms"] / 1e3) / 1e9
     line = {
         "metric": METRIC,
@@ -567,8 +737,12 @@ def main():
                    "params": c2["params"], "tensors": c2["tensors"], "bytes_per_param": 28,
                    "step_GBps": 28 * c2["params_per_s"] / 1e9,
                    "step_pct_hbm_peak": 100 * 28 * c2["params_per_s"] / 1e9 / HBM_PEAK_GBPS},
+        "median_ms_per_step": c2["median_ms_per_step"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": pmc_traffic(),
+                     "traffic_source": f"FETCH_SIZE/WRITE_SIZE of the same kernel from the committed rocprofv3 PMC "
+                                       f"summary {PROFILE_PMC.relative_to(ROOT)} (calibrated by a 1 GiB copy), "
+                                       f"not counted in this run",
                      "kernel": "nt::adamw_mt_kernel<TF32,TF32,TF32,TNone,RoundF32,false,64,1>",
                      "kernel_ms": c2["kernel_ms"],
                      "mix_ceiling_GBps": ceilings["r4w3_inplace"]["GBps"] if ceilings else None,
