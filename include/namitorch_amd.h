@@ -395,6 +395,34 @@ int32_t nt_stream_probe(const void *const *reads, int32_t nreads, int32_t nreads
                         void *const *writes, int32_t nwrites, int32_t nwrites16,
                         uint64_t count, void *stream);
 
+/*
+ * Launch-shape probe, no counterpart in the reference: a measurement aid.
+ * Runs one of the AdamW pass's in-place read/write mixes with AdamW-like
+ * arithmetic under launch shape `shape`, so a benchmark can compare the
+ * shapes the pass could use.  Mix 0 (the float32 pass, 28 B/element):
+ * streams[0..3] = p, g, m, v (fp32); p, m, v are rewritten in place.  Mix 1
+ * (the GPT-1.3B pass, 20 B/element): streams[0] = fp32 master, [1..3] =
+ * bfloat16 g, m, v, [4] = bfloat16 copy; master, m, v rewritten in place, the
+ * copy written.  `count` elements per stream, a positive multiple of 8192;
+ * streams 16-byte aligned.  `per_cu` (1..64) sizes persistent grids in
+ * workgroups per compute unit.
+ */
+#define NT_SHAPE_WAVE 0               /* 64 lanes x 1 group: the pass's shape */
+#define NT_SHAPE_WAVE_XCD 1           /* the same, tile order contiguous per XCD */
+#define NT_SHAPE_WAVE_U2 2            /* 64 lanes x 2 groups per lane */
+#define NT_SHAPE_B128 3               /* 128 lanes x 1 group */
+#define NT_SHAPE_B256 4               /* 256 lanes x 1 group */
+#define NT_SHAPE_B256_U2 5            /* 256 lanes x 2 groups */
+#define NT_SHAPE_B512 6               /* 512 lanes x 1 group */
+#define NT_SHAPE_PERSISTENT 7         /* 64 lanes, per_cu workgroups per CU walk the tiles */
+#define NT_SHAPE_PERSISTENT_PIPE 8    /* the same, next tile loaded before this tile is stored */
+#define NT_SHAPE_PERSISTENT_B256_PIPE 9
+#define NT_SHAPE_PERSISTENT_U2_PIPE 10
+#define NT_SHAPE_DIRECT_TO_LDS 11     /* mix 0 only: global_load_lds_dwordx4, nontemporal */
+#define NT_SHAPE_TEMPORAL 12          /* NT_SHAPE_WAVE with ordinary (temporal) loads and stores */
+int32_t nt_stream_probe_shape(int32_t mix, int32_t shape, void *const *streams, uint64_t count,
+                              int32_t per_cu, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

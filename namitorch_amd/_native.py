@@ -147,6 +147,7 @@ SIGNATURES = {
                                             c_double, c_double, c_int32, c_double, c_double, c_int32, c_void_p]),
     "nt_stream_probe": (c_int32, [ctypes.POINTER(c_void_p), c_int32, c_int32, ctypes.POINTER(c_void_p), c_int32, c_int32,
                                   c_uint64, c_void_p]),
+    "nt_stream_probe_shape": (c_int32, [c_int32, c_int32, ctypes.POINTER(c_void_p), c_uint64, c_int32, c_void_p]),
 }
 
 _lock = threading.Lock()
