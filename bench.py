@@ -96,6 +96,14 @@ def decay_groups(params, mask=None):
             {"params": [p for p, m in zip(params, mask) if not m], "weight_decay": 0.0}]
 
 
+def release(nt, torch):
+    """Return cached device memory of both allocators (PyTorch's, which holds
+    the synthetic inputs, and the library's, which holds optimizer state)."""
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    nt.runtime.empty_cache(0)
+
+
 def event_pair(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -135,7 +143,7 @@ def bench_c2(nt, torch, steps, warmup):
     result = dict(params=n, tensors=len(shapes), ms_per_step=ms_per_step, params_per_s=n / (ms_per_step / 1e3),
                   median_ms_per_step=median_ms, kernel_ms=kernel_ms, bytes_per_param=28)
     del optimizer, params
-    torch.cuda.empty_cache()
+    release(nt, torch)
     return result
 
 
@@ -191,7 +199,7 @@ def bench_c1(nt, torch, steps, warmup):
         total += a.elapsed_time(b)
     flushed_ms = total / steps
     del scratch, optimizer, param
-    torch.cuda.empty_cache()
+    release(nt, torch)
     return dict(params=n, bytes_per_param=28, hot_ms=hot_ms, flushed_ms=flushed_ms,
                 hot_GBps=28 * n / hot_ms / 1e6, flushed_GBps=28 * n / flushed_ms / 1e6)
 
@@ -261,9 +269,9 @@ def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype
         del optimizer, scaler
         for p, g in zip(params, grads):
             p.grad = g
-        torch.cuda.empty_cache()
+        release(nt, torch)
     del params, grads
-    torch.cuda.empty_cache()
+    release(nt, torch)
     return result
 
 
@@ -297,7 +305,7 @@ def bench_edges(nt, torch, shapes, steps, warmup):
                             pct_hbm_peak=100 * bytes_per_param * n / ms / 1e6 / HBM_PEAK_GBPS)
         log(f"edges {name}: {ms:.3f} ms")
     del params, incoming, optimizer
-    torch.cuda.empty_cache()
+    release(nt, torch)
     return result
 
 
@@ -362,7 +370,7 @@ def bench_ceilings(nt, torch, steps, warmup):
                                 bytes_per_element=dict(read=4 * r32 + 2 * r16, write=4 * w32 + 2 * w16))
             log(f"probe {name}: {gbps:.0f} GB/s")
         del wide, narrow
-        torch.cuda.empty_cache()
+        release(nt, torch)
     return result
 
 
@@ -417,7 +425,7 @@ def bench_shape_sweep(nt, torch, launches=8, warmup=2, rounds=5):
             log(f"shape sweep mix{mix} {size_name}: pass shape {rows['wave (the pass)']['GBps']:.0f} GB/s, "
                 f"fastest {best} {rows[best]['GBps']:.0f} GB/s")
             del buffers
-            torch.cuda.empty_cache()
+            release(nt, torch)
     return result
 
 
@@ -491,7 +499,7 @@ def bench_chunks(nt, torch, launches=20, reps=4):
         for handle in plans.values():
             _native.call("nt_plan_destroy", handle)
         del keep, rows, table
-        torch.cuda.empty_cache()
+        release(nt, torch)
     return result
 
 
@@ -710,6 +718,9 @@ def main():
     import namitorch_amd as nt
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a HIP device")
+    # The synthetic inputs and the timing events live on PyTorch's current
+    # stream: make the library launch there too.
+    nt.runtime.set_stream_provider(lambda device: torch.cuda.current_stream(device).cuda_stream)
     log(f"device {torch.cuda.get_device_name(0)}")
     wanted = [c.strip() for c in args.configs.split(",") if c.strip()]
     extra = {}

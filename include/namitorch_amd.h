@@ -164,12 +164,77 @@ int32_t nt_device_count(int32_t *count);
 /* Name of the gfx target of `device` (e.g. "gfx950") into buf[len]. */
 int32_t nt_device_arch(int32_t device, char *buf, int32_t len);
 
+/* The calling thread's current device: entry points that take only
+ * pointers and a stream queue on the null stream of this device when
+ * `stream` is NULL (replaces the device scope `cupy.cuda.Device(...)` that
+ * the reference's CUDA calls run in, backends/_cuda_execution.py:132). */
+int32_t nt_set_device(int32_t device);
+int32_t nt_get_device(int32_t *device);
+
 /* Wait for all work queued on `stream`. */
 int32_t nt_stream_synchronize(void *stream);
 
 /* Copy `bytes` between host and device on `stream` and wait for it. */
 int32_t nt_memcpy_d2h(void *dst, const void *src, uint64_t bytes, void *stream);
 int32_t nt_memcpy_h2d(void *dst, const void *src, uint64_t bytes, void *stream);
+
+/* ---- device memory, streams, events (nt_memory.hip) ---------------------
+ * The services the reference takes from CuPy (its memory pool and OOM
+ * report, backends/_cuda_memory.py:24-94; streams and event-ordered
+ * lifetimes, backends/_cuda_execution.py:21-137; transfers,
+ * backends/cuda/__init__.py:87-153), owned by the library so a host layer
+ * needs no other GPU framework.
+ *
+ * nt_malloc: `bytes` of device memory on `device` for use on `stream`, from
+ * a caching pool: a freed block is reused only by later allocations on the
+ * stream it was allocated on (stream order makes that safe); a block also
+ * used on other streams (nt_record_stream) is reused once an event recorded
+ * on each of them at nt_free has completed.  An out-of-memory hipMalloc
+ * releases the cached blocks and retries; the error names the bytes in use
+ * and reserved.  nt_empty_cache releases every cached block (waits for the
+ * device). */
+#define NT_COPY_H2D 1
+#define NT_COPY_D2H 2
+#define NT_COPY_D2D 3
+int32_t nt_malloc(int32_t device, uint64_t bytes, void *stream, void **out);
+int32_t nt_free(void *ptr);
+int32_t nt_record_stream(void *ptr, void *stream);
+int32_t nt_memory_stats(int32_t device, uint64_t *in_use, uint64_t *reserved);
+int32_t nt_empty_cache(int32_t device);
+/* Page-locked host memory (hipHostMalloc). */
+int32_t nt_host_alloc(uint64_t bytes, void **out);
+int32_t nt_host_free(void *ptr);
+/* Streams are created at the default priority and do not synchronize with
+ * the null stream. */
+int32_t nt_stream_create(int32_t device, void **out);
+int32_t nt_stream_destroy(void *stream);
+int32_t nt_stream_wait_event(void *stream, void *event);
+/* Events (`timing` != 0 for nt_event_elapsed); nt_event_query sets *done to
+ * 1 once the recorded work has completed, else 0. */
+int32_t nt_event_create(int32_t timing, void **out);
+int32_t nt_event_destroy(void *event);
+int32_t nt_event_record(void *event, void *stream);
+int32_t nt_event_synchronize(void *event);
+int32_t nt_event_query(void *event, int32_t *done);
+int32_t nt_event_elapsed(void *start, void *stop, float *milliseconds);
+/* Asynchronous copy of `bytes` (NT_COPY_*) ordered on `stream`. */
+int32_t nt_memcpy_async(void *dst, const void *src, uint64_t bytes, int32_t kind, void *stream);
+/* Write `count` items of `itemsize` bytes (1, 2, 4, 8), each the low bytes
+ * of `pattern`: Tensor.fill_/zero_ and zero-initialized state
+ * (optim/_common.py:50-54) without hipMemset, so it can be captured. */
+int32_t nt_fill(void *ptr, uint64_t count, int32_t itemsize, uint64_t pattern, void *stream);
+/* out[i] = in[i] converted between NT_F32/NT_F16/NT_BF16/NT_F64 with one
+ * rounding to nearest even, as NumPy's astype (Tensor.to(dtype),
+ * tensor.py:1252-1287 on device arrays). */
+int32_t nt_cast(const void *in, int32_t in_dtype, void *out, int32_t out_dtype,
+                uint64_t count, void *stream);
+/* Device ordinal of a device pointer (NT_ERR_VALUE for host memory):
+ * backend.adamw.supports's "array on this device" check
+ * (backends/cuda/adamw.py:33-46) for arrays handed over by address. */
+int32_t nt_pointer_device(const void *ptr, int32_t *device);
+/* *capturing = 1 while `stream` is being captured into a HIP graph: the
+ * guard of backends/_graph_capture.py:12-14. */
+int32_t nt_stream_capturing(void *stream, int32_t *capturing);
 
 /* ---- per-tensor AdamW: the reference kernel's own ABI ------------------ */
 

@@ -7,6 +7,7 @@ fallback: when the library is missing every device operation raises
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import threading
 from pathlib import Path
@@ -123,6 +124,8 @@ SIGNATURES = {
     "nt_abi_version": (c_int32, []),
     "nt_device_count": (c_int32, [ctypes.POINTER(c_int32)]),
     "nt_device_arch": (c_int32, [c_int32, ctypes.c_char_p, c_int32]),
+    "nt_set_device": (c_int32, [c_int32]),
+    "nt_get_device": (c_int32, [ctypes.POINTER(c_int32)]),
     "nt_stream_synchronize": (c_int32, [c_void_p]),
     "nt_memcpy_d2h": (c_int32, [c_void_p, c_void_p, c_uint64, c_void_p]),
     "nt_memcpy_h2d": (c_int32, [c_void_p, c_void_p, c_uint64, c_void_p]),
@@ -148,7 +151,49 @@ SIGNATURES = {
     "nt_stream_probe": (c_int32, [ctypes.POINTER(c_void_p), c_int32, c_int32, ctypes.POINTER(c_void_p), c_int32, c_int32,
                                   c_uint64, c_void_p]),
     "nt_stream_probe_shape": (c_int32, [c_int32, c_int32, ctypes.POINTER(c_void_p), c_uint64, c_int32, c_void_p]),
+    "nt_malloc": (c_int32, [c_int32, c_uint64, c_void_p, ctypes.POINTER(c_void_p)]),
+    "nt_free": (c_int32, [c_void_p]),
+    "nt_record_stream": (c_int32, [c_void_p, c_void_p]),
+    "nt_memory_stats": (c_int32, [c_int32, ctypes.POINTER(c_uint64), ctypes.POINTER(c_uint64)]),
+    "nt_empty_cache": (c_int32, [c_int32]),
+    "nt_host_alloc": (c_int32, [c_uint64, ctypes.POINTER(c_void_p)]),
+    "nt_host_free": (c_int32, [c_void_p]),
+    "nt_stream_create": (c_int32, [c_int32, ctypes.POINTER(c_void_p)]),
+    "nt_stream_destroy": (c_int32, [c_void_p]),
+    "nt_stream_wait_event": (c_int32, [c_void_p, c_void_p]),
+    "nt_event_create": (c_int32, [c_int32, ctypes.POINTER(c_void_p)]),
+    "nt_event_destroy": (c_int32, [c_void_p]),
+    "nt_event_record": (c_int32, [c_void_p, c_void_p]),
+    "nt_event_synchronize": (c_int32, [c_void_p]),
+    "nt_event_query": (c_int32, [c_void_p, ctypes.POINTER(c_int32)]),
+    "nt_event_elapsed": (c_int32, [c_void_p, c_void_p, ctypes.POINTER(c_float)]),
+    "nt_memcpy_async": (c_int32, [c_void_p, c_void_p, c_uint64, c_int32, c_void_p]),
+    "nt_fill": (c_int32, [c_void_p, c_uint64, c_int32, c_uint64, c_void_p]),
+    "nt_cast": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_uint64, c_void_p]),
+    "nt_pointer_device": (c_int32, [c_void_p, ctypes.POINTER(c_int32)]),
+    "nt_stream_capturing": (c_int32, [c_void_p, ctypes.POINTER(c_int32)]),
 }
+
+NT_COPY_H2D = 1
+NT_COPY_D2H = 2
+NT_COPY_D2D = 3
+
+# Set at interpreter exit: objects released after that point leave their
+# device memory, streams and events to the process teardown instead of
+# calling into a HIP runtime that may already be gone.
+_exiting = False
+
+
+def _mark_exit() -> None:
+    global _exiting
+    _exiting = True
+
+
+atexit.register(_mark_exit)
+
+
+def shutting_down() -> bool:
+    return _exiting
 
 _lock = threading.Lock()
 _lib = None

@@ -25,7 +25,7 @@ from numbers import Real
 
 import numpy as np
 
-from . import _native
+from . import _native, runtime
 from .backends import get_backend
 from .backends._graph_capture import reject_during_capture
 from .dtype import float32, float64, promote_with_scalar
@@ -53,7 +53,6 @@ class DeviceStep:
     block, and the host-side bookkeeping to undo if the step was skipped."""
 
     def __init__(self, backend, block, unscale: bool, honor_skip: bool, clip_bumps: list):
-        import torch
         self.backend = backend
         self.block = block
         self.unscale = unscale
@@ -61,8 +60,8 @@ class DeviceStep:
         self.records: list = []
         self.optimizers: set = set()
         self.clip_bumps = clip_bumps          # (gradient, version after the optimistic clip bump)
-        self.snapshot = torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, pin_memory=True)
-        self.event = torch.cuda.Event()
+        self.snapshot = runtime.pinned(ctypes.sizeof(_native.AmpCtrl))
+        self.event = runtime.Event()
         self._ctrl = None
         self._reconciled = False
         self.scheduler = None                 # advanced at reconciliation iff the step updated
@@ -76,11 +75,9 @@ class DeviceStep:
         work completes."""
         current = self.backend.stream()
         if self.stream is not None and current != self.stream:
-            import torch
             with self.backend.context():
-                stream = torch.cuda.current_stream(self.backend.device.index)
-                stream.wait_event(self.ready)
-                self.block.record_stream(stream)
+                _native.call("nt_stream_wait_event", current, self.ready.handle)
+                self.block.record_stream(current)
         return self.block
 
     def capture(self) -> None:
@@ -88,24 +85,21 @@ class DeviceStep:
         copy runs on the backend's side stream once the work queued so far
         on the current stream is done, so the AdamW pass queued next does not
         wait behind it.  Nothing writes the block after the finalize kernel."""
-        import torch
         with self.backend.context():
-            ready = torch.cuda.Event()
-            ready.record()
-            # Work on another stream that reads this block waits on `ready`.
-            self.ready = ready
             self.stream = self.backend.stream()
+            # Work on another stream that reads this block waits on `ready`.
+            self.ready = runtime.Event().record(self.stream)
             side = self.backend.side_stream()
-            side.wait_event(ready)
-            with torch.cuda.stream(side):
-                self.snapshot.copy_(self.block, non_blocking=True)
-                self.event.record(side)
-            self.block.record_stream(side)        # not reused before the copy has read it
+            side.wait_event(self.ready)
+            _native.call("nt_memcpy_async", self.snapshot.ctypes.data, self.block.data_ptr(), self.snapshot.nbytes,
+                         _native.NT_COPY_D2H, side.handle)
+            self.event.record(side.handle)
+            self.block.record_stream(side.handle)    # not reused before the copy has read it
 
     def ctrl(self) -> _native.AmpCtrl:
         if self._ctrl is None:
             self.event.synchronize()
-            self._ctrl = _native.AmpCtrl.from_buffer_copy(self.snapshot.numpy().tobytes())
+            self._ctrl = _native.AmpCtrl.from_buffer_copy(self.snapshot.tobytes())
         return self._ctrl
 
     def reconcile(self) -> None:

@@ -2,10 +2,14 @@
 
 Protocol of the reference's CUDA backend object
 (namitorch/backends/cuda/__init__.py:23-225) as far as the optimizer step
-uses it: ``device``, ``context``, ``result``, ``item``, ``writable`` and the
-optional kernel attribute ``adamw``.  Storage arrays are torch tensors on
-the device; every operation launches the gfx950 kernels of
-``libnamitorch_amd.so`` on torch's current stream for the device.
+uses it: ``device``, ``array_type``, ``array``, ``to_numpy``, ``item``,
+``context``, ``result``, ``ready_for_host``, ``writable``, ``readonly`` and
+the optional kernel attribute ``adamw``.  Backend arrays are
+:class:`namitorch_amd.array.DeviceArray` (memory of the library's caching
+allocator, or another framework's device array wrapped without a copy);
+every operation launches the gfx950 kernels of ``libnamitorch_amd.so`` on
+the calling thread's current stream of the device
+(``namitorch_amd.runtime.current_stream``).
 
 Multi-tensor plans (descriptor table + workgroup task map, see
 ``include/namitorch_amd.h``) are cached per backend, keyed by the raw
@@ -21,13 +25,13 @@ import math
 import threading
 import weakref
 from collections import OrderedDict
-from contextlib import contextmanager
 
 import numpy as np
-import torch
 
-from .. import _native
+from .. import _native, runtime
+from ..array import DeviceArray
 from ..device import Device
+from ..dtype import float32, int32, uint8
 
 PLAN_CACHE_SIZE = 16
 _backends_alive: "weakref.WeakSet[HIPBackend]" = weakref.WeakSet()
@@ -73,9 +77,9 @@ class Plan:
 class AdamWHIPKernel:
     """The reference's per-tensor fused AdamW hook (backends/cuda/adamw.py:32-73).
 
-    Arguments are raw storage arrays (torch tensors on this device), exactly
-    as the reference passes ``._data``; the caller owns version counters and
-    ``state['step']``.
+    Arguments are raw storage arrays (DeviceArrays, or device arrays of
+    another framework, on this device), exactly as the reference passes
+    ``._data``; the caller owns version counters and ``state['step']``.
     """
 
     def __init__(self, backend: "HIPBackend"):
@@ -85,14 +89,20 @@ class AdamWHIPKernel:
         arrays = (parameter, gradient, first, second)
         if parameter is None or gradient is None:
             return False
-        present = tuple(array for array in arrays if array is not None)
-        index = self._backend.device.index
+        present = []
+        for array in arrays:
+            if array is None:
+                continue
+            try:
+                array = DeviceArray.wrap(array)
+            except (TypeError, ValueError):
+                return False
+            present.append(array)
+        shape = present[0].shape
         for array in present:
-            if not isinstance(array, torch.Tensor):
+            if array.device != self._backend.device or array.dtype is not float32:
                 return False
-            if array.device.type != "cuda" or array.device.index != index or array.dtype != torch.float32:
-                return False
-            if not array.is_contiguous() or array.data_ptr() % 4 or tuple(array.shape) != tuple(parameter.shape):
+            if array.data_ptr() % 4 or array.shape != shape:
                 return False
         ranges = [(array.data_ptr(), array.data_ptr() + array.numel() * 4) for array in present if array.numel()]
         return not any(
@@ -110,6 +120,7 @@ class AdamWHIPKernel:
             raise ValueError("Fused AdamW eps and bias corrections must be positive.")
         if type(maximize) is not bool or type(update_parameter) is not bool:
             raise TypeError("Fused AdamW flags must be Python bools.")
+        parameter, gradient, first, second = (DeviceArray.wrap(array) for array in (parameter, gradient, first, second))
         count = parameter.numel()
         if count == 0:
             return False
@@ -124,6 +135,8 @@ class AdamWHIPKernel:
 
 
 class HIPBackend:
+    array_type = DeviceArray
+
     def __init__(self, device: Device):
         lib = _native.load()
         count = ctypes.c_int32()
@@ -142,34 +155,64 @@ class HIPBackend:
         return f"HIPBackend({self.device})"
 
     # ---- reference protocol --------------------------------------------------------------
-    @contextmanager
     def context(self, *operands):
-        with torch.cuda.device(self.device.index):
-            yield
+        """Make this backend's device the calling thread's current device."""
+        return runtime.device_scope(self.device.index)
 
     def result(self, value):
         return value
 
+    def ready_for_host(self, array):
+        return array
+
+    def array(self, value, dtype=None, copy=True, *, non_blocking=False):
+        """`value` (host data, a DeviceArray or another framework's device
+        array) as a DeviceArray of this device, converted to `dtype`."""
+        from ..tensor import _host_array, _resolve_dtype, _values
+        kind = _resolve_dtype(value, dtype)
+        if isinstance(value, DeviceArray) or (not isinstance(value, np.ndarray) and _is_device(value)):
+            source = DeviceArray.wrap(value)
+            if source.device == self.device and (source.dtype is kind or (source.dtype._floating and kind._floating)):
+                if not copy and source.dtype is kind:
+                    return source
+                with self.context():
+                    return DeviceArray.empty(source.shape, kind, self.device).copy_from(source)
+            value = _values(source.download(), source.dtype)
+        host = _host_array(value, kind)
+        with self.context():
+            return DeviceArray.empty(host.shape, kind, self.device).upload(host)
+
     def item(self, array):
-        return array.item()
+        return self.to_numpy(array).reshape(()).item()
+
+    def to_numpy(self, array):
+        """Host copy of the values (bfloat16 widened exactly to float32)."""
+        from ..tensor import _values
+        array = DeviceArray.wrap(array)
+        with self.context():
+            return _values(array.download(), array.dtype)
 
     def writable(self, array):
         return True
 
+    def readonly(self, array):
+        return array
+
     # ---- streams ---------------------------------------------------------------------------
     def stream(self) -> int:
-        """Handle of torch's current stream on this device (a hipStream_t)."""
-        return torch.cuda.current_stream(self.device.index).cuda_stream
+        """Handle of the calling thread's current stream on this device (a hipStream_t)."""
+        return runtime.current_stream(self.device.index)
 
     def synchronize(self) -> None:
-        _native.call("nt_stream_synchronize", self.stream())
+        with self.context():
+            _native.call("nt_stream_synchronize", self.stream())
 
-    def side_stream(self) -> torch.cuda.Stream:
+    def side_stream(self) -> runtime.Stream:
         """A stream of this device (default priority) for small copies that
         work queued on the caller's stream should not wait behind."""
         with self._lock:
             if self._side_stream is None:
-                self._side_stream = torch.cuda.Stream(device=self.device.torch)
+                self._side_stream = runtime.Stream(self.device.index)
             return self._side_stream
 
     # ---- plans -----------------------------------------------------------------------------
@@ -271,31 +314,31 @@ class HIPBackend:
             _native.call("nt_grad_apply", plan.handle, ctypes.byref(xform), self.stream())
 
     # ---- control blocks ----------------------------------------------------------------------
-    def new_ctrl(self, scale: float = 1.0, growth_tracker: int = 0) -> torch.Tensor:
-        block = torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, device=self.device.torch)
+    def new_ctrl(self, scale: float = 1.0, growth_tracker: int = 0) -> DeviceArray:
+        block = self.empty_ctrl()
         self.reset_ctrl(block, scale, growth_tracker)
         return block
 
-    def reset_ctrl(self, block: torch.Tensor, scale: float, growth_tracker: int = 0) -> None:
+    def reset_ctrl(self, block: DeviceArray, scale: float, growth_tracker: int = 0) -> None:
         with self.context():
             _native.call("nt_ctrl_reset", block.data_ptr(), scale, growth_tracker, self.stream())
 
-    def empty_ctrl(self) -> torch.Tensor:
+    def empty_ctrl(self) -> DeviceArray:
         """Device memory for a control block that a finalize will write whole."""
-        return torch.empty(ctypes.sizeof(_native.AmpCtrl), dtype=torch.uint8, device=self.device.torch)
+        with self.context():
+            return DeviceArray.empty((ctypes.sizeof(_native.AmpCtrl),), uint8, self.device)
 
-    def neutral_ctrl(self) -> torch.Tensor:
+    def neutral_ctrl(self) -> DeviceArray:
         """A block with scale 1 and no history, kept per backend: the carry
         source of steps without a GradScaler.  Nothing writes it after set-up."""
         with self._lock:
             if self._neutral_ctrl is None:
                 block = self.new_ctrl()
-                with self.context():
-                    torch.cuda.current_stream(self.device.index).synchronize()   # readable from any stream
+                self.synchronize()   # readable from any stream
                 self._neutral_ctrl = block
             return self._neutral_ctrl
 
-    def read_ctrl(self, block: torch.Tensor) -> _native.AmpCtrl:
+    def read_ctrl(self, block: DeviceArray) -> _native.AmpCtrl:
         out = _native.AmpCtrl()
         with self.context():
             _native.call("nt_memcpy_d2h", ctypes.addressof(out), block.data_ptr(), ctypes.sizeof(out), self.stream())
@@ -335,7 +378,7 @@ class HIPBackend:
             plan = self.grad_plan(group, dtype)
             self.grad_apply(plan, make_xform(transform))
 
-    def scalar_arithmetic(self, tensor, operand: float, op: int, dtype, ctrl: torch.Tensor | None = None):
+    def scalar_arithmetic(self, tensor, operand: float, op: int, dtype, ctrl: DeviceArray | None = None):
         """``tensor * operand`` (NT_OP_MUL) or ``tensor / operand`` (NT_OP_DIV)
         computed in `dtype`, a new Tensor of that dtype; `operand` is already
         a value of `dtype`.  With `ctrl` the operand is the loss scale held in
@@ -344,18 +387,23 @@ class HIPBackend:
         if tensor.dtype.code == _native.NT_DTYPE_NONE or dtype.code == _native.NT_DTYPE_NONE:
             raise TypeError("Only floating Tensors support scalar arithmetic on the device.")
         source = tensor._data
-        out = torch.empty(tuple(source.shape), dtype=dtype.torch_dtype, device=self.device.torch)
         with self.context():
+            out = DeviceArray.empty(source.shape, dtype, self.device)
             _native.call("nt_tensor_scalar", source.data_ptr(), tensor.dtype.code, out.data_ptr(), dtype.code,
                          float(operand), int(op), None if ctrl is None else ctrl.data_ptr(), tensor.size,
                          self.stream())
         return Tensor._from_storage(out, tensor.requires_grad)
 
-    def any_negative(self, array: torch.Tensor, code: int) -> bool:
-        flag = torch.empty(1, dtype=torch.int32, device=self.device.torch)
+    def any_negative(self, array: DeviceArray, code: int) -> bool:
         with self.context():
+            flag = DeviceArray.empty((1,), int32, self.device)
             _native.call("nt_any_negative", array.data_ptr(), code, array.numel(), flag.data_ptr(), self.stream())
-        return bool(flag.item())
+            return bool(flag.download()[0])
+
+
+def _is_device(value) -> bool:
+    from ..array import is_device_array
+    return is_device_array(value)
 
 
 def make_xform(transform, ctrl_ptr: int | None = None, honor_skip: bool = False) -> _native.GradXform:

@@ -105,6 +105,21 @@ int32_t nt_device_arch(int32_t device, char *buf, int32_t len) {
     return NT_OK;
 }
 
+int32_t nt_set_device(int32_t device) {
+    clear_error();
+    NT_HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    return NT_OK;
+}
+
+int32_t nt_get_device(int32_t *device) {
+    clear_error();
+    if (device == nullptr) return fail(NT_ERR_VALUE, "device output pointer is NULL");
+    int d = 0;
+    NT_HIP_TRY(hipGetDevice(&d), "hipGetDevice");
+    *device = d;
+    return NT_OK;
+}
+
 int32_t nt_stream_synchronize(void *stream) {
     clear_error();
     NT_HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");

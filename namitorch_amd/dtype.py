@@ -4,8 +4,9 @@ Mirrors ``namitorch/dtype.py:16-25`` (float16/32/64, int8/16/32/64, uint8,
 bool) and adds ``bfloat16``, which the reference does not have: it is needed
 for the low-precision model copies, moments and gradients of mixed-precision
 training.  Each dtype knows its NumPy dtype (bfloat16 has none; its host
-form is float32 values or uint16 bit patterns), its torch storage dtype and
-its code in the C ABI.
+form is float32 values or uint16 bit patterns) and its code in the C ABI.
+The package does not need PyTorch; ``torch_dtype`` and the acceptance of
+``torch.dtype`` values are for callers that hand in PyTorch arrays.
 """
 
 from __future__ import annotations
@@ -13,7 +14,6 @@ from __future__ import annotations
 from enum import Enum
 
 import numpy as np
-import torch
 
 from . import _native
 
@@ -65,8 +65,9 @@ class DType(Enum):
         return np.dtype(self.value)
 
     @property
-    def torch_dtype(self) -> torch.dtype:
-        return _TORCH[self]
+    def torch_dtype(self):
+        """The matching ``torch.dtype`` (imports PyTorch)."""
+        return _torch_table()[0][self]
 
     @property
     def code(self) -> int:
@@ -104,11 +105,22 @@ uint8 = DType.uint8
 bool_ = DType.bool
 
 _ITEMSIZE = {float16: 2, float32: 4, float64: 8, bfloat16: 2, int8: 1, int16: 2, int32: 4, int64: 8, uint8: 1, bool_: 1}
-_TORCH = {
-    float16: torch.float16, float32: torch.float32, float64: torch.float64, bfloat16: torch.bfloat16,
-    int8: torch.int8, int16: torch.int16, int32: torch.int32, int64: torch.int64, uint8: torch.uint8, bool_: torch.bool,
-}
-_FROM_TORCH = {value: key for key, value in _TORCH.items()}
+_TORCH_TABLE: list = []
+
+
+def _torch_table():
+    """(DType -> torch.dtype, torch.dtype -> DType), built on first use."""
+    if not _TORCH_TABLE:
+        import torch
+        forward = {member: getattr(torch, "bool" if member is bool_ else member.value) for member in DType}
+        _TORCH_TABLE.extend((forward, {value: key for key, value in forward.items()}))
+    return _TORCH_TABLE
+
+
+def _is_torch_dtype(value: object) -> bool:
+    return type(value).__module__ == "torch" and type(value).__name__ == "dtype"
+
+
 _CODES = {float32: _native.NT_F32, float16: _native.NT_F16, bfloat16: _native.NT_BF16, float64: _native.NT_F64}
 for _member in DType:
     # Plain attributes (not enum lookups) because the step loop reads them per tensor.
@@ -120,10 +132,8 @@ del _member
 def normalize_dtype(value: object) -> DType:
     if isinstance(value, DType):
         return value
-    if isinstance(value, torch.dtype):
-        if value not in _FROM_TORCH:
-            raise UnsupportedDTypeError(value)
-        return _FROM_TORCH[value]
+    if _is_torch_dtype(value):
+        return from_torch_dtype(value)
     if isinstance(value, str):
         return DType("bool" if value == "bool_" else value)
     try:
@@ -142,10 +152,11 @@ def from_numpy_dtype(value: np.dtype) -> DType:
         raise UnsupportedDTypeError(value) from None
 
 
-def from_torch_dtype(value: torch.dtype) -> DType:
-    if value not in _FROM_TORCH:
+def from_torch_dtype(value) -> DType:
+    found = _torch_table()[1].get(value)
+    if found is None:
         raise UnsupportedDTypeError(value)
-    return _FROM_TORCH[value]
+    return found
 
 
 # ---- promotion of a floating Tensor with a scalar operand ------------------------------

@@ -13,7 +13,7 @@ uses ``zero_grads``, one launch per dtype.
 
 from __future__ import annotations
 
-import torch
+from .array import DeviceArray
 
 from .backends import ensure_same_device, get_backend
 from .backends._graph_capture import reject_during_capture
@@ -88,7 +88,8 @@ def _accumulate_round(members) -> None:
                 gradient._materialize()
             stored = parameter._grad
             if stored is None:
-                storage = torch.empty(parameter.shape, dtype=parameter.dtype.torch_dtype, device=parameter.device.torch)
+                with backend.context():
+                    storage = DeviceArray.empty(parameter.shape, parameter.dtype, parameter.device)
                 parameter._grad = Tensor._from_storage(storage)
                 fresh.append((parameter._grad, gradient))
             else:

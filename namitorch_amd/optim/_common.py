@@ -24,11 +24,11 @@ import struct
 from numbers import Real
 
 import numpy as np
-import torch
 
+from ..array import DeviceArray, is_device_array
 from ..backends import ensure_same_device, get_backend
 from ..backends._graph_capture import reject_during_capture
-from ..dtype import DType, from_numpy_dtype, from_torch_dtype
+from ..dtype import DType, bfloat16, from_numpy_dtype
 from ..tensor import Tensor, enable_grad, no_grad
 from .optimizer import Optimizer
 
@@ -108,8 +108,12 @@ def _zeros_views(shapes, dtype: DType, device) -> list:
     for count in counts:
         offsets.append(total)
         total += -(-count // _ARENA_ALIGN) * _ARENA_ALIGN
-    flat = torch.zeros(max(total, 1), dtype=dtype.torch_dtype, device=device.torch)
-    return [Tensor._from_storage(flat.narrow(0, offset, count).view(tuple(shape)))
+    if device.type == "cpu":
+        flat = np.zeros(max(total, 1), dtype=np.uint16 if dtype is bfloat16 else dtype.numpy_dtype)
+        return [Tensor._from_storage(flat[offset:offset + count].reshape(tuple(shape)), dtype=dtype)
+                for offset, count, shape in zip(offsets, counts, shapes)]
+    flat = DeviceArray.zeros((max(total, 1),), dtype, device)
+    return [Tensor._from_storage(flat.narrow(offset, count, tuple(shape)))
             for offset, count, shape in zip(offsets, counts, shapes)]
 
 
@@ -131,7 +135,10 @@ def _pack_state_buffers(states, names, keep=frozenset()) -> None:
             views = _zeros_views([buffer.shape for buffer in buffers], dtype, device)
             moved = {}
             for buffer, view in zip(buffers, views):
-                view._storage.copy_(buffer._storage)
+                if isinstance(view._storage, DeviceArray):
+                    view._storage.copy_from(buffer._storage)
+                else:
+                    np.copyto(view._storage, buffer._storage)
                 moved[id(buffer)] = view
             for values in states:
                 for key, buffer in values.items():
@@ -221,14 +228,14 @@ class _FirstOrderOptimizer(Optimizer):
             if name not in values:
                 continue
             value = values[name]
-            if not isinstance(value, (Tensor, np.ndarray, torch.Tensor)):
-                raise TypeError(f"{path}[{name!r}] must be a floating Tensor or NumPy array.")
             if isinstance(value, Tensor):
                 dtype = value.dtype
-            elif isinstance(value, torch.Tensor):
-                dtype = from_torch_dtype(value.dtype)
-            else:
+            elif isinstance(value, np.ndarray):
                 dtype = from_numpy_dtype(value.dtype)
+            elif is_device_array(value):
+                dtype = DeviceArray.wrap(value).dtype
+            else:
+                raise TypeError(f"{path}[{name!r}] must be a floating Tensor or NumPy array.")
             if not dtype.is_floating_point:
                 raise TypeError(f"{path}[{name!r}] must have a floating dtype.")
             if tuple(value.shape) != parameter.shape:
@@ -249,14 +256,17 @@ class _FirstOrderOptimizer(Optimizer):
             if value._clean_version is not None and value._clean_version == value._version_counter.value:
                 return False      # written only by this optimizer's kernels since the last check
             if value.device.type == "cpu":
-                result = bool((value._data.to(torch.float32) < 0).any())
+                result = bool(np.any(np.less(value.numpy(), 0)))
             else:
                 result = get_backend(value).any_negative(value._data, value.dtype.code)
             if not result:
                 value._clean_version = value._version_counter.value
             return result
-        if isinstance(value, torch.Tensor):
-            return bool((value.to(torch.float32) < 0).any())
+        if not isinstance(value, np.ndarray):
+            array = DeviceArray.wrap(value)
+            if array.dtype.code != -1:
+                return get_backend(array).any_negative(array, array.dtype.code)
+            value = array.download()
         return bool(np.any(np.less(value, 0)))
 
     def _prepare_state(self, values: dict, parameter: Tensor, path: str) -> dict:

@@ -37,15 +37,14 @@ from ..backends import get_backend
 from ..backends._settings import fused_kernels_enabled
 from ..backends.hip import make_xform
 from ..dtype import DType, bfloat16, float16, float32, float64, normalize_dtype
-from ..tensor import Tensor
+from ..tensor import Tensor, _assign_host
 from ._common import _FirstOrderOptimizer, _real_option, _round_scalar, _zeros_views
 
 _LOW_PRECISION = (float16, bfloat16, float32)
 
 
 def _zeros_like(parameter: Tensor, dtype: DType) -> Tensor:
-    import torch
-    return Tensor._from_storage(torch.zeros(parameter.shape, dtype=dtype.torch_dtype, device=parameter.device.torch))
+    return _zeros_views([parameter.shape], dtype, parameter.device)[0]
 
 
 class Adam(_FirstOrderOptimizer):
@@ -130,7 +129,10 @@ class Adam(_FirstOrderOptimizer):
                 views = _zeros_views([parameter.shape for parameter in members], dtype, device)
                 for parameter, view in zip(members, views):
                     if name == "master":
-                        view._storage.copy_(parameter._data)       # exact: widening to float32
+                        if view._device.type == "cpu":
+                            _assign_host(view._storage, parameter._data, view._dtype, parameter._dtype)
+                        else:
+                            view._storage.copy_from(parameter._data)     # exact: widening to float32
                     states[id(parameter)][name] = view
 
     def _buffers(self, parameter: Tensor, state: dict):

@@ -29,10 +29,11 @@ from itertools import repeat
 from operator import attrgetter, eq, is_
 
 import numpy as np
-import torch
 
+from ..array import DeviceArray
 from ..backends import ensure_same_device, get_backend
 from ..backends._graph_capture import reject_during_capture
+from ..dtype import float64
 from ..tensor import GradTransform, Tensor, no_grad
 
 _NORM_EPS = 1e-6
@@ -240,8 +241,11 @@ def _total_norm(gradients: list[Tensor], norm_type: float) -> float:
 
 def _norm_tensor(norm: float, gradients) -> Tensor:
     device = gradients[0].device if gradients else None
-    # A fill with the value as a kernel argument: no host-to-device copy to wait for.
-    storage = torch.full((), norm, dtype=torch.float64, device=None if device is None else device.torch)
+    if device is None or device.type == "cpu":
+        return Tensor._from_storage(np.array(norm, dtype=np.float64), False)
+    # A fill with the value's bits as a kernel argument: no host-to-device copy to wait for.
+    storage = DeviceArray.empty((), float64, device)
+    storage.fill_bits(int(np.float64(norm).view(np.uint64)))
     return Tensor._from_storage(storage, False)
 
 

@@ -32,8 +32,8 @@ from itertools import chain, compress, repeat
 from operator import and_, attrgetter, eq, is_, is_not, itemgetter
 
 import numpy as np
-import torch
 
+from ..array import DeviceArray, is_device_array
 from ..backends import ensure_same_device
 from ..backends._graph_capture import reject_during_capture
 from ..device import Device
@@ -51,7 +51,13 @@ _FIRST_OF = itemgetter(0)
 _SECOND_OF = itemgetter(1)
 _CALL_REF = weakref.ReferenceType.__call__
 
-_ARRAY_TYPES = (Tensor, np.ndarray, torch.Tensor)
+_ARRAY_TYPES = (Tensor, np.ndarray, DeviceArray)
+
+
+def _is_array(value) -> bool:
+    """A Tensor, a NumPy array or a device array (ours or another framework's)."""
+    return isinstance(value, _ARRAY_TYPES) or is_device_array(value)
+
 _PASS_THROUGH = (bool, int, float, str, bytes)
 _KEY_TYPES = (str, int)
 
@@ -75,7 +81,7 @@ class _StateTree:
         self.open: set = set()
 
     def rebuild(self, value, path: str):
-        if isinstance(value, _ARRAY_TYPES):
+        if _is_array(value):
             return self.leaf(value, path)
         if isinstance(value, np.generic):
             from_numpy_dtype(value.dtype)
@@ -121,7 +127,7 @@ def _copy_leaf(parameter_shape):
         if isinstance(value, np.ndarray):
             from_numpy_dtype(value.dtype)
             return value.copy()
-        return value.clone()
+        return DeviceArray.wrap(value).clone()
 
     return copy
 

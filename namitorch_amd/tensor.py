@@ -7,9 +7,10 @@ the in-place version counter (``tensor.py:71-76``) and ``copy_`` /
 ``__setitem__(...)`` that convert to the destination dtype and bump the
 version (``tensor.py:1269-1287``).
 
-Storage is a contiguous ``torch.Tensor`` (device memory on HIP devices):
-torch is used for allocation and streams only, never for the step's
-arithmetic.
+Storage is contiguous: a NumPy array on the host (bfloat16 as uint16 bit
+patterns) and a :class:`namitorch_amd.array.DeviceArray` on HIP devices,
+memory of the library's own allocator or, wrapped without a copy, a device
+array of another framework.
 
 Deferred gradient transforms.  ``GradScaler.unscale_`` and
 ``clip_grad_norm_`` rewrite gradients in place in the reference
@@ -29,14 +30,13 @@ from dataclasses import dataclass
 from numbers import Real
 
 import numpy as np
-import torch
 
+from .array import DeviceArray, is_device_array
 from .backends._graph_capture import reject_during_capture
 from .device import Device
 from .dtype import (
     DType,
     bfloat16,
-    float16,
     float32,
     from_numpy_dtype,
     from_torch_dtype,
@@ -46,6 +46,9 @@ from .dtype import (
     round_scalar,
     scalar_dtype,
 )
+
+_CPU = Device("cpu")
+_UNSIGNED = {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}
 
 
 class _VersionCounter:
@@ -71,17 +74,6 @@ def _settle_device_steps() -> None:
 
 # ---- grad mode (namitorch/autograd.py:15-42) -----------------------------------------
 _grad_mode = threading.local()
-# One immutable Device per torch device: tensors on one device share it, so
-# device comparisons between them are identity checks.
-_DEVICES: dict = {}
-
-
-def _storage_device(place: torch.device) -> Device:
-    found = _DEVICES.get(place)
-    if found is None:
-        found = Device("cpu") if place.type == "cpu" else Device("cuda", place.index)
-        _DEVICES[place] = found
-    return found
 
 
 def is_grad_enabled() -> bool:
@@ -153,18 +145,37 @@ def _bf16_bits_from_f32_bits(bits: np.ndarray) -> np.ndarray:
     return np.where(nan, quiet, rounded)
 
 
-def _host_array(data: object, dtype: DType) -> torch.Tensor:
-    """Host data -> CPU torch tensor of `dtype`, rounded once like NumPy's cast."""
+def _values(storage: np.ndarray, dtype: DType) -> np.ndarray:
+    """The values a host storage array holds (bfloat16 bits widened exactly to float32)."""
     if dtype is bfloat16:
-        array = np.asarray(data)
+        return (np.ascontiguousarray(storage).astype(np.uint32) << 16).view(np.float32)
+    return storage
+
+
+def _host_framework_array(data) -> np.ndarray | None:
+    """Values of another framework's host array (PyTorch-style ``numpy()``),
+    bfloat16 widened exactly; None for anything else."""
+    place = getattr(data, "device", None)
+    if getattr(place, "type", None) != "cpu" or not callable(getattr(data, "numpy", None)):
+        return None
+    if str(getattr(data, "dtype", "")).endswith("bfloat16"):
+        return data.float().numpy()
+    return data.numpy()
+
+
+def _host_array(data: object, dtype: DType) -> np.ndarray:
+    """Host data -> a NumPy array in `dtype`'s storage format (bfloat16 as
+    uint16 bit patterns), rounded once like NumPy's cast."""
+    framework = _host_framework_array(data)
+    if framework is not None:
+        data = framework
+    if dtype is bfloat16:
+        array = np.ascontiguousarray(data)
         if array.dtype == np.float32:
-            bits = _bf16_bits_from_f32_bits(array.view(np.uint32))
-        else:
-            bits = _bf16_bits_from_f64(array.astype(np.float64))
-        return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16)
+            return np.ascontiguousarray(_bf16_bits_from_f32_bits(array.view(np.uint32)))
+        return np.ascontiguousarray(_bf16_bits_from_f64(array.astype(np.float64)))
     with np.errstate(over="ignore", under="ignore", invalid="ignore"):
-        array = np.array(data, dtype=dtype.numpy_dtype, copy=True, order="C")
-    return torch.from_numpy(array)
+        return np.array(data, dtype=dtype.numpy_dtype, copy=True, order="C")
 
 
 def _resolve_dtype(data: object, dtype: object) -> DType:
@@ -172,8 +183,12 @@ def _resolve_dtype(data: object, dtype: object) -> DType:
         return normalize_dtype(dtype)
     if isinstance(data, Tensor):
         return data.dtype
-    if isinstance(data, torch.Tensor):
+    if isinstance(data, DeviceArray):
+        return data.dtype
+    if not isinstance(data, (np.ndarray, np.generic)) and type(getattr(data, "dtype", None)).__module__ == "torch":
         return from_torch_dtype(data.dtype)
+    if is_device_array(data):
+        return DeviceArray.wrap(data).dtype
     if isinstance(data, (np.ndarray, np.generic)):
         return from_numpy_dtype(data.dtype)
     if isinstance(data, builtins.bool):
@@ -188,17 +203,76 @@ def _resolve_dtype(data: object, dtype: object) -> DType:
     return from_numpy_dtype(array.dtype)
 
 
-def _make_storage(data: object, dtype: DType, device: Device) -> torch.Tensor:
-    source = data._data if isinstance(data, Tensor) else data
-    if isinstance(source, torch.Tensor):
-        if source.dtype == torch.float64 and dtype in (float16, bfloat16) and source.device.type != "cpu":
-            raise TypeError("Device float64 -> float16/bfloat16 conversions must go through the host for exact rounding.")
-        if source.dtype == torch.float64 and dtype in (float16, bfloat16):
-            host = _host_array(source.numpy(), dtype)
-            return host.to(device.torch, copy=True).contiguous()
-        return source.to(device=device.torch, dtype=dtype.torch_dtype, copy=True).contiguous()
+def _make_storage(data: object, dtype: DType, device: Device):
+    """New storage of `dtype` on `device` holding `data`'s values, each
+    rounded once to `dtype` (NumPy's cast; on the device ``nt_cast``)."""
+    if isinstance(data, Tensor):
+        source, source_dtype = data._data, data._dtype
+    else:
+        source, source_dtype = data, None
+    if isinstance(source, DeviceArray) or (not isinstance(source, np.ndarray) and is_device_array(source)):
+        array = DeviceArray.wrap(source)
+        if device is array.device and (array.dtype is dtype or (array.dtype._floating and dtype._floating)):
+            return DeviceArray.empty(array.shape, dtype, device).copy_from(array)
+        source = _values(array.download(), array.dtype)
+    elif source_dtype is not None:
+        source = _values(source, source_dtype)
     host = _host_array(source, dtype)
-    return host.to(device.torch, copy=True).contiguous()
+    if device.type == "cpu":
+        return host
+    return DeviceArray.empty(host.shape, dtype, device).upload(host)
+
+
+def _device_of(data: object) -> Device:
+    """Where data handed to the Tensor constructor lives."""
+    if isinstance(data, Tensor):
+        return data.device
+    if isinstance(data, DeviceArray):
+        return data.device
+    if not isinstance(data, np.ndarray) and is_device_array(data):
+        return DeviceArray.wrap(data).device
+    return _CPU
+
+
+def _on_device(value: object) -> bool:
+    return isinstance(value, DeviceArray) or (not isinstance(value, np.ndarray) and is_device_array(value))
+
+
+def _assign_device(target: DeviceArray, source: object, dtype: DType) -> None:
+    """``target[...] = source`` for device storage: device sources are copied
+    (and converted between floating dtypes) on the device; host values are
+    converted on the host and uploaded, a single value as a fill."""
+    if _on_device(source):
+        array = DeviceArray.wrap(source)
+        if array.device != target.device:
+            raise RuntimeError(f"Operands are on different devices: {target.device}, {array.device}; "
+                               "use an explicit .to() transfer.")
+        if array.numel() == target.numel() and (array.dtype is dtype or (array.dtype._floating and dtype._floating)):
+            if array.data_ptr() != target.data_ptr():
+                target.copy_from(array)
+            return
+        source = _values(array.download(), array.dtype)
+    host = _host_array(source, dtype)
+    if host.size == 1 and target.numel() != 1:
+        target.fill_bits(int(host.reshape(-1).view(_UNSIGNED[dtype.itemsize])[0]))
+        return
+    if host.size != target.numel():
+        host = np.ascontiguousarray(np.broadcast_to(host, target.shape))
+    target.upload(host)
+
+
+def _assign_host(target: np.ndarray, source: object, dtype: DType, source_dtype: DType | None) -> None:
+    """``target[...] = source`` for host storage; `source_dtype` names the
+    dtype of a Tensor's storage handed in as `source`."""
+    if source_dtype is not None:
+        source = _values(source, source_dtype)
+    elif _on_device(source):
+        array = DeviceArray.wrap(source)
+        source = _values(array.download(), array.dtype)
+    host = _host_array(source, dtype)
+    if host.size == target.size:
+        host = host.reshape(target.shape)
+    np.copyto(target, np.broadcast_to(host, target.shape))
 
 
 class Tensor:
@@ -209,23 +283,37 @@ class Tensor:
 
     def __init__(self, data: object, dtype: object = None, requires_grad: builtins.bool = False, *, device=None):
         resolved = _resolve_dtype(data, dtype)
-        if device is None:
-            if isinstance(data, Tensor):
-                target = data.device
-            elif isinstance(data, torch.Tensor):
-                target = Device(str(data.device)) if data.device.type == "cpu" else Device("cuda", data.device.index)
-            else:
-                target = Device("cpu")
-        else:
-            target = Device(device)
-        self._initialize(_make_storage(data, resolved, target), requires_grad)
+        target = _device_of(data) if device is None else Device(device)
+        self._initialize(_make_storage(data, resolved, target), requires_grad, dtype=resolved)
 
-    def _initialize(self, storage: torch.Tensor, requires_grad: builtins.bool, version_counter: _VersionCounter | None = None):
-        if not isinstance(storage, torch.Tensor) or not storage.is_contiguous():
-            raise TypeError("Tensor storage must be a contiguous array.")
+    def _initialize(self, storage, requires_grad: builtins.bool, version_counter: _VersionCounter | None = None,
+                    dtype: DType | None = None):
+        """Adopt `storage` without a copy: a C-contiguous NumPy array (bfloat16
+        as uint16 bits, with ``dtype=bfloat16``), a DeviceArray, or another
+        framework's contiguous device array (wrapped)."""
+        if isinstance(storage, np.ndarray):
+            if not storage.flags.c_contiguous:
+                raise TypeError("Tensor storage must be a contiguous array.")
+            kind = from_numpy_dtype(storage.dtype) if dtype is None else normalize_dtype(dtype)
+            expected = np.dtype(np.uint16) if kind is bfloat16 else kind.numpy_dtype
+            if storage.dtype != expected:
+                raise TypeError(f"{kind.name} host storage must be a {expected.name} array, got {storage.dtype.name}.")
+            self._device = _CPU
+            self._ptr = None
+            self._numel = storage.size
+        else:
+            try:
+                storage = DeviceArray.wrap(storage)
+            except ValueError as error:
+                raise TypeError(f"Tensor storage must be a contiguous array: {error}") from None
+            kind = storage.dtype
+            if dtype is not None and normalize_dtype(dtype) is not kind:
+                raise TypeError(f"Storage of dtype {kind.name} cannot back a {normalize_dtype(dtype).name} Tensor.")
+            self._device = storage.device
+            self._ptr = storage.data_ptr()
+            self._numel = storage.numel()
         self._storage = storage
-        self._dtype = from_torch_dtype(storage.dtype)
-        self._device = _storage_device(storage.device)
+        self._dtype = kind
         if requires_grad and not self._dtype.can_require_grad:
             raise TypeError(f"Only floating Tensors can require gradients, got {self._dtype.name}.")
         self._requires_grad = requires_grad
@@ -234,20 +322,19 @@ class Tensor:
         self._writable = True
         self._pending = None
         self._is_leaf = True
-        self._ptr = storage.data_ptr() if storage.device.type != "cpu" else None
-        self._numel = storage.numel()
         self._clean_version = None      # version at which a state buffer was last known nonnegative
         self._finite_version = None     # version at which GradScaler last knew the gradient's finiteness
 
     @classmethod
-    def _from_storage(cls, storage: torch.Tensor, requires_grad: builtins.bool = False, version_counter=None) -> "Tensor":
+    def _from_storage(cls, storage, requires_grad: builtins.bool = False, version_counter=None,
+                      dtype: DType | None = None) -> "Tensor":
         instance = cls.__new__(cls)
-        Tensor._initialize(instance, storage, requires_grad, version_counter)
+        Tensor._initialize(instance, storage, requires_grad, version_counter, dtype)
         return instance
 
     # ---- storage access --------------------------------------------------------------
     @property
-    def _data(self) -> torch.Tensor:
+    def _data(self):
         if self._pending is not None:
             self._materialize()
         return self._storage
@@ -271,7 +358,7 @@ class Tensor:
 
     @property
     def ndim(self) -> int:
-        return self._storage.dim()
+        return len(self._storage.shape)
 
     @property
     def size(self) -> int:
@@ -361,13 +448,12 @@ class Tensor:
         self._ensure_inplace_allowed()
         if isinstance(value, Tensor) and value.device != self.device:
             raise RuntimeError(f"Operands are on different devices: {self.device}, {value.device}; use an explicit .to() transfer.")
-        converted = _make_storage(value, self._dtype, self._device)
-        if converted.numel() == 1 and self.size != 1:
-            converted = converted.reshape(()).expand(self.shape)
-        elif tuple(converted.shape) != self.shape:
-            converted = converted.reshape(self.shape) if converted.numel() == self.size else converted.expand(self.shape)
+        source = value._data if isinstance(value, Tensor) else value
         self._pending = None
-        self._storage.copy_(converted)
+        if isinstance(self._storage, DeviceArray):
+            _assign_device(self._storage, source, self._dtype)
+        else:
+            _assign_host(self._storage, source, self._dtype, value._dtype if isinstance(value, Tensor) else None)
         self._version_counter.increment()
 
     def _accumulate_grad(self, gradient: "Tensor") -> None:
@@ -391,30 +477,29 @@ class Tensor:
         """Host copy; bfloat16 is returned as (exact) float32 values."""
         reject_during_capture("Host Tensor reads")
         storage = self._data
-        if self._dtype is bfloat16:
-            storage = storage.to(torch.float32)
-        return storage.detach().cpu().numpy().copy()
+        host = storage.download() if isinstance(storage, DeviceArray) else storage.copy()
+        return _values(host, self._dtype)
 
     def bits(self) -> np.ndarray:
         """Host copy of the raw bit patterns (uint16 for 16-bit types)."""
         reject_during_capture("Host Tensor reads")
         storage = self._data
-        view = {2: torch.int16, 4: torch.int32, 8: torch.int64, 1: torch.uint8}[self._dtype.itemsize]
-        unsigned = {2: np.uint16, 4: np.uint32, 8: np.uint64, 1: np.uint8}[self._dtype.itemsize]
-        return storage.view(view).cpu().numpy().view(unsigned).copy()
+        if isinstance(storage, DeviceArray):
+            return storage.raw_bits()
+        return storage.view(_UNSIGNED[self._dtype.itemsize]).copy()
 
     def item(self):
         reject_during_capture("Host Tensor reads")
         if self.size != 1:
             raise ValueError(f"item() requires exactly one element, got {self.size}.")
-        return self._data.reshape(()).item()
+        return self.numpy().reshape(()).item()
 
     def detach(self) -> "Tensor":
-        result = Tensor._from_storage(self._data, False, self._version_counter)
-        return result
+        return Tensor._from_storage(self._data, False, self._version_counter, self._dtype)
 
     def clone(self) -> "Tensor":
-        return Tensor._from_storage(self._data.clone(), False)
+        return Tensor._from_storage(self._data.clone() if isinstance(self._data, DeviceArray) else self._data.copy(),
+                                    False, dtype=self._dtype)
 
     def to(self, device=None, dtype=None) -> "Tensor":
         target = self.device if device is None else Device(device)

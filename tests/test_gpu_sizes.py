@@ -20,6 +20,7 @@ import pytest
 import torch
 
 import namitorch_amd as nt
+from namitorch_amd.array import DeviceArray
 from oracle import adam as oadam
 from oracle import clip as oclip
 from oracle import lowp
@@ -47,7 +48,9 @@ def _window(block: np.ndarray, lo: int, hi: int) -> np.ndarray:
     return block[np.arange(lo, hi, dtype=np.int64) % BLOCK]
 
 
-def _host(tensor: torch.Tensor, lo: int, hi: int) -> np.ndarray:
+def _host(tensor, lo: int, hi: int) -> np.ndarray:
+    if isinstance(tensor, DeviceArray):
+        return tensor.narrow(lo, hi - lo).download()      # bfloat16 as uint16 bits
     values = tensor[lo:hi].cpu()
     return values.view(torch.int16).numpy().view(np.uint16) if values.dtype == torch.bfloat16 else values.numpy()
 
@@ -61,6 +64,7 @@ def _release():
     yield
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
+    nt.runtime.empty_cache(0)
 
 
 @pytest.mark.parametrize("path", ["optimizer", "per_tensor_hook"])

@@ -156,7 +156,7 @@ def _run(monkeypatch, memo: bool, master: bool = False):
             for p in params:
                 p.grad = nt.Tensor(rng.standard_normal(p.shape).astype(np.float32), dtype=dtype)
         elif k == 23:                                         # a gradient aliasing its parameter's storage
-            params[2].grad = nt.Tensor._from_storage(params[2]._storage)
+            params[2].grad = nt.Tensor._from_storage(params[2]._storage, dtype=params[2].dtype)
         elif k == 24:
             params[2].grad = nt.Tensor(rng.standard_normal(params[2].shape).astype(np.float32), dtype=dtype)
         try:
