@@ -5,9 +5,10 @@
  * AdamW.step(), GradScaler unscale_/finite-check/update and clip_grad_norm_.
  * Every entry point takes plain pointers, sizes and a hipStream_t passed as
  * `void*`; no framework types cross the boundary.  Callers (the Python host
- * layer in namitorch_amd/, through ctypes) own every tensor buffer.  The
- * library owns only multi-tensor plans (descriptor table, task map and
- * reduction workspace), released by nt_plan_destroy().
+ * layer in namitorch_amd/, through ctypes) own every tensor buffer: memory
+ * from the library's caching allocator (nt_malloc) or from any other
+ * allocator.  The library also owns multi-tensor plans (descriptor table,
+ * task map and reduction workspace), released by nt_plan_destroy().
  *
  * Status codes: 0 = OK; a negative code names the exception class the
  * Python layer raises, with the message from nt_last_error() (per thread).
@@ -271,8 +272,17 @@ int32_t nt_plan_destroy(nt_plan *plan);
 
 /*
  * Replace one pointer column of every descriptor of `plan`: column 0 param,
- * 1 grad, 2 exp_avg, 3 exp_avg_sq, 4 model_copy; `pointers[n]` with n the
- * plan's tensor count.  The update is a copy queued on `stream` after the
+ * 1 grad, 2 exp_avg, 3 exp_avg_sq, 4 model_copy, 5 incoming; `pointers[n]`
+ * with n the plan's tensor count.
+ *
+ * Column 5 (incoming, NULL allowed per tensor, grad dtype, not float64)
+ * defers the last micro-batch's gradient accumulation into the step
+ * (Tensor._accumulate_grad, tensor.py:443-450, autograd.py:198-205): for a
+ * tensor with an incoming pointer, nt_amp_prepass and nt_adamw_mt use
+ * round_to_grad_dtype(grad + incoming) as its gradient, the value the
+ * accumulation would have stored, and do not write `grad`.  nt_grad_apply,
+ * nt_grad_norm_pow, nt_grad_zero and nt_grad_accumulate refuse a plan with
+ * any incoming pointer set (NT_ERR_VALUE).  The update is a copy queued on `stream` after the
  * work already queued there, so kernels launched earlier keep the old
  * pointers.  Lets one plan serve gradients that are reallocated every step
  * (Optimizer.zero_grad(set_to_none=True), optim/optimizer.py:197-206, then a
@@ -295,6 +305,8 @@ int32_t nt_plan_info(const nt_plan *plan, uint64_t *numel, int32_t *tensors,
  * element arithmetic is the reference's, operation for operation and
  * without FMA contraction (backends/cuda/adamw.py:15-25 ==
  * optim/adam.py:35-42 + optim/_common.py:67-73).  `xform` may be NULL.
+ * A tensor's incoming gradient (plan column 5) is added to its gradient
+ * first.
  */
 int32_t nt_adamw_mt(nt_plan *plan, const void *slots, int32_t nslots,
                     const nt_grad_xform *xform, void *stream);
@@ -305,7 +317,8 @@ int32_t nt_adamw_mt(nt_plan *plan, const void *slots, int32_t nslots,
  * finiteness of g' (amp.py:152-167) and the fp64 sum of squares and max of
  * |g'| (optim/clip_grad.py:63-79).  Writes per-workgroup partials into the
  * plan's workspace; grads are not written.  With `ctrl != NULL` the scale
- * is read from ctrl->scale on the device (the sync-free path).
+ * is read from ctrl->scale on the device (the sync-free path).  A tensor's
+ * incoming gradient (plan column 5) is added to its gradient first.
  */
 int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale,
                        const nt_amp_ctrl *ctrl, void *stream);

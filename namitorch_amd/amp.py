@@ -30,7 +30,7 @@ from .backends import get_backend
 from .backends._graph_capture import reject_during_capture
 from .dtype import float32, float64, promote_with_scalar
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
-from .tensor import GradTransform, _unsettled_steps, is_grad_enabled
+from .tensor import GradTransform, _unsettled_steps, check_addends, is_grad_enabled
 
 _REQUIRES = attrgetter("_requires_grad")
 _WRITABLE = attrgetter("_writable")
@@ -482,6 +482,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     if (any(map(_REQUIRES, gradients)) and is_grad_enabled()) or not all(map(_WRITABLE, gradients)):
         for gradient in gradients:
             gradient._ensure_inplace_allowed()            # raises the matching error
+    check_addends(gradients)                              # before any bookkeeping changes
     if any(map(_PENDING, gradients)):
         for gradient in gradients:
             if gradient._pending is not None:
@@ -496,7 +497,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     deque(map(setattr, gradients, repeat("_finite_version"), map(_VALUE, counters)), 0)
     if maximum is not None:
         clip_bumps.extend(zip(gradients, map(_VALUE, map(_COUNTER, gradients))))
-    plan = backend.grad_plan(gradients, dtype)
+    plan = backend.grad_plan(gradients, dtype, incoming=True)
     backend.grad_prepass(plan, None, previous.data_ptr(), unscale=amp)
     flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)

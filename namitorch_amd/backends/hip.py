@@ -34,6 +34,7 @@ from ..device import Device
 from ..dtype import float32, int32, uint8
 
 PLAN_CACHE_SIZE = 16
+INCOMING = 5          # plan pointer column of deferred incoming gradients
 _backends_alive: "weakref.WeakSet[HIPBackend]" = weakref.WeakSet()
 _shutting_down = False
 
@@ -238,8 +239,9 @@ class HIPBackend:
                 if plan is not None:
                     return plan
             full = rows
-            if volatile:
-                full = [tuple(pointers[c][i] if c in pointers else value for c, value in enumerate(row))
+            in_rows = {column: values for column, values in (pointers or {}).items() if column < INCOMING}
+            if in_rows:
+                full = [tuple(in_rows[c][i] if c in in_rows else value for c, value in enumerate(row))
                         for i, row in enumerate(rows)]
             table = (_native.MtTensor * max(1, len(full)))()
             for index, (param, grad, first, second, copy, numel, slot) in enumerate(full):
@@ -249,7 +251,9 @@ class HIPBackend:
             with self.context():
                 _native.call("nt_plan_create", self.device.index, table, len(full), ctypes.byref(spec), chunk, stream, ctypes.byref(handle))
             plan = Plan(handle.value, layout)
-            plan.columns = {column: tuple(values) for column, values in (pointers or {}).items()}
+            plan.columns = {column: tuple(values) for column, values in in_rows.items()}
+            if INCOMING in (pointers or {}) and not self._refresh_locked(plan, {INCOMING: pointers[INCOMING]}, stream):
+                raise ValueError("Incoming gradients must be 16-byte aligned.")
             self._plans[key] = plan
             self._plans.move_to_end(key)
             while len(self._plans) > PLAN_CACHE_SIZE:
@@ -276,11 +280,22 @@ class HIPBackend:
             plan.columns[column] = values
         return True
 
-    def grad_plan(self, tensors, dtype) -> Plan:
-        """Gradient-only plan (the `grad` column volatile)."""
+    def grad_plan(self, tensors, dtype, incoming: bool = False) -> Plan:
+        """Gradient-only plan (the `grad` column volatile).  With `incoming`
+        (the pre-pass) the deferred accumulations of the gradients become the
+        plan's incoming column; otherwise they are written back first."""
+        pointers = {1: [tensor._ptr for tensor in tensors]}
+        addends = incoming_pointers(tensors)
+        if addends is not None:
+            if incoming:
+                pointers[INCOMING] = addends
+            else:
+                for tensor in tensors:
+                    if tensor._incoming is not None:
+                        tensor._materialize()
         layout = (_native.NT_DTYPE_NONE, dtype.code, _native.NT_DTYPE_NONE, _native.NT_DTYPE_NONE)
         rows = [(0, 0, 0, 0, 0, tensor._numel, 0) for tensor in tensors]
-        return self.plan(rows, layout, pointers={1: [tensor._ptr for tensor in tensors]})
+        return self.plan(rows, layout, pointers=pointers)
 
     # ---- multi-tensor kernels --------------------------------------------------------------
     def adamw_multi(self, plan: Plan, slots, xform: _native.GradXform | None) -> None:
@@ -399,6 +414,21 @@ class HIPBackend:
             flag = DeviceArray.empty((1,), int32, self.device)
             _native.call("nt_any_negative", array.data_ptr(), code, array.numel(), flag.data_ptr(), self.stream())
             return bool(flag.download()[0])
+
+
+def incoming_pointers(gradients) -> list | None:
+    """The incoming-gradient column for `gradients` (0 where nothing is
+    deferred), or None when no gradient has a deferred accumulation.
+    Raises if an incoming gradient changed since it was deferred."""
+    if not any(map(_INCOMING_OF, gradients)):
+        return None
+    from ..tensor import check_addends
+    check_addends(gradients)
+    return [0 if gradient._incoming is None else gradient._incoming[0]._ptr for gradient in gradients]
+
+
+def _INCOMING_OF(gradient):
+    return gradient._incoming
 
 
 def _is_device(value) -> bool:

@@ -170,6 +170,8 @@ __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__rest
     auto *ap = reinterpret_cast<typename S::raw *>(d.exp_avg);
     auto *bp = reinterpret_cast<typename S::raw *>(d.exp_avg_sq);
     auto *cp = reinterpret_cast<typename C::raw *>(d.model_copy);
+    // A deferred accumulation: the gradient is round(grad + incoming).
+    const auto *ip = reinterpret_cast<const typename G::raw *>(d.incoming);
     const bool update = c.update_parameter != 0;
     const bool read_param = update || (c.coupled_weight_decay && c.weight_decay != 0.0f);
 
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__rest
         // All groups of an iteration are loaded first, then updated, then
         // stored stream by stream (fewer read/write turnarounds per wave).
         for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kTileElems) {
-            float p[UNROLL][kVec], g[UNROLL][kVec], a[UNROLL][kVec], b[UNROLL][kVec];
+            float p[UNROLL][kVec], g[UNROLL][kVec], h[UNROLL][kVec], a[UNROLL][kVec], b[UNROLL][kVec];
             bool ok[UNROLL];
 #pragma unroll
             for (int u = 0; u < UNROLL; ++u) {
@@ -187,6 +189,7 @@ __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__rest
                 ok[u] = i < vend;
                 if (ok[u]) {
                     Vec4IO<G, true>::load(gp, i, g[u]);
+                    if (ip != nullptr) Vec4IO<G, true>::load(ip, i, h[u]);
                     Vec4IO<S, true>::load(ap, i, a[u]);
                     Vec4IO<S, true>::load(bp, i, b[u]);
                     if (read_param) Vec4IO<P, true>::load(pp, i, p[u]);
@@ -197,7 +200,8 @@ __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__rest
                 if (ok[u]) {
 #pragma unroll
                     for (int k = 0; k < kVec; ++k) {
-                        const float gk = clip_one<G>(unscale_one<G>(g[u][k], xf), xf);
+                        const float gs = ip != nullptr ? G::round_f32(g[u][k] + h[u][k]) : g[u][k];
+                        const float gk = clip_one<G>(unscale_one<G>(gs, xf), xf);
                         adamw_elem<R>(p[u][k], gk, a[u][k], b[u][k], c);
                     }
                 }
@@ -224,7 +228,9 @@ __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__rest
     for (uint64_t i = scalar_from + threadIdx.x; i < end; i += BLOCK) {
         float p = read_param ? load1<P>(pp, i) : 0.0f;
         float a = load1<S>(ap, i), b = load1<S>(bp, i);
-        float g = clip_one<G>(unscale_one<G>(load1<G>(gp, i), xf), xf);
+        float g = load1<G>(gp, i);
+        if (ip != nullptr) g = G::round_f32(g + load1<G>(ip, i));
+        g = clip_one<G>(unscale_one<G>(g, xf), xf);
         adamw_elem<R>(p, g, a, b, c);
         store1<S>(ap, i, a);
         store1<S>(bp, i, b);

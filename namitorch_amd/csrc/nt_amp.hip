@@ -204,6 +204,17 @@ __device__ __forceinline__ void wave_join_finish(WaveJoin &j, Partial mine, Part
     *out = r;
 }
 
+// g <- round_G(g + h) elementwise: Tensor._accumulate_grad's add in the
+// gradient dtype (both operands already of that dtype; NumPy's float16 add
+// widens to float32 and rounds once, and so does bfloat16 here).
+template <class G>
+__device__ __forceinline__ void add_incoming(float (&g)[kPrepassUnroll][kVec], const float (&h)[kPrepassUnroll][kVec]) {
+#pragma unroll
+    for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) g[u][k] = G::round_f32(g[u][k] + h[u][k]);
+}
+
 // Visits the elements of this workgroup's tasks: vec(g) for each group of
 // kPrepassUnroll x 4 loaded values (missing ones 0), one(value) for
 // tail/unaligned elements.  Task entries and descriptors are read at
@@ -217,14 +228,23 @@ __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tens
         const DevTensor d = tensors[task.tensor];
         const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
         const auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
+        // A deferred accumulation: the gradient is round(grad + incoming).
+        const auto *ip = reinterpret_cast<const typename G::raw *>(d.incoming);
         // A whole, aligned 4096-element task (all but tensor tails): straight
-        // code with the kPrepassUnroll loads issued back to back.  The branch
-        // is workgroup-uniform.
+        // code with the kPrepassUnroll loads issued back to back.  The
+        // branches are workgroup-uniform.
         if (chunk == kPrepassTile && (d.flags & kAligned16) != 0u && start + (uint64_t)kPrepassTile <= d.numel) {
             float g[kPrepassUnroll][kVec];
 #pragma unroll
             for (int u = 0; u < kPrepassUnroll; ++u)
                 Vec4IO<G, true>::load(gp + start, (uint64_t)u * kBlock * kVec + (uint64_t)threadIdx.x * kVec, g[u]);
+            if (ip != nullptr) {
+                float h[kPrepassUnroll][kVec];
+#pragma unroll
+                for (int u = 0; u < kPrepassUnroll; ++u)
+                    Vec4IO<G, true>::load(ip + start, (uint64_t)u * kBlock * kVec + (uint64_t)threadIdx.x * kVec, h[u]);
+                add_incoming<G>(g, h);
+            }
             vec(g);
             continue;
         }
@@ -233,22 +253,28 @@ __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tens
         if (d.flags & kAligned16) {
             const uint64_t vend = start + ((end - start) & ~(uint64_t)(kVec - 1));
             for (uint64_t base = start + (uint64_t)threadIdx.x * kVec; base < vend; base += kPrepassTile) {
-                float g[kPrepassUnroll][kVec];
+                float g[kPrepassUnroll][kVec], h[kPrepassUnroll][kVec];
 #pragma unroll
                 for (int u = 0; u < kPrepassUnroll; ++u) {
                     const uint64_t i = base + (uint64_t)u * kBlock * kVec;
                     if (i < vend) {
                         Vec4IO<G, true>::load(gp, i, g[u]);
+                        if (ip != nullptr) Vec4IO<G, true>::load(ip, i, h[u]);
                     } else {
 #pragma unroll
-                        for (int k = 0; k < kVec; ++k) g[u][k] = 0.0f;
+                        for (int k = 0; k < kVec; ++k) g[u][k] = h[u][k] = 0.0f;
                     }
                 }
+                if (ip != nullptr) add_incoming<G>(g, h);
                 vec(g);
             }
             scalar_from = vend;
         }
-        for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock) one(load1<G>(gp, i));
+        for (uint64_t i = scalar_from + threadIdx.x; i < end; i += kBlock) {
+            float v = load1<G>(gp, i);
+            if (ip != nullptr) v = G::round_f32(v + load1<G>(ip, i));
+            one(v);
+        }
     }
 }
 
@@ -878,6 +904,7 @@ int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, dou
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
+    if ((rc = check_no_incoming(plan, "nt_grad_norm_pow")) != NT_OK) return rc;
     if (ctrl == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
     if (!(norm_type > 0.0) || __builtin_isinf(norm_type))
         return fail(NT_ERR_VALUE, "nt_grad_norm_pow needs a finite positive norm_type");
@@ -915,6 +942,7 @@ int32_t nt_grad_apply(nt_plan *plan, const nt_grad_xform *xform, void *stream) {
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
+    if ((rc = check_no_incoming(plan, "nt_grad_apply")) != NT_OK) return rc;
     if (xform == nullptr || plan->ntasks == 0) return NT_OK;
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");

@@ -187,6 +187,7 @@ int32_t nt_grad_zero(nt_plan *plan, void *stream) {
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
+    if ((rc = check_no_incoming(plan, "nt_grad_zero")) != NT_OK) return rc;
     if (plan->ntasks == 0) return NT_OK;
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
@@ -206,6 +207,7 @@ int32_t nt_grad_accumulate(nt_plan *plan, int32_t assign, void *stream) {
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
+    if ((rc = check_no_incoming(plan, "nt_grad_accumulate")) != NT_OK) return rc;
     const int32_t dst = plan->layout.grad_dtype, src = plan->layout.param_dtype;
     if (src == NT_DTYPE_NONE) return fail(NT_ERR_VALUE, "nt_grad_accumulate: the plan has no incoming gradients");
     if (plan->ntasks == 0) return NT_OK;

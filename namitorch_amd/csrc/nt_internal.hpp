@@ -35,6 +35,10 @@ struct nt_plan {
     hipEvent_t ring_events[nt::kRingSlots];
     bool ring_used[nt::kRingSlots];
     int32_t ring_next;
+    // Descriptors whose incoming-gradient column is set: only nt_amp_prepass
+    // and nt_adamw_mt (16/32-bit gradients) read that column; every other
+    // entry point refuses such a plan rather than ignore the addend.
+    int32_t n_incoming;
 };
 
 namespace nt {
@@ -100,6 +104,8 @@ Xform make_xform(const nt_grad_xform *x);
 
 // Validate a plan pointer.
 int32_t check_plan(const nt_plan *plan);
+// NT_ERR_VALUE (naming `entry`) when the plan has incoming gradients set.
+int32_t check_no_incoming(const nt_plan *plan, const char *entry);
 
 }  // namespace nt
 

@@ -19,12 +19,21 @@ struct alignas(64) DevTensor {
     uint64_t numel;
     uint32_t slot;
     uint32_t flags;       // bit 0: every role pointer is 16-byte aligned
+    // A gradient of the grad dtype still to be added to `grad` (the last
+    // micro-batch's accumulation, deferred): the kernels that take it use
+    // round(grad + incoming) as the gradient and do not write `grad`.
+    // NULL: none.
+    const void *incoming;
 };
 static_assert(sizeof(DevTensor) == 64, "descriptor layout");
 static_assert(offsetof(DevTensor, param) == 0 && offsetof(DevTensor, grad) == 8 && offsetof(DevTensor, exp_avg) == 16 &&
-                  offsetof(DevTensor, exp_avg_sq) == 24 && offsetof(DevTensor, model_copy) == 32,
+                  offsetof(DevTensor, exp_avg_sq) == 24 && offsetof(DevTensor, model_copy) == 32 &&
+                  offsetof(DevTensor, incoming) == 56,
               "pointer columns of the descriptor (nt_plan_set_pointers)");
 constexpr uint32_t kAligned16 = 1u;
+constexpr int32_t kIncomingColumn = 5;
+// Byte offset of pointer column c (0 param .. 4 model_copy, 5 incoming).
+constexpr size_t column_offset(int32_t c) { return c == kIncomingColumn ? offsetof(DevTensor, incoming) : (size_t)c * 8; }
 
 // One task per `chunk` consecutive elements of one tensor; workgroup i of a
 // multi-tensor launch processes task i.

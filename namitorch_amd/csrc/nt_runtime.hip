@@ -74,6 +74,13 @@ int32_t check_plan(const nt_plan *plan) {
     return NT_OK;
 }
 
+int32_t check_no_incoming(const nt_plan *plan, const char *entry) {
+    if (plan->n_incoming == 0) return NT_OK;
+    return fail(NT_ERR_VALUE, std::string(entry) +
+                                  ": the plan has incoming gradients (column 5); add them into the stored "
+                                  "gradients first (nt_grad_accumulate) or clear the column");
+}
+
 }  // namespace nt
 
 using namespace nt;
@@ -254,11 +261,16 @@ int32_t nt_plan_set_pointers(nt_plan *plan, int32_t column, const void *const *p
     hipStream_t s = (hipStream_t)stream;
     // Strided copy into column `column` of every descriptor, ordered on the
     // stream after the kernels already queued with the old pointers.
-    char *dst = reinterpret_cast<char *>(plan->d_tensors) + (size_t)column * sizeof(void *);
+    char *dst = reinterpret_cast<char *>(plan->d_tensors) + column_offset(column);
     NT_HIP_TRY(hipMemcpy2DAsync(dst, sizeof(DevTensor), ring, sizeof(void *), sizeof(void *), (size_t)n,
                                 hipMemcpyHostToDevice, s), "hipMemcpy2DAsync(plan pointers)");
     NT_HIP_TRY(hipEventRecord(plan->ring_events[slot], s), "hipEventRecord(plan ring)");
     plan->ring_used[slot] = true;
+    if (column == kIncomingColumn) {
+        int32_t set = 0;
+        for (int32_t t = 0; t < n; ++t) set += pointers[t] != nullptr;
+        plan->n_incoming = set;
+    }
     return NT_OK;
 }
 

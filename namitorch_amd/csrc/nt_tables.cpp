@@ -94,24 +94,29 @@ int32_t build_plan_tables(const nt_mt_tensor *tensors, int32_t n, const nt_mt_la
 
 int32_t check_pointer_column(const nt_mt_layout &layout, const std::vector<uint32_t> &flags, int32_t column,
                              const void *const *pointers, int32_t n, std::string &error) {
-    if (column < 0 || column > 4) {
-        error = "nt_plan_set_pointers: column must be 0..4";
+    if (column < 0 || column > kIncomingColumn) {
+        error = "nt_plan_set_pointers: column must be 0..5";
         return NT_ERR_VALUE;
     }
     if (n != (int32_t)flags.size() || (n > 0 && pointers == nullptr)) {
         error = "nt_plan_set_pointers: one pointer per plan tensor is required";
         return NT_ERR_VALUE;
     }
-    const int32_t dtypes[5] = {layout.param_dtype, layout.grad_dtype, layout.state_dtype, layout.state_dtype,
-                               layout.copy_dtype};
+    const int32_t dtypes[6] = {layout.param_dtype, layout.grad_dtype, layout.state_dtype, layout.state_dtype,
+                               layout.copy_dtype, layout.grad_dtype};
     const size_t size = dtype_size(dtypes[column]);
     if (size == 0) {
         error = "nt_plan_set_pointers: the plan layout has no such column";
         return NT_ERR_VALUE;
     }
+    if (column == kIncomingColumn && size == 8) {
+        error = "nt_plan_set_pointers: incoming gradients are not supported for float64 gradients";
+        return NT_ERR_TYPE;
+    }
     for (int32_t t = 0; t < n; ++t) {
         const uintptr_t p = (uintptr_t)pointers[t];
         if (p == 0) {
+            if (column == kIncomingColumn) continue;       // no incoming gradient for this tensor
             error = "nt_plan_set_pointers: pointer " + std::to_string(t) + " is NULL";
             return NT_ERR_VALUE;
         }

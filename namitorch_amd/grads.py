@@ -46,10 +46,22 @@ def _validate_accumulation(parent: Tensor, gradient) -> None:
             raise RuntimeError("Stored gradients must be detached from autograd.")
 
 
-def accumulate_grads(parameters, gradients) -> None:
+def accumulate_grads(parameters, gradients, *, defer: bool = False) -> None:
     """For each (leaf, incoming gradient): ``leaf.grad`` becomes the incoming
     gradient cast to the leaf's dtype, or has it added in the leaf's dtype.
-    Every pair is validated before anything is written."""
+    Every pair is validated before anything is written.
+
+    ``defer=True`` (the last micro-batch before a step): where the leaf has
+    a gradient of the incoming gradient's dtype (float16, bfloat16 or
+    float32), the addition is recorded instead of launched, and the step's
+    pre-pass and AdamW pass add the incoming values as they read the
+    gradient, which saves writing the sum and reading it back.  Any other
+    read of the gradient adds first, so every observer sees the accumulated
+    values; the version counter advances as for the addition.  The incoming
+    gradients must stay unchanged until then (a RuntimeError names a
+    violation)."""
+    if type(defer) is not bool:
+        raise TypeError("accumulate_grads defer must be a Python bool.")
     parameters = list(parameters)
     gradients = list(gradients)
     if len(parameters) != len(gradients):
@@ -72,19 +84,31 @@ def accumulate_grads(parameters, gradients) -> None:
             rounds.append([])
         rounds[index].append((parameter, gradient))
     for members in rounds:
-        _accumulate_round(members)
+        _accumulate_round(members, defer)
 
 
-def _accumulate_round(members) -> None:
+_DEFERRABLE = ("float16", "bfloat16", "float32")
+
+
+def _deferrable(stored: Tensor, gradient: Tensor) -> bool:
+    """The step's kernels can add `gradient` into `stored` as they read it:
+    same 16/32-bit dtype, and a 16-byte aligned incoming array (so it never
+    breaks the vector path of the stored gradient's plan)."""
+    return (gradient._dtype is stored._dtype and stored._dtype.value in _DEFERRABLE and stored._numel > 0
+            and gradient is not stored and gradient._ptr is not None and gradient._ptr % 16 == 0
+            and gradient._ptr != stored._ptr)
+
+
+def _accumulate_round(members, defer: bool = False) -> None:
     by_backend: dict = {}
     for parameter, gradient in members:
         by_backend.setdefault(get_backend(parameter), []).append((parameter, gradient))
     for backend, pairs in by_backend.items():
         if getattr(backend, "adamw", None) is None:
             backend._unsupported("Gradient accumulation")
-        fresh, existing = [], []
+        fresh, existing, deferred = [], [], []
         for parameter, gradient in pairs:
-            if gradient._pending is not None:
+            if gradient._pending is not None or gradient._incoming is not None:
                 gradient._materialize()
             stored = parameter._grad
             if stored is None:
@@ -93,15 +117,21 @@ def _accumulate_round(members) -> None:
                 parameter._grad = Tensor._from_storage(storage)
                 fresh.append((parameter._grad, gradient))
             else:
-                if stored._pending is not None:
+                if stored._pending is not None or stored._incoming is not None:
                     stored._materialize()
-                existing.append((stored, gradient))
+                if defer and _deferrable(stored, gradient):
+                    deferred.append((stored, gradient))
+                else:
+                    existing.append((stored, gradient))
         if fresh:
             backend.accumulate_tensors([s for s, _ in fresh], [g for _, g in fresh], assign=True)
         if existing:
             backend.accumulate_tensors([s for s, _ in existing], [g for _, g in existing], assign=False)
             for stored, _ in existing:
                 stored._version_counter.increment()
+        for stored, gradient in deferred:
+            stored._incoming = (gradient, gradient._version_counter.value)
+            stored._version_counter.increment()
 
 
 def zero_grads(gradients) -> None:
@@ -116,6 +146,8 @@ def zero_grads(gradients) -> None:
             continue
         by_backend.setdefault(get_backend(gradient), []).append(gradient)
     for backend, members in by_backend.items():
+        for gradient in members:
+            gradient._incoming = None        # overwritten whole: nothing left to add
         backend.zero_tensors(members)
         for gradient in members:
             gradient._pending = None

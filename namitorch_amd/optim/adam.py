@@ -35,7 +35,7 @@ import numpy as np
 from .. import _native
 from ..backends import get_backend
 from ..backends._settings import fused_kernels_enabled
-from ..backends.hip import make_xform
+from ..backends.hip import INCOMING, incoming_pointers, make_xform
 from ..dtype import DType, bfloat16, float16, float32, float64, normalize_dtype
 from ..tensor import Tensor, _assign_host
 from ._common import _FirstOrderOptimizer, _real_option, _round_scalar, _zeros_views
@@ -264,9 +264,18 @@ class Adam(_FirstOrderOptimizer):
             grad_pointers.append(gradient._ptr)
             bookkeeping.append((parameter, state, first, second, master, step, fused, options["lr"] != 0))
         slots = ((_native.AdamWCoefs64 if compute is float64 else _native.AdamWCoefs) * len(records))(*records)
-        plan = backend.plan(rows, layout, chunk=_pass_chunk(layout), pointers={1: grad_pointers})
+        pointers = {1: grad_pointers}
+        # Deferred accumulations (accumulate_grads(..., defer=True)) are added
+        # by the pass as it reads each gradient.
+        addends = incoming_pointers([gradient for _, gradient, _ in members])
+        if addends is not None:
+            pointers[INCOMING] = addends
+        plan = backend.plan(rows, layout, chunk=_pass_chunk(layout), pointers=pointers)
         backend.adamw_multi(plan, slots, None if transform is None else make_xform(transform))
-        self._batches.append((backend, plan, compute, slot_specs, member_slots, bookkeeping))
+        # A plan with an incoming column is not memoized: a replay could
+        # otherwise add the same addends again.
+        self._batches.append((backend, plan, compute, slot_specs, member_slots, bookkeeping) if addends is None
+                             else None)
         device_step = None if transform is None else transform.device
         for parameter, state, first, second, master, step, fused, moves in bookkeeping:
             bumped = not fused or parameter._numel
@@ -290,7 +299,7 @@ class Adam(_FirstOrderOptimizer):
     def _memoize_step(self, options: dict) -> None:
         batches = self.__dict__.pop("_batches", None)
         self._replay = None
-        if batches is None or len(batches) != 1:
+        if batches is None or len(batches) != 1 or batches[0] is None:
             return
         cached = self.__dict__.get("_registered_cache")
         if cached is None:
@@ -466,6 +475,8 @@ class _Replay:
         if tuple(map(_REQUIRES, registered)) != self.requires:
             return False
         current = tuple(map(_GRAD, registered))
+        if any(gradient is not None and gradient._incoming is not None for gradient in current):
+            return False                                        # the full step adds deferred accumulations
         if not all(map(is_, current, self.grads)) and not self._adopt(optimizer, current):
             return False
         state = optimizer.state

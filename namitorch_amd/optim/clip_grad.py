@@ -165,8 +165,9 @@ def _device_groups(gradients) -> dict:
 
 
 def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tuple[GradStats, dict]:
-    """Run the device pre-pass over `gradients` (with their pending unscale)
-    and return the merged statistics; also the per-group control blocks."""
+    """Run the device pre-pass over `gradients` (with their deferred
+    accumulations and pending unscale) and return the merged statistics;
+    also, per (backend, dtype) group, its members, control block and scale."""
     stats = GradStats()
     blocks = {}
     for (backend, dtype), members in _device_groups(gradients).items():
@@ -185,13 +186,13 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
         else:
             transform = next(iter(transforms))
             scale = None if transform is None else transform.scale
-        plan = backend.grad_plan(members, dtype)
+        plan = backend.grad_plan(members, dtype, incoming=True)
         block = backend.new_ctrl()
         backend.grad_prepass(plan, scale)
         backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0)
         ctrl = backend.read_ctrl(block)
         stats.merge(GradStats(ctrl.sumsq, ctrl.amax, bool(ctrl.has_nan), bool(ctrl.found_inf and not ctrl.has_nan)))
-        blocks[(backend, dtype)] = (plan, block, scale)
+        blocks[(backend, dtype)] = (members, block, scale)
     if remember:
         _remember_stats(gradients, stats)
     return stats, blocks
@@ -200,7 +201,8 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
 def _pow_total(blocks, amax: float, order: float) -> float:
     """Sum over gradients of (|g|/amax)^p in float64 (clip_grad.py:73-76)."""
     total = 0.0
-    for (backend, _), (plan, block, scale) in blocks.items():
+    for (backend, dtype), (members, block, scale) in blocks.items():
+        plan = backend.grad_plan(members, dtype)         # deferred accumulations written back first
         ctrl = backend.read_ctrl(block)
         ctrl.amax = amax
         import ctypes

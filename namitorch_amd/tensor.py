@@ -19,6 +19,12 @@ on the gradient as a pending :class:`GradTransform` and fused into the next
 kernel that reads the gradient (the AdamW pass); any other access to
 ``_data`` first writes the transformed values back with a kernel, so every
 observer sees exactly the values the reference would have stored.
+
+Deferred accumulation.  ``accumulate_grads(..., defer=True)`` records the
+last micro-batch's gradient on the stored gradient (``_incoming``) instead
+of adding it; the pre-pass and the AdamW pass add it as they read the
+gradient, and any other access writes the sum back first.  The addition
+comes before a pending transform, as in the reference's order of events.
 """
 
 from __future__ import annotations
@@ -70,6 +76,17 @@ _unsettled_steps: list = []
 def _settle_device_steps() -> None:
     while _unsettled_steps:
         _unsettled_steps[0].reconcile()
+
+
+def check_addends(gradients) -> None:
+    """Raise if the incoming gradient of a deferred accumulation
+    (``accumulate_grads(..., defer=True)``) changed after it was deferred:
+    its values are read only when the accumulation is consumed."""
+    for gradient in gradients:
+        incoming = gradient._incoming
+        if incoming is not None and incoming[0]._version_counter.value != incoming[1]:
+            raise RuntimeError("An incoming gradient of a deferred accumulation was modified in place before the "
+                               "accumulation ran; keep it unchanged until the next step or read of the gradient.")
 
 
 # ---- grad mode (namitorch/autograd.py:15-42) -----------------------------------------
@@ -278,7 +295,8 @@ def _assign_host(target: np.ndarray, source: object, dtype: DType, source_dtype:
 class Tensor:
     __slots__ = (
         "_storage", "_dtype", "_device", "_requires_grad", "_grad", "_version_counter",
-        "_writable", "_pending", "_is_leaf", "_ptr", "_numel", "_clean_version", "_finite_version", "__weakref__",
+        "_writable", "_pending", "_incoming", "_is_leaf", "_ptr", "_numel", "_clean_version", "_finite_version",
+        "__weakref__",
     )
 
     def __init__(self, data: object, dtype: object = None, requires_grad: builtins.bool = False, *, device=None):
@@ -321,6 +339,7 @@ class Tensor:
         self._version_counter = version_counter if version_counter is not None else _VersionCounter()
         self._writable = True
         self._pending = None
+        self._incoming = None
         self._is_leaf = True
         self._clean_version = None      # version at which a state buffer was last known nonnegative
         self._finite_version = None     # version at which GradScaler last knew the gradient's finiteness
@@ -335,12 +354,19 @@ class Tensor:
     # ---- storage access --------------------------------------------------------------
     @property
     def _data(self):
-        if self._pending is not None:
+        if self._pending is not None or self._incoming is not None:
             self._materialize()
         return self._storage
 
     def _materialize(self) -> None:
-        """Write a pending gradient transform back into storage."""
+        """Write a deferred accumulation, then a pending gradient transform,
+        back into storage."""
+        incoming = self._incoming
+        if incoming is not None:
+            check_addends([self])
+            self._incoming = None
+            from .backends import get_backend
+            get_backend(self).accumulate_tensors([self], [incoming[0]], assign=False)
         pending = self._pending
         if pending is None:
             return
@@ -450,6 +476,7 @@ class Tensor:
             raise RuntimeError(f"Operands are on different devices: {self.device}, {value.device}; use an explicit .to() transfer.")
         source = value._data if isinstance(value, Tensor) else value
         self._pending = None
+        self._incoming = None
         if isinstance(self._storage, DeviceArray):
             _assign_device(self._storage, source, self._dtype)
         else:
@@ -566,4 +593,5 @@ def tensor(data: object, dtype: object = None, requires_grad: builtins.bool = Fa
     return Tensor(data, dtype=dtype, requires_grad=requires_grad, device=device)
 
 
-__all__ = ["Tensor", "Parameter", "tensor", "no_grad", "enable_grad", "is_grad_enabled", "GradTransform"]
+__all__ = ["Tensor", "Parameter", "tensor", "no_grad", "enable_grad", "is_grad_enabled", "GradTransform",
+           "check_addends"]

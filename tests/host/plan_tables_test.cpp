@@ -116,8 +116,21 @@ static void test_pointer_columns() {
     CHECK(check_pointer_column(layout, flags, 1, null_ptr, 2, error) == NT_ERR_VALUE);
     CHECK(check_pointer_column(layout, flags, 1, good, 1, error) == NT_ERR_VALUE);   // wrong count
     CHECK(check_pointer_column(layout, flags, 4, good, 2, error) == NT_ERR_VALUE);   // no copy column
-    CHECK(check_pointer_column(layout, flags, 5, good, 2, error) == NT_ERR_VALUE);
+    CHECK(check_pointer_column(layout, flags, 6, good, 2, error) == NT_ERR_VALUE);   // no such column
     CHECK(check_pointer_column(layout, flags, 0, good, 2, error) == NT_ERR_VALUE);   // fp32 param at 2 bytes
+    // Column 5: incoming gradients of the grad dtype; NULL means none.
+    CHECK(check_pointer_column(layout, flags, 5, good, 2, error) == NT_OK);
+    CHECK(check_pointer_column(layout, flags, 5, null_ptr, 2, error) == NT_OK);
+    const void *none[2] = {nullptr, nullptr};
+    CHECK(check_pointer_column(layout, flags, 5, none, 2, error) == NT_OK);
+    CHECK(check_pointer_column(layout, flags, 5, misaligned, 2, error) == NT_ERR_VALUE);
+    CHECK(check_pointer_column(layout, flags, 5, odd, 2, error) == NT_ERR_VALUE);
+    const nt_mt_layout f64{NT_F64, NT_F64, NT_F64, NT_DTYPE_NONE};
+    const void *wide[2] = {ptr(0x10010), ptr(0x20008)};
+    CHECK(check_pointer_column(f64, flags, 1, wide, 2, error) == NT_OK);
+    CHECK(check_pointer_column(f64, flags, 5, wide, 2, error) == NT_ERR_TYPE);    // float64: not supported
+    // Column 5 sits after numel/slot/flags in the descriptor.
+    CHECK(column_offset(5) == offsetof(DevTensor, incoming) && column_offset(5) == 56 && column_offset(4) == 32);
 }
 
 int main() {

@@ -263,8 +263,8 @@ def test_gradient_edges_and_pointer_columns(plans):
         _call("nt_grad_accumulate", grads, 0, _stream())
     fresh = [torch.zeros(4096, dtype=torch.bfloat16, device=DEV), torch.zeros(100, dtype=torch.bfloat16, device=DEV)]
     pointers = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in fresh])
-    for column in (-1, 5):
-        with pytest.raises(ValueError, match="column must be 0..4"):
+    for column in (-1, 6):
+        with pytest.raises(ValueError, match="column must be 0..5"):
             _call("nt_plan_set_pointers", grads, column, pointers, 2, _stream())
     with pytest.raises(ValueError, match="no such column"):
         _call("nt_plan_set_pointers", grads, 2, pointers, 2, _stream())
