@@ -37,6 +37,7 @@ import json
 import math
 import os
 import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -211,6 +212,7 @@ def fresh_gradients(grads):
     The stored (scaled) values stay the same every step."""
     for gradient in grads:
         gradient._pending = None
+        gradient._incoming = None
         gradient._version_counter.value += 1
 
 
@@ -305,6 +307,68 @@ def bench_edges(nt, torch, shapes, steps, warmup):
                             pct_hbm_peak=100 * bytes_per_param * n / ms / 1e6 / HBM_PEAK_GBPS)
         log(f"edges {name}: {ms:.3f} ms")
     del params, incoming, optimizer
+    release(nt, torch)
+    return result
+
+
+def bench_accumulate(nt, torch, steps, warmup, rounds=3):
+    """The C5 step (Llama-7B list, bf16 model + fp32 master, bf16 grads,
+    AMP + clip at 1.0) after a second micro-batch's gradients, three ways,
+    interleaved over `rounds` on the same buffers:
+    - none: the step alone (30 B/param: pre-pass 2, pass 28);
+    - separate: accumulate_grads launch (6 B/param), then the step (36 B/param);
+    - deferred: accumulate_grads(defer=True), the pre-pass and the pass add
+      the incoming gradient as they read (pre-pass 4 + pass 30 = 34 B/param).
+    Each step starts from fresh gradient objects over the same buffers, as
+    a new backward leaves them.  Per mode: the median step of each round."""
+    from namitorch_amd.param_lists import llama7b_shapes, total_params
+    shapes = llama7b_shapes()
+    n = total_params(shapes)
+    params = make_params(nt, torch, shapes, nt.bfloat16)
+    attach_grads(nt, torch, params, nt.bfloat16, scale=65536.0)
+    grads = [p.grad for p in params]
+    generator = torch.Generator(device="cuda").manual_seed(4337)
+    incoming = []
+    for p in params:
+        data = torch.randn(p.shape, generator=generator, device="cuda", dtype=torch.float32).mul_(1e-3 * 8192.0)
+        incoming.append(nt.Tensor._from_storage(data.to(torch.bfloat16).contiguous()))
+        del data
+    loss = nt.Tensor._from_storage(torch.ones((), device="cuda"))
+    optimizer = nt.optim.AdamW(decay_groups(params), lr=3e-4, betas=(0.9, 0.999), eps=1e-8, master_weights=True)
+    scaler = nt.GradScaler(init_scale=65536.0)
+    modes = {"none": 30, "separate": 36, "deferred": 34}
+
+    def one_step(mode):
+        fresh_gradients(grads)
+        if mode != "none":
+            nt.accumulate_grads(params, incoming, defer=mode == "deferred")
+        scaler.scale(loss)
+        nt.amp.fused_step(optimizer, scaler, max_norm=1.0)
+
+    medians = {mode: [] for mode in modes}
+    for _ in range(rounds):
+        for mode in modes:
+            for _ in range(warmup):
+                one_step(mode)
+            marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+            torch.cuda.synchronize()
+            for k in range(steps):
+                marks[k].record()
+                one_step(mode)
+            marks[steps].record()
+            torch.cuda.synchronize()
+            medians[mode].append(median_interval(marks))
+    result = dict(params=n, tensors=len(shapes), rounds=rounds, steps_per_round=steps, scale=scaler.get_scale())
+    for mode, bytes_per_param in modes.items():
+        ms = statistics.median(medians[mode])
+        result[mode] = dict(median_ms_per_step=ms, round_medians_ms=medians[mode], bytes_per_param=bytes_per_param,
+                            GBps=bytes_per_param * n / ms / 1e6,
+                            pct_hbm_peak=100 * bytes_per_param * n / ms / 1e6 / HBM_PEAK_GBPS)
+        log(f"c5 accumulate {mode}: median {ms:.3f} ms/step ({medians[mode]})")
+    result["deferred_vs_separate_speedup"] = result["separate"]["median_ms_per_step"] / result["deferred"]["median_ms_per_step"]
+    for p in params:
+        p._grad = None
+    del params, grads, incoming, optimizer, scaler
     release(nt, torch)
     return result
 
@@ -768,6 +832,9 @@ def main():
     if "chunks" in wanted:
         log("AdamW pass task size: 4096 against 2048 elements, same buffers")
         extra["pass_chunks"] = bench_chunks(nt, torch)
+    if "accum" in wanted:
+        log("c5 after a second micro-batch: separate accumulate launch against the deferred addend")
+        extra["c5_accumulate"] = bench_accumulate(nt, torch, max(5, args.steps // 4), min(args.warmup, 2))
     if "edges" in wanted:
         log("gradient edges: accumulate and zero over the gpt-1.3b list (bf16)")
         extra["grad_edges_gpt1p3b"] = bench_edges(nt, torch, gpt_1p3b_shapes(), max(5, args.steps // 2), args.warmup)

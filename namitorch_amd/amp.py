@@ -60,7 +60,7 @@ class DeviceStep:
         self.records: list = []
         self.optimizers: set = set()
         self.clip_bumps = clip_bumps          # (gradient, version after the optimistic clip bump)
-        self.snapshot = runtime.pinned(ctypes.sizeof(_native.AmpCtrl))
+        self.snapshot = runtime.take_pinned(ctypes.sizeof(_native.AmpCtrl))
         self.event = runtime.Event()
         self._ctrl = None
         self._reconciled = False
@@ -100,6 +100,8 @@ class DeviceStep:
         if self._ctrl is None:
             self.event.synchronize()
             self._ctrl = _native.AmpCtrl.from_buffer_copy(self.snapshot.tobytes())
+            runtime.give_pinned(self.snapshot)       # the copy into it has completed
+            self.snapshot = None
         return self._ctrl
 
     def reconcile(self) -> None:

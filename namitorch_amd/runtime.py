@@ -193,6 +193,28 @@ def pinned(nbytes: int) -> np.ndarray:
     return array
 
 
+# Releasing page-locked memory waits for the whole device, which would stall
+# the host behind every kernel queued so far; buffers that are used once per
+# optimizer step are therefore recycled through this pool.
+_PINNED_KEEP = 64                  # idle buffers kept per size
+_pinned_idle: dict = {}            # size -> idle arrays
+
+
+def take_pinned(nbytes: int) -> np.ndarray:
+    """A page-locked buffer from the pool (or a new one)."""
+    idle = _pinned_idle.get(nbytes)
+    return idle.pop() if idle else pinned(nbytes)
+
+
+def give_pinned(array: np.ndarray) -> None:
+    """Return a buffer of :func:`take_pinned` to the pool.  The caller
+    guarantees that no queued copy still writes or reads it; a buffer never
+    given back is released when it is garbage collected."""
+    idle = _pinned_idle.setdefault(array.nbytes, [])
+    if len(idle) < _PINNED_KEEP:
+        idle.append(array)
+
+
 def memory_stats(device: int = 0) -> dict:
     """Bytes of device memory handed out and held by the library's pool."""
     in_use = ctypes.c_uint64()
