@@ -63,7 +63,8 @@ def parse_args():
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-only", action="store_true", help="only the C2 kernel loop (for profilers)")
     parser.add_argument("--calibrate", action="store_true",
-                        help="with --kernel-only: also run 3 plain 1 GiB device copies (known bytes, for PMC scaling)")
+                        help="with --kernel-only or --profile: also run 3 plain 1 GiB device copies (known bytes, "
+                             "for PMC scaling)")
     parser.add_argument("--profile", default=None, choices=sorted(MIXED),
                         help="only this config's fused step (for profilers): --warmup untimed, --steps timed")
     return parser.parse_args()
@@ -103,6 +104,20 @@ def release(nt, torch):
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     nt.runtime.empty_cache(0)
+
+
+def calibration_copies(torch) -> dict:
+    """Three plain 1 GiB device-to-device copies (known traffic: 1 GiB read
+    and 1 GiB written each), which scale the PMC byte counters."""
+    source = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    target = torch.empty_like(source)
+    for _ in range(3):
+        target.copy_(source)
+    torch.cuda.synchronize()
+    record = {"read": source.numel() * 4, "write": target.numel() * 4, "launches": 3}
+    del source, target
+    torch.cuda.empty_cache()
+    return record
 
 
 def event_pair(torch):
@@ -793,6 +808,8 @@ def main():
         spec = dict(spec, modes=("fused",))
         shapes = spec.pop("shapes")
         log(f"{args.profile} fused step only ({args.warmup} untimed, {args.steps} timed)")
+        if args.calibrate:
+            log(f"calibration copies: {calibration_copies(torch)}")
         print(json.dumps({key: bench_mixed(nt, torch, args.profile, shapes, steps=args.steps, warmup=args.warmup,
                                            **spec)}), flush=True)
         return
@@ -801,12 +818,7 @@ def main():
     log(f"C2: {c2['ms_per_step']:.3f} ms/step, kernel {c2['kernel_ms']:.3f} ms")
     if args.kernel_only:
         if args.calibrate:
-            source = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
-            target = torch.empty_like(source)
-            for _ in range(3):
-                target.copy_(source)
-            torch.cuda.synchronize()
-            c2["calibration_copy_bytes"] = {"read": source.numel() * 4, "write": target.numel() * 4, "launches": 3}
+            c2["calibration_copy_bytes"] = calibration_copies(torch)
         print(json.dumps(c2))
         return
     from namitorch_amd.param_lists import gpt_1p3b_shapes
