@@ -187,9 +187,9 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
             transform = next(iter(transforms))
             scale = None if transform is None else transform.scale
         plan = backend.grad_plan(members, dtype, incoming=True)
-        block = backend.new_ctrl()
+        block = backend.empty_ctrl()                     # written whole by the finalize
         backend.grad_prepass(plan, scale)
-        backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0)
+        backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0, carry_ptr=backend.neutral_ctrl().data_ptr())
         ctrl = backend.read_ctrl(block)
         stats.merge(GradStats(ctrl.sumsq, ctrl.amax, bool(ctrl.has_nan), bool(ctrl.found_inf and not ctrl.has_nan)))
         blocks[(backend, dtype)] = (members, block, scale)
