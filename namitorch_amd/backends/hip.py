@@ -166,6 +166,10 @@ class HIPBackend:
     def ready_for_host(self, array):
         return array
 
+    def supports_float16(self) -> bool:
+        """gfx950 computes float16 natively (backends/cuda/__init__.py:47-53)."""
+        return True
+
     def array(self, value, dtype=None, copy=True, *, non_blocking=False):
         """`value` (host data, a DeviceArray or another framework's device
         array) as a DeviceArray of this device, converted to `dtype`."""
