@@ -261,9 +261,11 @@ int32_t nt_adamw_f32(float *parameter, const float *gradient, float *exp_avg,
  * the per-gradient loops of GradScaler.unscale_/_finite (amp.py:152-192)
  * and _total_norm (optim/clip_grad.py:63-79) with one launch per pass.
  * `chunk` is the elements per workgroup task (0 = default).  The tables
- * are staged in pinned host memory owned by the plan and copied
- * asynchronously on `stream`, so creation does not wait for queued work.
- * nt_plan_destroy() waits for the device before freeing.
+ * live in memory of the library's pools and are staged in page-locked host
+ * memory, copied asynchronously on `stream`, so creation does not wait for
+ * queued work.  nt_plan_destroy() does not wait either: the plan's memory
+ * returns to the pools in the order of every stream the plan was used on
+ * (those streams must still exist when the plan is destroyed).
  */
 int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
                        const nt_mt_layout *layout, int64_t chunk,

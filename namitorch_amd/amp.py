@@ -96,6 +96,19 @@ class DeviceStep:
             self.event.record(side.handle)
             self.block.record_stream(side.handle)    # not reused before the copy has read it
 
+    def __del__(self):
+        # A step dropped before its snapshot was read: wait for the copy into
+        # the page-locked buffer (it ran right after the finalize), then
+        # return the buffer to the pool rather than free it, which would wait
+        # for the whole device.
+        try:
+            if self.snapshot is not None and not _native.shutting_down():
+                self.event.synchronize()
+                runtime.give_pinned(self.snapshot)
+                self.snapshot = None
+        except Exception:
+            pass
+
     def ctrl(self) -> _native.AmpCtrl:
         if self._ctrl is None:
             self.event.synchronize()

@@ -45,12 +45,11 @@ class _Block:
         self.device = device
 
     def __del__(self):
-        ptr = getattr(self, "ptr", None)
-        if ptr and not _native.shutting_down():
-            try:
-                _native.load().nt_free(ptr)
-            except Exception:
-                pass
+        try:                           # module globals may already be gone at interpreter exit
+            if self.ptr and not _native.shutting_down():
+                _native.load().nt_free(self.ptr)
+        except Exception:
+            pass
 
 
 def _numel(shape) -> int:

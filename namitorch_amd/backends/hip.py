@@ -52,11 +52,14 @@ def _release_plans() -> None:
 class Plan:
     """A multi-tensor plan owned by the library; destroyed with this object."""
 
-    __slots__ = ("handle", "numel", "ntensors", "ntasks", "layout", "columns", "__weakref__")
+    __slots__ = ("handle", "numel", "ntensors", "ntasks", "layout", "columns", "stream_owner", "__weakref__")
 
-    def __init__(self, handle: int, layout: tuple):
+    def __init__(self, handle: int, layout: tuple, stream_owner=None):
         self.handle = handle
         self.layout = layout
+        # Destroying the plan records events on the streams it was used on:
+        # a stream object created here stays alive as long as the plan.
+        self.stream_owner = stream_owner
         self.columns: dict = {}       # volatile column -> pointers it currently holds
         numel = ctypes.c_uint64()
         tensors = ctypes.c_int32()
@@ -254,7 +257,7 @@ class HIPBackend:
             handle = ctypes.c_void_p()
             with self.context():
                 _native.call("nt_plan_create", self.device.index, table, len(full), ctypes.byref(spec), chunk, stream, ctypes.byref(handle))
-            plan = Plan(handle.value, layout)
+            plan = Plan(handle.value, layout, runtime.current_stream_owner(self.device.index))
             plan.columns = {column: tuple(values) for column, values in in_rows.items()}
             if INCOMING in (pointers or {}) and not self._refresh_locked(plan, {INCOMING: pointers[INCOMING]}, stream):
                 raise ValueError("Incoming gradients must be 16-byte aligned.")

@@ -381,6 +381,7 @@ int32_t nt_adamw_mt(nt_plan *plan, const void *slots, int32_t nslots, const nt_g
     const nt_mt_layout &L = plan->layout;
     if ((rc = check_mt_layout(L)) != NT_OK) return rc;
     if (plan->ntasks == 0) return NT_OK;
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;

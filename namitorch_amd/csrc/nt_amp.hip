@@ -847,6 +847,7 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale, const nt_amp
     if (rc != NT_OK) return rc;
     if (unscale && ctrl == nullptr && !(scale > 0.0f && __builtin_isfinite(scale)))
         return fail(NT_ERR_VALUE, "loss scale must be finite and positive");
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     nt_grad_xform hx{};
@@ -888,6 +889,7 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *car
     if ((flags & NT_FINALIZE_SCALER_UPDATE) &&
         (growth_interval <= 0 || !(growth_factor > 1.0) || !(backoff_factor > 0.0 && backoff_factor < 1.0)))
         return fail(NT_ERR_VALUE, "invalid GradScaler growth/backoff settings");
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     const Partial *src = plan->nstage2 > 0 ? plan->d_partials2 : plan->d_partials;
@@ -911,6 +913,7 @@ int32_t nt_grad_norm_pow(nt_plan *plan, nt_amp_ctrl *ctrl, double norm_type, dou
     if (flags & ~NT_NORM_POW_GUARD) return fail(NT_ERR_VALUE, "nt_grad_norm_pow: unknown flags");
     const int32_t guard_on = (flags & NT_NORM_POW_GUARD) ? 1 : 0;
     if (guard_on && norm_type != 2.0) return fail(NT_ERR_VALUE, "nt_grad_norm_pow: the guard applies to norm_type 2 only");
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     nt_grad_xform hx{};
@@ -944,6 +947,7 @@ int32_t nt_grad_apply(nt_plan *plan, const nt_grad_xform *xform, void *stream) {
     if (rc != NT_OK) return rc;
     if ((rc = check_no_incoming(plan, "nt_grad_apply")) != NT_OK) return rc;
     if (xform == nullptr || plan->ntasks == 0) return NT_OK;
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     Xform xf = make_xform(xform);

@@ -189,6 +189,7 @@ int32_t nt_grad_zero(nt_plan *plan, void *stream) {
     if (rc != NT_OK) return rc;
     if ((rc = check_no_incoming(plan, "nt_grad_zero")) != NT_OK) return rc;
     if (plan->ntasks == 0) return NT_OK;
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
@@ -211,6 +212,7 @@ int32_t nt_grad_accumulate(nt_plan *plan, int32_t assign, void *stream) {
     const int32_t dst = plan->layout.grad_dtype, src = plan->layout.param_dtype;
     if (src == NT_DTYPE_NONE) return fail(NT_ERR_VALUE, "nt_grad_accumulate: the plan has no incoming gradients");
     if (plan->ntasks == 0) return NT_OK;
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;

@@ -39,6 +39,12 @@ struct nt_plan {
     // and nt_adamw_mt (16/32-bit gradients) read that column; every other
     // entry point refuses such a plan rather than ignore the addend.
     int32_t n_incoming;
+    // Streams the plan has been used on: the creation stream and any other
+    // stream passed to an entry point with this plan.  Its memory returns to
+    // the library's pools in their order when the plan is destroyed.
+    hipStream_t stream;
+    std::vector<hipStream_t> others;
+    uint64_t host_bytes;         // h_staging and h_ring share one page-locked buffer of this size
 };
 
 namespace nt {
@@ -102,8 +108,25 @@ class DeviceGuard {
 // Device-side transform parameters from a host nt_grad_xform (ctrl ignored).
 Xform make_xform(const nt_grad_xform *x);
 
+// The library's caching pools (nt_pool.hpp) over HIP; they live until the process ends.
+class PoolOps;
+class DevicePool;
+class HostPool;
+PoolOps &hip_pool_ops();
+DevicePool &device_pool();
+HostPool &host_pool();
+
 // Validate a plan pointer.
 int32_t check_plan(const nt_plan *plan);
+
+// Remember that `stream` uses `plan` (see nt_plan::others).
+inline void note_stream(nt_plan *plan, void *stream) {
+    const hipStream_t s = (hipStream_t)stream;
+    if (s == plan->stream) return;
+    for (hipStream_t known : plan->others)
+        if (known == s) return;
+    plan->others.push_back(s);
+}
 // NT_ERR_VALUE (naming `entry`) when the plan has incoming gradients set.
 int32_t check_no_incoming(const nt_plan *plan, const char *entry);
 

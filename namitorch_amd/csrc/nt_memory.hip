@@ -4,86 +4,94 @@
 // backends/_cuda_execution.py, backends/cuda/__init__.py:87-153); here they
 // are the library's own.
 //
-// Allocation is a per-device caching pool ordered by streams, the way CuPy's
-// and PyTorch's pools work: a block is allocated on a stream; freeing it
-// returns it to the pool for reuse by later allocations on that same stream,
-// which stream order already places after every use queued on it.  A block
-// used on other streams as well (nt_record_stream) is reused only after an
-// event recorded on each of those streams at free time has completed.
-// Blocks are never handed across streams, so the pool never synchronizes.
+// Memory comes from the stream-ordered caching pools of nt_pool.hpp, with
+// HIP as their device services.  The pools live until the process ends
+// (they are never destroyed, so no HIP call runs during static teardown).
 #include <hip/hip_runtime.h>
 
-#include <map>
-#include <mutex>
-#include <unordered_map>
-#include <vector>
-
 #include "nt_internal.hpp"
+#include "nt_pool.hpp"
 
 namespace nt {
 namespace {
 
-constexpr uint64_t kSmallRound = 512;                  // blocks up to 1 MiB: 512-byte steps
-constexpr uint64_t kLargeRound = uint64_t(2) << 20;    // larger blocks: 2 MiB steps
-constexpr uint64_t kSmallLimit = uint64_t(1) << 20;
-
-struct Block {
-    void *ptr = nullptr;
-    uint64_t size = 0;
-    int32_t device = 0;
-    hipStream_t stream = nullptr;                       // allocation stream: reuse happens only on it
-    std::vector<hipStream_t> also_used;                 // streams recorded with nt_record_stream
-    std::vector<hipEvent_t> pending;                    // events to complete before reuse
-};
-
-struct Pool {
-    std::multimap<uint64_t, Block *> free_blocks;       // by size
-    uint64_t reserved = 0;                              // bytes obtained from hipMalloc
-    uint64_t in_use = 0;                                // bytes handed out
-};
-
-std::mutex g_lock;
-std::map<int32_t, Pool> g_pools;
-std::unordered_map<void *, Block *> g_live;
-
-uint64_t rounded(uint64_t bytes) {
-    if (bytes == 0) bytes = 1;
-    const uint64_t step = bytes <= kSmallLimit ? kSmallRound : kLargeRound;
-    return (bytes + step - 1) / step * step;
-}
-
-// True when every pending event of a free block has completed (those events
-// are then released).
-bool settled(Block *b) {
-    for (size_t k = 0; k < b->pending.size(); ++k) {
-        const hipError_t status = hipEventQuery(b->pending[k]);
-        if (status == hipErrorNotReady) return false;
-        if (status != hipSuccess) (void)hipGetLastError();
-    }
-    for (hipEvent_t e : b->pending) (void)hipEventDestroy(e);
-    b->pending.clear();
-    return true;
-}
-
-// Release every free block of `pool` that has settled (after a device-wide wait).
-void trim(int32_t device, Pool &pool) {
-    (void)hipDeviceSynchronize();
-    for (auto it = pool.free_blocks.begin(); it != pool.free_blocks.end();) {
-        Block *b = it->second;
-        if (settled(b)) {
-            (void)hipFree(b->ptr);
-            pool.reserved -= b->size;
-            delete b;
-            it = pool.free_blocks.erase(it);
-        } else {
-            ++it;
+class HipOps final : public PoolOps {
+  public:
+    int device_alloc(int32_t device, uint64_t bytes, void **out, std::string &error) override {
+        DeviceGuard guard(device);
+        if (!guard.ok()) {
+            error = "hipSetDevice failed";
+            return -1;
         }
+        const hipError_t status = hipMalloc(out, bytes);
+        if (status == hipSuccess) return 0;
+        (void)hipGetLastError();
+        error = std::string("hipMalloc: ") + hipGetErrorName(status);
+        return (status == hipErrorOutOfMemory || status == hipErrorMemoryAllocation) ? 1 : -1;
     }
-    (void)hipGetLastError();
-    (void)device;
-}
+    void device_free(int32_t device, void *ptr) override {
+        DeviceGuard guard(device);
+        if (hipFree(ptr) != hipSuccess) (void)hipGetLastError();
+    }
+    int host_alloc(uint64_t bytes, void **out, std::string &error) override {
+        const hipError_t status = hipHostMalloc(out, bytes, hipHostMallocDefault);
+        if (status == hipSuccess) return 0;
+        (void)hipGetLastError();
+        error = std::string("hipHostMalloc: ") + hipGetErrorName(status);
+        return -1;
+    }
+    void host_free(void *ptr) override {
+        if (hipHostFree(ptr) != hipSuccess) (void)hipGetLastError();
+    }
+    void *event_record(int32_t device, void *stream) override {
+        DeviceGuard guard(device);
+        hipEvent_t event = nullptr;
+        if (hipEventCreateWithFlags(&event, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        if (hipEventRecord(event, (hipStream_t)stream) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipEventDestroy(event);
+            return nullptr;
+        }
+        return event;
+    }
+    bool event_done(void *event) override {
+        const hipError_t status = hipEventQuery((hipEvent_t)event);
+        if (status == hipErrorNotReady) {
+            (void)hipGetLastError();
+            return false;
+        }
+        if (status != hipSuccess) (void)hipGetLastError();   // a failed event cannot guard anything
+        return true;
+    }
+    void event_destroy(void *event) override {
+        if (hipEventDestroy((hipEvent_t)event) != hipSuccess) (void)hipGetLastError();
+    }
+    void device_synchronize(int32_t device) override {
+        DeviceGuard guard(device);
+        if (hipDeviceSynchronize() != hipSuccess) (void)hipGetLastError();
+    }
+};
 
 }  // namespace
+
+PoolOps &hip_pool_ops() {
+    static HipOps *ops = new HipOps();       // never destroyed
+    return *ops;
+}
+
+DevicePool &device_pool() {
+    static DevicePool *pool = new DevicePool(hip_pool_ops());
+    return *pool;
+}
+
+HostPool &host_pool() {
+    static HostPool *pool = new HostPool(hip_pool_ops());
+    return *pool;
+}
+
 
 // ---- element kernels: fill a bit pattern, cast between float types ------------------
 __global__ __launch_bounds__(kBlock) void fill_pattern_kernel(uint8_t *out, uint64_t count, int32_t itemsize,
@@ -136,110 +144,35 @@ extern "C" {
 // ---- memory -------------------------------------------------------------------------
 int32_t nt_malloc(int32_t device, uint64_t bytes, void *stream, void **out) {
     clear_error();
-    if (out == nullptr) return fail(NT_ERR_VALUE, "nt_malloc: output pointer is NULL");
-    if (device < 0) return fail(NT_ERR_VALUE, "nt_malloc: invalid device");
-    *out = nullptr;
-    const uint64_t size = rounded(bytes);
-    hipStream_t s = (hipStream_t)stream;
-    std::lock_guard<std::mutex> lock(g_lock);
-    Pool &pool = g_pools[device];
-    // Smallest free block of this stream that fits and wastes at most half of itself.
-    for (auto it = pool.free_blocks.lower_bound(size); it != pool.free_blocks.end() && it->first <= 2 * size; ++it) {
-        Block *b = it->second;
-        if (b->device != device || b->stream != s || !settled(b)) continue;
-        pool.free_blocks.erase(it);
-        b->also_used.clear();
-        g_live[b->ptr] = b;
-        pool.in_use += b->size;
-        *out = b->ptr;
-        return NT_OK;
-    }
-    DeviceGuard guard(device);
-    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
-    void *ptr = nullptr;
-    hipError_t status = hipMalloc(&ptr, size);
-    if (status == hipErrorOutOfMemory || status == hipErrorMemoryAllocation) {
-        (void)hipGetLastError();
-        trim(device, pool);
-        status = hipMalloc(&ptr, size);
-    }
-    if (status != hipSuccess)
-        return hip_check(status, ("hipMalloc(" + std::to_string(size) + " bytes; " + std::to_string(pool.in_use) +
-                                  " in use, " + std::to_string(pool.reserved) + " reserved)").c_str());
-    Block *b = new Block;
-    b->ptr = ptr;
-    b->size = size;
-    b->device = device;
-    b->stream = s;
-    g_live[ptr] = b;
-    pool.reserved += size;
-    pool.in_use += size;
-    *out = ptr;
-    return NT_OK;
+    std::string error;
+    const int32_t rc = device_pool().allocate(device, bytes, stream, out, error);
+    return rc == NT_OK ? NT_OK : fail(rc, error);
 }
 
 int32_t nt_record_stream(void *ptr, void *stream) {
     clear_error();
-    std::lock_guard<std::mutex> lock(g_lock);
-    auto it = g_live.find(ptr);
-    if (it == g_live.end()) return fail(NT_ERR_VALUE, "nt_record_stream: not a live allocation of this library");
-    Block *b = it->second;
-    hipStream_t s = (hipStream_t)stream;
-    if (s != b->stream) {
-        for (hipStream_t known : b->also_used)
-            if (known == s) return NT_OK;
-        b->also_used.push_back(s);
-    }
-    return NT_OK;
+    std::string error;
+    const int32_t rc = device_pool().record(ptr, stream, error);
+    return rc == NT_OK ? NT_OK : fail(rc, error);
 }
 
 int32_t nt_free(void *ptr) {
     clear_error();
-    if (ptr == nullptr) return NT_OK;
-    std::lock_guard<std::mutex> lock(g_lock);
-    auto it = g_live.find(ptr);
-    if (it == g_live.end()) return fail(NT_ERR_VALUE, "nt_free: not a live allocation of this library");
-    Block *b = it->second;
-    g_live.erase(it);
-    Pool &pool = g_pools[b->device];
-    pool.in_use -= b->size;
-    if (!b->also_used.empty()) {
-        DeviceGuard guard(b->device);
-        for (hipStream_t other : b->also_used) {
-            hipEvent_t e = nullptr;
-            if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess ||
-                hipEventRecord(e, other) != hipSuccess) {
-                // Cannot track the other stream: keep the block out of the pool.
-                (void)hipGetLastError();
-                if (e) (void)hipEventDestroy(e);
-                for (hipEvent_t p : b->pending) (void)hipEventDestroy(p);
-                pool.reserved -= b->size;
-                delete b;          // leaked on purpose: its memory may still be read
-                return NT_OK;
-            }
-            b->pending.push_back(e);
-        }
-        b->also_used.clear();
-    }
-    pool.free_blocks.emplace(b->size, b);
-    return NT_OK;
+    std::string error;
+    const int32_t rc = device_pool().release(ptr, error);
+    return rc == NT_OK ? NT_OK : fail(rc, error);
 }
 
 int32_t nt_memory_stats(int32_t device, uint64_t *in_use, uint64_t *reserved) {
     clear_error();
-    std::lock_guard<std::mutex> lock(g_lock);
-    const Pool &pool = g_pools[device];
-    if (in_use) *in_use = pool.in_use;
-    if (reserved) *reserved = pool.reserved;
+    device_pool().stats(device, in_use, reserved);
     return NT_OK;
 }
 
 int32_t nt_empty_cache(int32_t device) {
     clear_error();
-    std::lock_guard<std::mutex> lock(g_lock);
-    DeviceGuard guard(device);
-    if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
-    trim(device, g_pools[device]);
+    if (device < 0) return fail(NT_ERR_VALUE, "nt_empty_cache: invalid device");
+    device_pool().trim(device);
     return NT_OK;
 }
 

@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "nt_internal.hpp"
+#include "nt_pool.hpp"
 #include "nt_tables.hpp"
 
 namespace nt {
@@ -185,36 +186,50 @@ int32_t nt_plan_create(int32_t device, const nt_mt_tensor *tensors, int32_t n,
     plan->flags.reserve((size_t)n);
     for (int32_t t = 0; t < n; ++t) plan->flags.push_back(host[(size_t)t].flags);
 
+    hipStream_t s = (hipStream_t)stream;
+    plan->stream = s;
+    // Device tables from the library's pool (ordered on the creation
+    // stream); the staging copy of the tables and the pointer ring share
+    // one page-locked buffer from the host pool.
     auto cleanup = [&](int32_t rc) {
+        (void)hipStreamSynchronize(s);     // nothing queued may still read what is returned below
+        std::string ignored;
+        for (void *block : {(void *)plan->d_tensors, (void *)plan->d_tasks, (void *)plan->d_partials,
+                            (void *)plan->d_partials2, (void *)plan->d_pow_partials})
+            if (block) (void)device_pool().release(block, ignored);
         for (int r = 0; r < kRingSlots; ++r)
             if (plan->ring_events[r]) (void)hipEventDestroy(plan->ring_events[r]);
-        if (plan->h_ring) (void)hipHostFree(plan->h_ring);
-        if (plan->d_tensors) (void)hipFree(plan->d_tensors);
-        if (plan->d_tasks) (void)hipFree(plan->d_tasks);
-        if (plan->d_partials) (void)hipFree(plan->d_partials);
-        if (plan->d_partials2) (void)hipFree(plan->d_partials2);
-        if (plan->d_pow_partials) (void)hipFree(plan->d_pow_partials);
-        if (plan->h_staging) (void)hipHostFree(plan->h_staging);
+        if (plan->h_staging) host_pool().give(plan->h_staging, plan->host_bytes, {});
         delete plan;
         (void)hipGetLastError();
         return rc;
     };
     const size_t tensor_bytes = host.size() * sizeof(DevTensor);
     const size_t task_bytes = (tasks.empty() ? 1 : tasks.size()) * sizeof(Task);
+    const size_t ring_bytes = (size_t)kRingSlots * host.size() * sizeof(void *);
+    auto take = [&](void **out, size_t bytes, const char *what) {
+        const int32_t code = device_pool().allocate(device, bytes, stream, out, error);
+        return code == NT_OK ? NT_OK : fail(code, std::string(what) + ": " + error);
+    };
     int32_t rc;
-    if ((rc = hip_check(hipMalloc((void **)&plan->d_tensors, tensor_bytes), "hipMalloc(plan tensors)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipMalloc((void **)&plan->d_tasks, task_bytes), "hipMalloc(plan tasks)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipMalloc((void **)&plan->d_partials, (size_t)plan->npartials * sizeof(Partial)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipMalloc((void **)&plan->d_partials2, (size_t)(plan->nstage2 > 0 ? plan->nstage2 : 1) * sizeof(Partial)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipMalloc((void **)&plan->d_pow_partials, (size_t)plan->pow_grid * sizeof(double)), "hipMalloc(plan partials)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipHostMalloc(&plan->h_staging, tensor_bytes + task_bytes, hipHostMallocDefault), "hipHostMalloc(plan staging)")) != NT_OK) return cleanup(rc);
-    if ((rc = hip_check(hipHostMalloc(&plan->h_ring, (size_t)kRingSlots * host.size() * sizeof(void *), hipHostMallocDefault), "hipHostMalloc(plan ring)")) != NT_OK) return cleanup(rc);
+    if ((rc = take((void **)&plan->d_tensors, tensor_bytes, "plan tensors")) != NT_OK) return cleanup(rc);
+    if ((rc = take((void **)&plan->d_tasks, task_bytes, "plan tasks")) != NT_OK) return cleanup(rc);
+    if ((rc = take((void **)&plan->d_partials, (size_t)plan->npartials * sizeof(Partial), "plan partials")) != NT_OK)
+        return cleanup(rc);
+    if ((rc = take((void **)&plan->d_partials2, (size_t)(plan->nstage2 > 0 ? plan->nstage2 : 1) * sizeof(Partial),
+                   "plan partials")) != NT_OK)
+        return cleanup(rc);
+    if ((rc = take((void **)&plan->d_pow_partials, (size_t)plan->pow_grid * sizeof(double), "plan partials")) != NT_OK)
+        return cleanup(rc);
+    plan->host_bytes = tensor_bytes + task_bytes + ring_bytes;
+    if (host_pool().take(plan->host_bytes, &plan->h_staging, error) != NT_OK)
+        return cleanup(fail(NT_ERR_HIP, "plan staging: " + error));
+    plan->h_ring = static_cast<char *>(plan->h_staging) + tensor_bytes + task_bytes;
     for (int r = 0; r < kRingSlots; ++r)
         if ((rc = hip_check(hipEventCreateWithFlags(&plan->ring_events[r], hipEventDisableTiming), "hipEventCreate(plan ring)")) != NT_OK) return cleanup(rc);
     char *staging = static_cast<char *>(plan->h_staging);
     std::memcpy(staging, host.data(), tensor_bytes);
     if (!tasks.empty()) std::memcpy(staging + tensor_bytes, tasks.data(), tasks.size() * sizeof(Task));
-    hipStream_t s = (hipStream_t)stream;
     if ((rc = hip_check(hipMemcpyAsync(plan->d_tensors, staging, tensor_bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync(plan tensors)")) != NT_OK) return cleanup(rc);
     if (!tasks.empty() &&
         (rc = hip_check(hipMemcpyAsync(plan->d_tasks, staging + tensor_bytes, tasks.size() * sizeof(Task), hipMemcpyHostToDevice, s), "hipMemcpyAsync(plan tasks)")) != NT_OK)
@@ -227,16 +242,32 @@ int32_t nt_plan_destroy(nt_plan *plan) {
     clear_error();
     if (plan == nullptr) return NT_OK;
     DeviceGuard guard(plan->device);
-    // Kernels queued with this plan may still read its tables.
-    (void)hipDeviceSynchronize();
-    (void)hipFree(plan->d_tensors);
-    (void)hipFree(plan->d_tasks);
-    (void)hipFree(plan->d_partials);
-    (void)hipFree(plan->d_partials2);
-    (void)hipFree(plan->d_pow_partials);
-    (void)hipHostFree(plan->h_staging);
+    // Kernels queued with this plan may still read its tables: the device
+    // blocks return to the pool in the order of every stream that used the
+    // plan, and the page-locked buffer once each of those streams has passed
+    // this point.  Nothing waits here.
+    std::string ignored;
+    for (void *block : {(void *)plan->d_tensors, (void *)plan->d_tasks, (void *)plan->d_partials,
+                        (void *)plan->d_partials2, (void *)plan->d_pow_partials}) {
+        if (block == nullptr) continue;
+        for (hipStream_t other : plan->others) (void)device_pool().record(block, other, ignored);
+        (void)device_pool().release(block, ignored);
+    }
+    std::vector<void *> after;
+    bool tracked = true;
+    for (size_t k = 0; k <= plan->others.size() && tracked; ++k) {
+        void *event = hip_pool_ops().event_record(plan->device, k == 0 ? plan->stream : plan->others[k - 1]);
+        if (event == nullptr) tracked = false;
+        else after.push_back(event);
+    }
+    if (!tracked) {
+        // A stream could not be tracked: wait for the device instead.
+        for (void *event : after) hip_pool_ops().event_destroy(event);
+        after.clear();
+        (void)hipDeviceSynchronize();
+    }
+    host_pool().give(plan->h_staging, plan->host_bytes, std::move(after));
     for (int r = 0; r < kRingSlots; ++r) (void)hipEventDestroy(plan->ring_events[r]);
-    (void)hipHostFree(plan->h_ring);
     delete plan;
     (void)hipGetLastError();   // teardown is best effort; leave no error for a later launch check
     return NT_OK;
@@ -250,6 +281,7 @@ int32_t nt_plan_set_pointers(nt_plan *plan, int32_t column, const void *const *p
     std::string error;
     rc = check_pointer_column(plan->layout, plan->flags, column, pointers, n, error);
     if (rc != NT_OK) return fail(rc, error);
+    note_stream(plan, stream);
     DeviceGuard guard(plan->device);
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     // The slot's previous upload must have left it before it is rewritten.

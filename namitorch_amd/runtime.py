@@ -53,11 +53,19 @@ def current_stream(device: int) -> int:
     thread's current stream on `device`."""
     stack = _stacks().get(device)
     if stack:
-        return stack[-1]
+        return stack[-1][0]
     provider = _provider
     if provider is not None:
         return int(provider(device) or 0)
     return 0
+
+
+def current_stream_owner(device: int):
+    """The :class:`Stream` object behind the current stream of `device` when
+    a ``with stream(Stream)`` block selected it, else None.  Holders of
+    library objects bound to a stream (plans) keep it alive with this."""
+    stack = _stacks().get(device)
+    return stack[-1][1] if stack else None
 
 
 @contextmanager
@@ -115,11 +123,11 @@ class Stream:
         return hash(self.handle)
 
     def __del__(self):
-        if getattr(self, "_owned", False) and self.handle and not _native.shutting_down():
-            try:
+        try:                           # module globals may already be gone at interpreter exit
+            if self._owned and self.handle and not _native.shutting_down():
                 _native.load().nt_stream_destroy(self.handle)
-            except Exception:
-                pass
+        except Exception:
+            pass
 
 
 @contextmanager
@@ -127,11 +135,11 @@ def stream(selected):
     """Make `selected` (a Stream, or ``(handle, device)``) the calling thread's
     current stream of its device inside the block."""
     if isinstance(selected, Stream):
-        handle, device = selected.handle, selected.device
+        handle, device, owner = selected.handle, selected.device, selected
     else:
-        handle, device = int(selected[0] or 0), int(selected[1])
+        handle, device, owner = int(selected[0] or 0), int(selected[1]), None
     stack = _stacks().setdefault(device, [])
-    stack.append(handle)
+    stack.append((handle, owner))
     try:
         yield selected
     finally:
@@ -166,19 +174,19 @@ class Event:
         return float(milliseconds.value)
 
     def __del__(self):
-        if getattr(self, "handle", None) and not _native.shutting_down():
-            try:
+        try:                           # module globals may already be gone at interpreter exit
+            if self.handle and not _native.shutting_down():
                 _native.load().nt_event_destroy(self.handle)
-            except Exception:
-                pass
+        except Exception:
+            pass
 
 
 def _release_host(address: int) -> None:
-    if not _native.shutting_down():
-        try:
+    try:                               # module globals may already be gone at interpreter exit
+        if not _native.shutting_down():
             _native.load().nt_host_free(address)
-        except Exception:
-            pass
+    except Exception:
+        pass
 
 
 def pinned(nbytes: int) -> np.ndarray:
@@ -228,5 +236,5 @@ def empty_cache(device: int = 0) -> None:
     _native.call("nt_empty_cache", device)
 
 
-__all__ = ["Stream", "Event", "stream", "current_stream", "set_stream_provider", "pinned", "memory_stats",
-           "empty_cache"]
+__all__ = ["Stream", "Event", "stream", "current_stream", "current_stream_owner", "set_stream_provider", "pinned",
+           "take_pinned", "give_pinned", "memory_stats", "empty_cache", "device_scope"]

@@ -1,5 +1,6 @@
-"""Host unit test of the C++ plan-table builder, compiled with g++ under
-AddressSanitizer and UndefinedBehaviorSanitizer (no GPU involved)."""
+"""Host unit tests of the library's plain C++ parts — the plan-table builder
+and the caching memory pools — compiled with g++ under AddressSanitizer and
+UndefinedBehaviorSanitizer (no GPU involved)."""
 
 from __future__ import annotations
 
@@ -12,13 +13,12 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 
 
-@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ is not installed")
-def test_plan_tables_under_sanitizers(tmp_path):
-    binary = tmp_path / "plan_tables_test"
+def _run_sanitized(tmp_path, test_source: str, library_source: str) -> None:
+    binary = tmp_path / Path(test_source).stem
     compile_cmd = ["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
                    "-fno-sanitize-recover=undefined", "-Wall", "-Wextra", "-Werror",
-                   str(ROOT / "tests" / "host" / "plan_tables_test.cpp"),
-                   str(ROOT / "namitorch_amd" / "csrc" / "nt_tables.cpp"), "-o", str(binary)]
+                   str(ROOT / "tests" / "host" / test_source),
+                   str(ROOT / "namitorch_amd" / "csrc" / library_source), "-o", str(binary)]
     built = subprocess.run(compile_cmd, capture_output=True, text=True)
     assert built.returncode == 0, built.stderr
     ran = subprocess.run([str(binary)], capture_output=True, text=True, timeout=60,
@@ -26,3 +26,13 @@ def test_plan_tables_under_sanitizers(tmp_path):
     assert ran.returncode == 0, ran.stdout + ran.stderr
     assert "all checks passed" in ran.stdout
     assert "runtime error" not in ran.stderr and "AddressSanitizer" not in ran.stderr
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ is not installed")
+def test_plan_tables_under_sanitizers(tmp_path):
+    _run_sanitized(tmp_path, "plan_tables_test.cpp", "nt_tables.cpp")
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ is not installed")
+def test_memory_pools_under_sanitizers(tmp_path):
+    _run_sanitized(tmp_path, "pool_test.cpp", "nt_pool.cpp")
