@@ -34,6 +34,8 @@ class CPUBackend:
 
     device = _CPU
     array_type = np.ndarray
+    module = np
+    namespace = np
     adamw = None
 
     def _unsupported(self, what: str):
@@ -125,6 +127,12 @@ def get_backend(value=None):
         return _backends[target]
 
 
+def namespace(value=None):
+    """The array namespace of `value`'s backend (backends/__init__.py:79-80):
+    NumPy on the host, ``HIPNamespace`` on a HIP device."""
+    return get_backend(value).namespace
+
+
 def ensure_same_device(*values, _active=None):
     active = set() if _active is None else _active
     devices = []
@@ -177,5 +185,5 @@ def readonly(array):
     return get_backend(array).readonly(array)
 
 
-__all__ = ["get_backend", "ensure_same_device", "same_device", "transfer", "is_array", "array_device",
+__all__ = ["get_backend", "namespace", "ensure_same_device", "same_device", "transfer", "is_array", "array_device",
            "enable_fused_kernels", "fused_kernels_enabled", "CPUBackend"]

@@ -31,7 +31,7 @@ import numpy as np
 from .. import _native, runtime
 from ..array import DeviceArray
 from ..device import Device
-from ..dtype import float32, int32, uint8
+from ..dtype import float32, int32, normalize_dtype, uint8
 
 PLAN_CACHE_SIZE = 16
 INCOMING = 5          # plan pointer column of deferred incoming gradients
@@ -138,6 +138,64 @@ class AdamWHIPKernel:
         return True
 
 
+class HIPNamespace:
+    """The backend's array namespace (the reference's ``backend.namespace``,
+    backends/_namespace.py), for the array constructors and copies a caller
+    of this path needs: ``zeros``, ``zeros_like``, ``empty``, ``empty_like``,
+    ``asarray``/``array``, ``copyto`` and ``errstate``.  Array arithmetic is
+    not offered: the optimizer step's arithmetic runs in the library's
+    kernels, and other names raise RuntimeError, as the reference's
+    namespace does for a primitive CuPy lacks (there is no CPU fallback)."""
+
+    def __init__(self, backend: "HIPBackend"):
+        self._backend = backend
+
+    def zeros(self, shape, dtype=float32):
+        with self._backend.context():
+            return DeviceArray.zeros(_shape(shape), dtype, self._backend.device)
+
+    def empty(self, shape, dtype=float32):
+        with self._backend.context():
+            return DeviceArray.empty(_shape(shape), dtype, self._backend.device)
+
+    def zeros_like(self, array, dtype=None):
+        array = DeviceArray.wrap(array)
+        return self.zeros(array.shape, array.dtype if dtype is None else normalize_dtype(dtype))
+
+    def empty_like(self, array, dtype=None):
+        array = DeviceArray.wrap(array)
+        return self.empty(array.shape, array.dtype if dtype is None else normalize_dtype(dtype))
+
+    def asarray(self, value, dtype=None):
+        return self._backend.array(value, dtype=dtype, copy=False)
+
+    def array(self, value, dtype=None, copy=True):
+        return self._backend.array(value, dtype=dtype, copy=copy)
+
+    def copyto(self, destination, source):
+        destination = DeviceArray.wrap(destination)
+        if isinstance(source, DeviceArray) or _is_device(source):
+            source = DeviceArray.wrap(source)
+            if source.shape != destination.shape:
+                raise ValueError(f"copyto: shapes {source.shape} and {destination.shape} differ.")
+            destination.copy_from(source)
+        else:
+            from ..tensor import _assign_device
+            _assign_device(destination, source, destination.dtype)
+
+    errstate = staticmethod(np.errstate)
+
+    def __getattr__(self, name):
+        if name.startswith("__"):              # protocol probes (copy, pickle, hasattr) see a plain absence
+            raise AttributeError(name)
+        raise RuntimeError(f"HIP primitive {name!r} is not available in namitorch_amd: the optimizer step's "
+                           "arithmetic runs in the library's kernels, and no CPU fallback is used.")
+
+
+def _shape(shape) -> tuple:
+    return (int(shape),) if isinstance(shape, (int, np.integer)) else tuple(int(size) for size in shape)
+
+
 class HIPBackend:
     array_type = DeviceArray
 
@@ -148,6 +206,7 @@ class HIPBackend:
         if device.index >= count.value:
             raise RuntimeError(f"CUDA device {device} is unavailable; found {count.value} CUDA devices.")
         self.device = device
+        self.namespace = HIPNamespace(self)
         self.adamw = AdamWHIPKernel(self)
         self._plans: OrderedDict = OrderedDict()
         self._lock = threading.RLock()
@@ -471,4 +530,4 @@ def is_power_of_two(value: float) -> bool:
     return mantissa == 0.5
 
 
-__all__ = ["HIPBackend", "AdamWHIPKernel", "Plan", "make_xform"]
+__all__ = ["HIPBackend", "HIPNamespace", "AdamWHIPKernel", "Plan", "make_xform"]

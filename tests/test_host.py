@@ -238,3 +238,17 @@ def test_device_spellings_match_reference(golden_dir):
         assert outcome(lambda: Device(Device(value), index)) == want, (value, index)
     assert Device("cuda") is Device("cuda:0") is Device("cuda", 0)
     assert Device("cpu") == Device(Device("cpu")) and hash(Device("cuda:2")) == hash(Device("cuda", 2))
+
+
+def test_host_backend_namespace_is_numpy():
+    """backends/__init__.py:79-80: the host backend's namespace is NumPy; the
+    HIP namespace offers only constructors and copies (checked on the GPU)."""
+    from namitorch_amd import backends
+    from namitorch_amd.backends.hip import HIPNamespace
+    assert backends.namespace() is np and backends.namespace("cpu") is np
+    assert backends.namespace(np.zeros(2, dtype=np.float32)) is np
+    assert nt.get_backend("cpu").namespace is np
+    probe = HIPNamespace.__new__(HIPNamespace)
+    with pytest.raises(RuntimeError, match="'sqrt' is not available"):
+        probe.sqrt
+    assert not hasattr(probe, "__array_namespace__")
