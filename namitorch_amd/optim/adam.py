@@ -475,7 +475,7 @@ class _Replay:
         if tuple(map(_REQUIRES, registered)) != self.requires:
             return False
         current = tuple(map(_GRAD, registered))
-        if any(gradient is not None and gradient._incoming is not None for gradient in current):
+        if any(map(getattr, current, repeat("_incoming"), repeat(None))):
             return False                                        # the full step adds deferred accumulations
         if not all(map(is_, current, self.grads)) and not self._adopt(optimizer, current):
             return False

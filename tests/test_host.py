@@ -37,6 +37,15 @@ def test_library_exports_every_declared_symbol():
     assert lib.nt_abi_version() == _native.ABI_VERSION
 
 
+def test_header_constants_match_python_mirror():
+    """Every integer #define of the header that the ctypes layer mirrors has the same value."""
+    defines = dict(re.findall(r"^#define (NT_[A-Z0-9_]+) \(?(-?\d+)\)?", HEADER.read_text(), flags=re.M))
+    mirrored = {name: value for name, value in defines.items() if hasattr(_native, name)}
+    assert {"NT_OK", "NT_F16", "NT_COPY_D2H", "NT_FINALIZE_CLIP_IF_FINITE"} <= set(mirrored)
+    for name, value in mirrored.items():
+        assert getattr(_native, name) == int(value), name
+
+
 def test_status_codes_map_to_reference_exceptions():
     lib = _native.load()
     with pytest.raises(ValueError, match="plan output pointer is NULL"):
