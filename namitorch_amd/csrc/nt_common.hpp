@@ -22,6 +22,7 @@ constexpr int kTile = kBlock * kVec * kUnroll;   // elements per workgroup itera
 constexpr int kPass2Unroll = 4;    // groups in flight per lane in the multi-tensor AdamW pass
 constexpr int kPass2Tile = kBlock * kVec * kPass2Unroll;
 constexpr int kPassSlice = 256;    // elements per one-wave workgroup of the split multi-tensor pass
+constexpr uint32_t kFp32XcdGroup = 256;   // workgroups per XCD per group, all-float32 pass layout
 
 // ---- bit casts ---------------------------------------------------------------
 __device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }

@@ -67,11 +67,38 @@ def _norm_type(value: object) -> float:
     return value
 
 
+_GRAD_OF = attrgetter("_grad")
+_DEVICE_OF = attrgetter("_device")
+_SHAPE_OF = attrgetter("shape")
+_FLOATING_OF = attrgetter("_dtype._floating")
+
+
+def _gradients_bulk(parameters) -> list[Tensor] | None:
+    """``_gradients`` for the common case, in C-level passes: every entry a
+    Tensor whose gradient is a distinct floating Tensor of its shape on its
+    (identical) Device object.  None when anything else holds, so that the
+    per-parameter loop skips, deduplicates or raises exactly as the
+    reference does."""
+    if not all(map(isinstance, parameters, repeat(Tensor))):
+        return None
+    gradients = list(map(_GRAD_OF, parameters))
+    if (not all(map(isinstance, gradients, repeat(Tensor))) or not all(map(_FLOATING_OF, gradients))
+            or not all(map(is_, map(_DEVICE_OF, gradients), map(_DEVICE_OF, parameters)))
+            or not all(map(eq, map(_SHAPE_OF, gradients), map(_SHAPE_OF, parameters)))
+            or len(set(map(id, gradients))) != len(gradients)):
+        return None
+    return gradients
+
+
 def _gradients(parameters) -> list[Tensor]:
     if isinstance(parameters, Tensor):
         parameters = (parameters,)
     if isinstance(parameters, (dict, str, bytes, set, frozenset)):
         raise TypeError("parameters must be a Tensor or an ordered iterable of Tensors.")
+    if type(parameters) in (list, tuple):
+        gradients = _gradients_bulk(parameters)
+        if gradients is not None:
+            return gradients
     try:
         parameters = iter(parameters)
     except TypeError:

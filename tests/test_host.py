@@ -261,3 +261,38 @@ def test_host_backend_namespace_is_numpy():
     with pytest.raises(RuntimeError, match="'sqrt' is not available"):
         probe.sqrt
     assert not hasattr(probe, "__array_namespace__")
+
+
+def test_clip_gradient_collection_bulk_path_matches_loop():
+    """clip_grad._gradients: the C-level pass for the common case returns what
+    the per-parameter loop (clip_grad.py:36-60) returns, and every other case
+    (None, repeated, wrong shape, integer) goes through the loop's skips and errors."""
+    from namitorch_amd.optim import clip_grad
+
+    def params(n):
+        out = []
+        for k in range(n):
+            p = nt.Parameter(np.zeros(k + 1, dtype=np.float32))
+            p.grad = nt.Tensor(np.full(k + 1, k, dtype=np.float32))
+            out.append(p)
+        return out
+
+    plain = params(5)
+    bulk = clip_grad._gradients_bulk(plain)
+    assert bulk is not None and all(g is p.grad for g, p in zip(bulk, plain))
+    assert [id(g) for g in clip_grad._gradients(tuple(plain))] == [id(g) for g in bulk]
+    holes = params(4)
+    holes[1].grad = None
+    holes[3].grad = holes[2].grad
+    assert clip_grad._gradients_bulk(holes) is None
+    assert [id(g) for g in clip_grad._gradients(holes)] == [id(holes[0].grad), id(holes[2].grad)]
+    wrong = params(3)
+    wrong[2].grad = nt.Tensor(np.zeros(7, dtype=np.float32))
+    with pytest.raises(ValueError, match=r"Gradient shape \(7,\) does not match parameter shape \(3,\)"):
+        clip_grad._gradients(wrong)
+    integer = params(2)
+    integer[0].grad = nt.Tensor(np.zeros(1, dtype=np.int32))
+    with pytest.raises(TypeError, match="Gradients must be floating NamiTorch Tensors."):
+        clip_grad._gradients(integer)
+    with pytest.raises(TypeError, match="parameters must contain only NamiTorch Tensors."):
+        clip_grad._gradients(params(2) + [3])
