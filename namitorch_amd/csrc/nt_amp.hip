@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "nt_internal.hpp"
 
@@ -215,14 +216,21 @@ __device__ __forceinline__ void add_incoming(float (&g)[kPrepassUnroll][kVec], c
         for (int k = 0; k < kVec; ++k) g[u][k] = G::round_f32(g[u][k] + h[u][k]);
 }
 
+// No raw-word visitor (prepass_visit's default).
+struct NoRaw {};
+
 // Visits the elements of this workgroup's tasks: vec(g) for each group of
 // kPrepassUnroll x 4 loaded values (missing ones 0), one(value) for
-// tail/unaligned elements.  Task entries and descriptors are read at
-// workgroup-uniform addresses, so they come through scalar loads with no
-// LDS staging or barrier; every wave covers its lanes' share of each task.
-template <class G, class Vec, class One>
+// tail/unaligned elements.  With a `raw` visitor, whole aligned tasks of
+// tensors without a deferred addend hand it the kPrepassUnroll pairs of
+// 32-bit words as loaded (4 16-bit values per pair, in memory order) instead.
+// Task entries and descriptors are read at workgroup-uniform addresses, so
+// they come through scalar loads with no LDS staging or barrier; every wave
+// covers its lanes' share of each task.
+template <class G, class Vec, class One, class Raw = NoRaw>
 __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tensors, const Task *__restrict__ tasks,
-                                              int64_t first, int ntask, int64_t chunk, Vec vec, One one) {
+                                              int64_t first, int ntask, int64_t chunk, Vec vec, One one,
+                                              Raw raw = Raw()) {
     for (int j = 0; j < ntask; ++j) {
         const Task task = tasks[first + j];
         const DevTensor d = tensors[task.tensor];
@@ -234,6 +242,19 @@ __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tens
         // code with the kPrepassUnroll loads issued back to back.  The
         // branches are workgroup-uniform.
         if (chunk == kPrepassTile && (d.flags & kAligned16) != 0u && start + (uint64_t)kPrepassTile <= d.numel) {
+            if constexpr (!std::is_same<Raw, NoRaw>::value) {
+                if (ip == nullptr) {
+                    u32x2 w[kPrepassUnroll];
+#pragma unroll
+                    for (int u = 0; u < kPrepassUnroll; ++u)
+                        w[u] = gload<true, u32x2, gu32x2>(gp + start + (uint64_t)u * kBlock * kVec +
+                                                          (uint64_t)threadIdx.x * kVec);
+                    // All loads issue before any of them is consumed.
+                    __builtin_amdgcn_sched_barrier(0);
+                    raw(w);
+                    continue;
+                }
+            }
             float g[kPrepassUnroll][kVec];
 #pragma unroll
             for (int u = 0; u < kPrepassUnroll; ++u)
@@ -276,6 +297,42 @@ __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tens
             one(v);
         }
     }
+}
+
+// fp16 gradients under a power-of-two unscale whose inverse is itself an
+// fp16 value (2**-24 .. 2**15): the fp16 product g * inv is the exact product
+// rounded once to fp16, which is what round_f16(f32(g) * inv) gives, so two
+// values are unscaled per packed instruction.  Each square is exact in fp32
+// and the fp64 sum adds them in pacc_fast's order (per lane: group by group,
+// values in memory order).  |h| bit patterns order like magnitudes in fp16 as
+// in fp32 (+inf 0x7c00, every NaN above), so the maximum runs on packed
+// 16-bit lanes and is widened to fp32 bits once at the end.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void pacc_f16_word(PAcc &a, ushort2_t &max2, half2_t inv2, uint32_t word) {
+    const half2_t h = __builtin_bit_cast(half2_t, word) * inv2;
+    const ushort2_t bits = __builtin_bit_cast(ushort2_t, h) & (ushort2_t)(0x7fff);
+    max2 = __builtin_elementwise_max(max2, bits);
+    // h*h + 0 (exact, so equal to h*h): one mixed-precision fma from the fp16 halves.
+    const float h0 = (float)h.x, h1 = (float)h.y;
+    a.sumsq += (double)__builtin_fmaf(h0, h0, 0.0f);
+    a.sumsq += (double)__builtin_fmaf(h1, h1, 0.0f);
+}
+
+// Runs body(unscale, raw): unscale is the per-value form for the generic
+// paths, raw the packed form for whole aligned tasks.
+template <class Body>
+__device__ __forceinline__ void visit_f16(half2_t inv2, ushort2_t &max2, PAcc &acc, Body body) {
+    const float inv = (float)inv2.x;
+    body([inv](float g) { return TF16::round_f32(g * inv); },
+         [&](const u32x2 (&w)[kPrepassUnroll]) {
+#pragma unroll
+             for (int u = 0; u < kPrepassUnroll; ++u) {
+                 pacc_f16_word(acc, max2, inv2, w[u].x);
+                 pacc_f16_word(acc, max2, inv2, w[u].y);
+             }
+         });
 }
 
 template <class G>
@@ -336,24 +393,65 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
         wave_join_finish(join, mine, partials + blockIdx.x);
         return;
     }
-    // Per-element path: unscale and round each value, then accumulate.
-    prepass_visit<G>(tensors, tasks, first, ntask, chunk,
-                     [&](const float (&g)[kPrepassUnroll][kVec]) {
-                         float h[kPrepassUnroll][kVec];
-#pragma unroll
-                         for (int u = 0; u < kPrepassUnroll; ++u)
-#pragma unroll
-                             for (int k = 0; k < kVec; ++k) h[u][k] = unscale_one<G>(g[u][k], xf);
-                         if constexpr (G::code == NT_F16) {
-                             pacc_fast<G>(acc, mn, h);
-                         } else {
+    // Per-element path: unscale and round each value, then accumulate.  The
+    // unscale mode is the same for the whole grid; each mode has its own
+    // element loop, so no element pays a test of it (the compiler does not
+    // hoist the test out of the unrolled loop by itself).
+    auto visit = [&](auto unscale) {
+        prepass_visit<G>(tensors, tasks, first, ntask, chunk,
+                         [&](const float (&g)[kPrepassUnroll][kVec]) {
+                             float h[kPrepassUnroll][kVec];
 #pragma unroll
                              for (int u = 0; u < kPrepassUnroll; ++u)
 #pragma unroll
-                                 for (int k = 0; k < kVec; ++k) pacc_wide(acc, h[u][k]);
-                         }
-                     },
-                     [&](float v) { pacc_wide(acc, unscale_one<G>(v, xf)); });
+                                 for (int k = 0; k < kVec; ++k) h[u][k] = unscale(g[u][k]);
+                             if constexpr (G::code == NT_F16) {
+                                 pacc_fast<G>(acc, mn, h);
+                             } else {
+#pragma unroll
+                                 for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+                                     for (int k = 0; k < kVec; ++k) pacc_wide(acc, h[u][k]);
+                             }
+                         },
+                         [&](float v) { pacc_wide(acc, unscale(v)); });
+    };
+    if constexpr (G::code == NT_F16) {
+        const uint32_t e = f32_bits(xf.inv_scale) >> 23;
+        if (xf.unscale == 2 && e >= 127u - 24u && e <= 127u + 15u) {
+            // inv = 2**(e - 127) is an fp16 value: the packed path.
+            const half2_t inv2 = {(_Float16)xf.inv_scale, (_Float16)xf.inv_scale};
+            ushort2_t max2 = {0, 0};
+            visit_f16(inv2, max2, acc, [&](auto unscale, auto raw) {
+                prepass_visit<G>(tensors, tasks, first, ntask, chunk,
+                                 [&](const float (&g)[kPrepassUnroll][kVec]) {
+                                     float h[kPrepassUnroll][kVec];
+#pragma unroll
+                                     for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+                                         for (int k = 0; k < kVec; ++k) h[u][k] = unscale(g[u][k]);
+                                     pacc_fast<G>(acc, mn, h);
+                                 },
+                                 [&](float v) { pacc_wide(acc, unscale(v)); }, raw);
+            });
+            const uint32_t m16 = max2.x > max2.y ? max2.x : max2.y;
+            const uint32_t wide = f32_bits(f16_to_f32((uint16_t)m16));
+            acc.amax_bits = wide > acc.amax_bits ? wide : acc.amax_bits;
+            const Partial mine{wave_sum(acc.sumsq), amax_from_bits(wave_max_u32(acc.amax_bits))};
+            wave_join_finish(join, mine, partials + blockIdx.x);
+            return;
+        }
+    }
+    // The three cases of unscale_one.
+    if (xf.unscale == 2) {
+        const float inv = xf.inv_scale;
+        visit([inv](float g) { return G::round_f32(g * inv); });
+    } else if (xf.unscale == 1) {
+        const float scale = xf.scale;
+        visit([scale](float g) { return G::round_f32(g / scale); });
+    } else {
+        visit([](float g) { return g; });
+    }
     const Partial mine{wave_sum(acc.sumsq), amax_from_bits(wave_max_u32(acc.amax_bits))};
     wave_join_finish(join, mine, partials + blockIdx.x);
 }

@@ -417,14 +417,16 @@ def test_fused_step_matches_api_sequence(config):
         assert not api_trace[config["inf_step"]][0]
 
 
-@pytest.mark.parametrize("scale", [None, 65536.0, 1.0, 3.0])
-@pytest.mark.parametrize("magnitude", ["normal", "tiny", "subnormal", "nonfinite"])
+@pytest.mark.parametrize("scale", [None, 65536.0, 1.0, 3.0, 2.0 ** 30])
+@pytest.mark.parametrize("magnitude", ["normal", "tiny", "subnormal", "nonfinite", "nan"])
 def test_fp16_grad_norm_paths(scale, magnitude):
     """Pre-pass exactness on float16 gradients, which are unscaled and
     rounded element by element: unscaled values that land in the float16
-    subnormal range, float16 subnormal inputs, and values that overflow to
-    inf on storage give the oracle's norm and found_inf, with no scale, a
-    power-of-two scale, scale 1 and any other scale."""
+    subnormal range, float16 subnormal inputs, values that overflow to inf
+    on storage and NaN give the oracle's norm and found_inf, with no scale,
+    a power-of-two scale whose inverse is a float16 value (65536, 1: the
+    packed float16 path), one whose inverse is not (2**30), and any other
+    scale."""
     rng = _rng(93)
     n = 70001
     g32 = (rng.standard_normal(n) * 4.0).astype(np.float32)
@@ -436,6 +438,9 @@ def test_fp16_grad_norm_paths(scale, magnitude):
     elif magnitude == "nonfinite":
         g32[77] = np.inf
         g32[4099] = np.float32(7e4)             # overflows float16 on storage
+    elif magnitude == "nan":
+        g32[8200] = np.nan
+        g32[9000] = -np.inf
     g = g32.astype(np.float16)
     param = nt.Parameter(np.zeros(n, dtype=np.float32), dtype="float16", device=DEV)
     param.grad = nt.Tensor(g, dtype="float16", device=DEV)
