@@ -209,9 +209,15 @@ _pinned_idle: dict = {}            # size -> idle arrays
 
 
 def take_pinned(nbytes: int) -> np.ndarray:
-    """A page-locked buffer from the pool (or a new one)."""
+    """A page-locked buffer from the pool (or a new one).  Safe across
+    threads: another thread may empty the list between the look and the pop."""
     idle = _pinned_idle.get(nbytes)
-    return idle.pop() if idle else pinned(nbytes)
+    if idle:
+        try:
+            return idle.pop()
+        except IndexError:
+            pass
+    return pinned(nbytes)
 
 
 def give_pinned(array: np.ndarray) -> None:
