@@ -43,8 +43,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
-// v_cvt_f16_f32: round to nearest even, overflow to inf.
+// v_cvt_f16_f32: round to nearest even, overflow to inf.  The operand is
+// made opaque first: otherwise the compiler folds a producing multiply and
+// this conversion into one v_fma_mixlo_f16 with a +0 addend, which turns a
+// -0 product into +0 (NumPy's float16 arithmetic, an fp32 operation rounded
+// once to fp16, keeps -0).  Every fp16 result is therefore the fp32 value of
+// its operation rounded once.
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    __asm__("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 

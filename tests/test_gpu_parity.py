@@ -299,6 +299,73 @@ def test_unscaled_grads_visible_in_place():
     assert _same(param.grad.numpy(), oscaler.unscale(g, 3000.0))[0]
 
 
+def _bits(array: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(array).view({2: np.uint16, 4: np.uint32}[array.dtype.itemsize])
+
+
+@pytest.mark.parametrize("scale", [65536.0, 3.0])
+def test_float16_signed_zeros_match_numpy(scale):
+    """Every float16 result is its float32 operation rounded once, -0 included
+    (NumPy's float16 arithmetic).  Products that are -0 (0 x negative, and
+    negative values that unscale below the smallest float16 subnormal) stay
+    -0 in the unscaled gradients read back, in the float16 AdamW update
+    (beta1 = 0, maximize: m = 0*m + 1*(-g)) and in the float32-master pass
+    that unscales float16 gradients itself."""
+    n = 4099
+    g = np.zeros(n, dtype=np.float16)
+    g[1::4] = np.float16(-0.0)
+    g[2::4] = np.float16(-6e-8)                  # the smallest float16 subnormal, negative
+    g[3::4] = (_rng(3).standard_normal(n)[3::4] * 1e-3).astype(np.float16)
+    # Unscaled in place and read back.
+    param = nt.Parameter(np.zeros(n, dtype=np.float16), device=DEV)
+    optimizer = nt.optim.AdamW([param], eps=1e-4)
+    scaler = nt.GradScaler(init_scale=scale)
+    scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+    param.grad = nt.Tensor(g, device=DEV)
+    assert scaler.unscale_(optimizer)
+    want = oscaler.unscale(g, scale, "float16")
+    assert np.signbit(want).sum() > n // 4
+    assert np.array_equal(_bits(param.grad.numpy()), _bits(want))
+    # float16 AdamW steps whose moments are -0 where the gradient is 0.
+    p0 = (_rng(4).standard_normal(n) * 0.02).astype(np.float16)
+    grads = [(_rng(5 + k).standard_normal(n) * 1e-2).astype(np.float16) for k in range(2)]
+    grads[1][::3] = np.float16(0.0)
+    param = nt.Parameter(p0, device=DEV)
+    options = dict(lr=1e-3, betas=(0.0, 0.95), eps=1e-4, weight_decay=0.0, maximize=True)
+    optimizer = nt.optim.AdamW([param], **options)
+    ref_p, ref_m, ref_v = p0.copy(), np.zeros(n, np.float16), np.zeros(n, np.float16)
+    for step, grad in enumerate(grads, start=1):
+        param.grad = nt.Tensor(grad, device=DEV)
+        optimizer.step()
+        oadam.adam_step(ref_p, grad, ref_m, ref_v, step, **options)
+    state = optimizer.state[id(param)]
+    assert np.signbit(ref_m[::3]).sum() > 0
+    assert np.array_equal(_bits(state["exp_avg"].numpy()), _bits(ref_m))
+    assert np.array_equal(_bits(state["exp_avg_sq"].numpy()), _bits(ref_v))
+    assert np.array_equal(_bits(param.numpy()), _bits(ref_p))
+    # The float32-master pass unscales the float16 gradient itself (fused
+    # path): after a first step leaves negative moments, the unscaled +0 and
+    # -0 of the second step's gradient give m = -0 and +0 respectively.
+    bf = nt.Parameter(lowp.round_bf16(p0.astype(np.float32)), dtype="bfloat16", device=DEV)
+    optimizer = nt.optim.AdamW([bf], master_weights=True, **options)
+    scaler = nt.GradScaler(init_scale=scale, growth_interval=1000)
+    master = lowp.round_bf16(p0.astype(np.float32))
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    first = (grads[0].astype(np.float32) * np.float32(scale)).astype(np.float16)
+    for step, stored in enumerate((first, g), start=1):
+        scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+        bf.grad = nt.Tensor(stored, device=DEV)
+        assert nt.amp.fused_step(optimizer, scaler).updated
+        unscaled = oscaler.unscale(stored, scale, "float16")
+        oadam.master_step(master, unscaled.astype(np.float32), m, v, step, **options)
+    assert (np.signbit(m) & (m == 0)).sum() > 0 and ((~np.signbit(m)) & (m == 0)).sum() > 0
+    state = optimizer.state[id(bf)]
+    assert np.array_equal(_bits(state["exp_avg"].numpy()), _bits(m))
+    assert np.array_equal(_bits(state["exp_avg_sq"].numpy()), _bits(v))
+    assert np.array_equal(_bits(state["master"].numpy()), _bits(master))
+
+
 def test_unscale_overflow_to_inf_in_grad_dtype():
     """scale < 1: finite float16 grads overflow after division -> found_inf."""
     param = nt.Parameter(np.zeros(10, dtype=np.float16), device=DEV)
