@@ -176,6 +176,9 @@ class HIPNamespace:
         destination = DeviceArray.wrap(destination)
         if isinstance(source, DeviceArray) or _is_device(source):
             source = DeviceArray.wrap(source)
+            if source.device != destination.device:
+                raise RuntimeError(f"Operands are on different devices: {destination.device}, {source.device}; "
+                                   "use an explicit .to() transfer.")
             if source.shape != destination.shape:
                 raise ValueError(f"copyto: shapes {source.shape} and {destination.shape} differ.")
             destination.copy_from(source)
