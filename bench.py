@@ -179,10 +179,13 @@ def bench_c2(nt, torch, steps, warmup):
 
 
 def kernel_time_c2(nt, torch, optimizer, params, launches):
-    backend = nt.get_backend("cuda:0")
-    plans = list(backend._plans.values())
-    plan = max(plans, key=lambda p: p.numel)
+    """Average duration (ms) of the optimizer's float32 AdamW pass relaunched
+    back to back through its cached plan, between two events on the launch
+    stream."""
     from namitorch_amd import _native
+    backend = nt.get_backend("cuda:0")
+    numel = sum(p.numel() for p in params)
+    plan = next(p for p in backend._plans.values() if p.numel == numel and p.layout[0] == _native.NT_F32)
     group = optimizer.param_groups
     records = []
     for g in group:
@@ -217,22 +220,39 @@ def bench_c1(nt, torch, steps, warmup):
     stop.record()
     stop.synchronize()
     hot_ms = start.elapsed_time(stop) / steps
-    # MALL flush: stream 1 GiB through HBM between steps; time only the step.
+    # The pass alone, relaunched back to back (the step loop above can wait
+    # for the host at this size).
+    hot_kernel_ms = kernel_time_c2(nt, torch, optimizer, [param], steps)
+    # MALL flush: stream 1 GiB through HBM before every step.  The step's cost
+    # is the difference between `steps` x (fill + step) and `steps` x fill,
+    # each timed between two events only: a timing event between every fill
+    # and step would add its own device time (about 6 us) to each step.
     scratch = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
-    total = 0.0
-    for _ in range(steps):
-        scratch.fill_(1.0)
+
+    def loop(with_step: bool) -> float:
         a, b = event_pair(torch)
+        torch.cuda.synchronize()
         a.record()
-        optimizer.step()
+        for _ in range(steps):
+            scratch.fill_(1.0)
+            if with_step:
+                optimizer.step()
         b.record()
         b.synchronize()
-        total += a.elapsed_time(b)
-    flushed_ms = total / steps
+        return a.elapsed_time(b) / steps
+
+    loop(True)
+    differences = []
+    for _ in range(5):
+        differences.append(loop(True) - loop(False))
+    flushed_ms = statistics.median(differences)
     del scratch, optimizer, param
     release(nt, torch)
-    return dict(params=n, bytes_per_param=28, hot_ms=hot_ms, flushed_ms=flushed_ms,
-                hot_GBps=28 * n / hot_ms / 1e6, flushed_GBps=28 * n / flushed_ms / 1e6)
+    return dict(params=n, bytes_per_param=28, hot_ms=hot_ms, hot_kernel_ms=hot_kernel_ms, flushed_ms=flushed_ms,
+                flushed_rounds_ms=differences, hot_GBps=28 * n / hot_ms / 1e6,
+                hot_kernel_GBps=28 * n / hot_kernel_ms / 1e6, flushed_GBps=28 * n / flushed_ms / 1e6,
+                flushed_method="median over 5 rounds of [steps x (1 GiB fill + step) - steps x 1 GiB fill], "
+                               "two events per loop")
 
 
 # ---- C3 / C4 / C5: mixed precision through the public API -------------------------------------------
@@ -830,7 +850,9 @@ def main():
     from namitorch_amd.param_lists import gpt_1p3b_shapes
     if "c1" in wanted:
         log("C1 flat 4M fp32")
-        extra["c1_flat4m_fp32"] = bench_c1(nt, torch, args.steps, args.warmup)
+        extra["c1_flat4m_fp32"] = c1 = bench_c1(nt, torch, args.steps, args.warmup)
+        log(f"C1: flushed {c1['flushed_ms'] * 1e3:.1f} us/step, hot {c1['hot_ms'] * 1e3:.1f} us/step, "
+            f"hot pass {c1['hot_kernel_ms'] * 1e3:.1f} us")
     # C3 GPT-2 AMP (bf16 model, fp32 master, fp16 grads x65536); C4 GPT-1.3B
     # bf16 params/m/v/grads, fp32 master, clip 1.0; C5 Llama-7B fp32
     # master/m/v, bf16 grads/params, AMP + clip; and one GPU's share of an
