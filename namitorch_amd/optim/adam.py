@@ -329,12 +329,19 @@ def _IS_NONE(value) -> bool:
     return value is None
 
 
+def _exact_float(value: float):
+    """A finite float as a key item that compares equal only to the same
+    value with the same sign: float equality is exact except that +0.0 and
+    -0.0 compare equal, so zeros carry their sign."""
+    return (value, math.copysign(1.0, value)) if value == 0.0 else value
+
+
 def _options_key(groups) -> tuple | None:
     """The option values of every parameter group, exactly: names, types,
-    and values, with floats by their bit pattern.  Two steps with equal keys
-    prepare equal options and pass the same checks.  None (do not memoize)
-    for values whose checks must run every step: non-finite floats, or
-    anything other than scalars and tuples/lists of scalars."""
+    and values (floats by value and, for zeros, sign).  Two steps with equal
+    keys prepare equal options and pass the same checks.  None (do not
+    memoize) for values whose checks must run every step: non-finite floats,
+    or anything other than scalars and tuples/lists of scalars."""
     key: list = []
     for group in groups:
         for name, value in group.items():
@@ -344,12 +351,12 @@ def _options_key(groups) -> tuple | None:
             if kind is float:
                 if not math.isfinite(value):
                     return None
-                value = value.hex()
+                value = _exact_float(value)
             elif kind is tuple or kind is list:
                 items = []
                 for item in value:
                     if type(item) is float and math.isfinite(item):
-                        items.append((float, item.hex()))
+                        items.append((float, _exact_float(item)))
                     elif type(item) in (int, bool):
                         items.append((type(item), item))
                     else:

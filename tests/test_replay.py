@@ -252,3 +252,18 @@ def test_next_coefficients_equal_a_full_computation():
             assert type(got) is type(want)
             assert bytes(got) == bytes(want), (trial, dtype, options, later)
             assert ctypes.addressof(got) != ctypes.addressof(previous)
+
+
+def test_options_key_is_exact():
+    """Equal keys only for the same option values and types; zeros keep their sign."""
+    from namitorch_amd.optim.adam import _options_key
+    base = [{"params": [], "lr": 1e-3, "betas": (0.9, 0.999), "eps": 1e-8, "weight_decay": 0.0, "maximize": False}]
+    same = [{"params": [1], "lr": 1e-3, "betas": (0.9, 0.999), "eps": 1e-8, "weight_decay": 0.0, "maximize": False}]
+    assert _options_key(base) == _options_key(same)
+    for name, value in (("weight_decay", -0.0), ("lr", float(np.nextafter(1e-3, 1.0))), ("betas", (0.9, 0.99)),
+                        ("betas", [0.9, 0.999]), ("weight_decay", 0), ("maximize", 0), ("eps", 1e-8 + 1e-24)):
+        changed = [dict(base[0], **{name: value})]
+        assert _options_key(changed) != _options_key(base), (name, value)
+    assert _options_key([dict(base[0], betas=(0.0, -0.0))]) != _options_key([dict(base[0], betas=(-0.0, 0.0))])
+    assert _options_key([dict(base[0], lr=float("nan"))]) is None
+    assert _options_key([dict(base[0], lr=np.float32(1e-3))]) is None
