@@ -9,6 +9,9 @@ from __future__ import annotations
 
 import atexit
 import ctypes
+import importlib.util
+import os
+import sys
 import threading
 from pathlib import Path
 
@@ -199,6 +202,37 @@ _lock = threading.Lock()
 _lib = None
 
 
+def _share_pytorch_runtime() -> None:
+    """Keep one HIP runtime in the process.
+
+    PyTorch's ROCm builds carry their own HIP and HSA runtime libraries
+    (``torch/lib``).  When PyTorch was imported first, the dynamic linker
+    binds this library's ``libamdhip64`` dependency to PyTorch's copy by
+    name, and both share one runtime.  When this library loads first, it
+    would bind to the system runtime, and a second runtime loaded later by
+    PyTorch finds no device.  So when PyTorch is installed but not loaded
+    yet, its two runtime libraries are loaded first (PyTorch itself is not
+    imported), and either package may then use the GPU first.  Setting
+    ``NT_SYSTEM_HIP_RUNTIME=1`` keeps the system runtime."""
+    if os.environ.get("NT_SYSTEM_HIP_RUNTIME") == "1" or "torch" in sys.modules:
+        return
+    try:
+        spec = importlib.util.find_spec("torch")
+    except (ImportError, ValueError):
+        return
+    if spec is None or spec.origin is None:
+        return
+    runtime_dir = Path(spec.origin).parent / "lib"
+    for name in ("libhsa-runtime64.so", "libamdhip64.so"):
+        path = runtime_dir / name
+        if not path.exists():
+            return
+        try:
+            ctypes.CDLL(str(path), mode=ctypes.RTLD_GLOBAL)
+        except OSError:
+            return
+
+
 def load() -> ctypes.CDLL:
     """Load the library (once) and declare every entry point's signature."""
     global _lib
@@ -212,6 +246,7 @@ def load() -> ctypes.CDLL:
                 f"{LIB_PATH} is missing; build it with `python -m namitorch_amd.build` "
                 "(hipcc --offload-arch=gfx950)."
             )
+        _share_pytorch_runtime()
         try:
             lib = ctypes.CDLL(str(LIB_PATH))
         except OSError as error:

@@ -6,7 +6,8 @@ master weights and float32 or bfloat16 moments), one or two parameter groups
 with their own options (lr including 0, betas including beta1 = 0, eps,
 weight decay, maximize, the fused switch; Adam with coupled decay or AdamW),
 tensors of ragged sizes around the kernels' slice and task boundaries,
-gradients with subnormal and (without a scaler) non-finite values, and
+gradients with subnormal and (without a scaler) non-finite values, storage
+adopted from PyTorch at offsets that break 16-byte alignment, and
 optionally a GradScaler (scales that are and are not powers of two, a seeded
 inf or NaN, growth within the run), clipping (active, inactive, or to zero
 with max_norm 0) and a second micro-batch accumulated eagerly or deferred,
@@ -111,6 +112,10 @@ def _draw_case(seed: int) -> dict:
     accumulate = bool(rng.random() < 0.3) and grad_dtype == param_dtype
     defer = bool(rng.random() < 0.5)
     zeroed = accumulate and bool(rng.random() < 0.4)
+    # Tensors adopted from another framework at an element offset that breaks
+    # 16-byte alignment (the kernels' scalar paths), per tensor.
+    misalign = bool(rng.random() < 0.25)
+    offsets = [int(rng.integers(0, 8)) if misalign else 0 for _ in range(count)]
     # Without a scaler: subnormal and non-finite gradient values at seeded places.
     specials = []
     if not amp and rng.random() < 0.3:
@@ -134,7 +139,7 @@ def _draw_case(seed: int) -> dict:
     return dict(seed=seed, kind=kind, layout=layout, param_dtype=param_dtype, grad_dtype=grad_dtype,
                 state_dtype=state_dtype, shapes=shapes, groups=groups, amp=amp, scale=scale, interval=interval,
                 poison=poison, specials=specials, max_norm=max_norm, accumulate=accumulate, defer=defer,
-                zeroed=zeroed, params=params, grads=grads, incoming=incoming)
+                zeroed=zeroed, params=params, grads=grads, incoming=incoming, offsets=offsets)
 
 
 def _oracle(case: dict) -> dict:
@@ -189,8 +194,27 @@ def _oracle(case: dict) -> dict:
                 scale=scaler.scale if scaler is not None else None, clipped=clipped_any)
 
 
+def _adopted(host: np.ndarray, dtype: str, offset: int, parameter: bool = False):
+    """`host` on the device in `dtype`; with an offset, as a view that starts
+    `offset` elements into a larger PyTorch allocation (adopted, not copied)."""
+    if offset == 0:
+        return (nt.Parameter if parameter else nt.Tensor)(host, dtype=dtype, device=DEV)
+    import torch
+    kind = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16,
+            "float64": torch.float64}[dtype]
+    base = torch.zeros(host.size + offset, dtype=kind, device=DEV)
+    view = base[offset:].view(host.shape)
+    view.copy_(torch.from_numpy(np.ascontiguousarray(host)).to(DEV).to(kind))    # exact: host holds dtype values
+    if not parameter:
+        return nt.Tensor._from_storage(view)
+    adopted = nt.Parameter.__new__(nt.Parameter)
+    nt.Tensor._initialize(adopted, view, True)
+    return adopted
+
+
 def _device(case: dict, path: str) -> dict:
-    params = [nt.Parameter(p, dtype=case["param_dtype"], device=DEV) for p in case["params"]]
+    offsets = case["offsets"]
+    params = [_adopted(p, case["param_dtype"], o, parameter=True) for p, o in zip(case["params"], offsets)]
     groups = [dict(params=[params[i] for i in g["members"]],
                    **{k: value for k, value in g.items() if k != "members"}) for g in case["groups"]]
     master_mode = case["layout"] == "master"
@@ -205,7 +229,7 @@ def _device(case: dict, path: str) -> dict:
     for step in range(STEPS):
         if scaler is not None:
             scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
-        arrived = [nt.Tensor(g, dtype=case["grad_dtype"], device=DEV) for g in case["grads"][step]]
+        arrived = [_adopted(g, case["grad_dtype"], (o * 3) % 8) for g, o in zip(case["grads"][step], offsets)]
         if case["zeroed"] and step > 0:
             optimizer.zero_grad(set_to_none=False)
             nt.accumulate_grads(params, arrived)
@@ -213,7 +237,7 @@ def _device(case: dict, path: str) -> dict:
             for p, g in zip(params, arrived):
                 p.grad = g
         if case["accumulate"]:
-            incoming = [nt.Tensor(h, dtype=case["grad_dtype"], device=DEV) for h in case["incoming"][step]]
+            incoming = [_adopted(h, case["grad_dtype"], (o * 5) % 8) for h, o in zip(case["incoming"][step], offsets)]
             nt.accumulate_grads(params, incoming, defer=case["defer"])
         if path == "api":
             finite = scaler.unscale_(optimizer) if scaler is not None else True
@@ -277,6 +301,7 @@ def test_random_composition_matches_oracle(seed):
     print(f"case {seed}: {case['kind']} {case['layout']} p={case['param_dtype']} g={case['grad_dtype']} s={case['state_dtype']} "
           f"shapes={case['shapes']} amp={case['amp']} scale={case['scale']} poison={case['poison']} "
           f"clip={case['max_norm']} accumulate={case['accumulate']} defer={case['defer']} zeroed={case['zeroed']} "
+          f"offsets={case['offsets']} "
           f"specials={case['specials']}", flush=True)
     want = _oracle(case)
     loose = want["clipped"]
