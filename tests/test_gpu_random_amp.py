@@ -8,7 +8,8 @@ that updated (runner.py:250-253; ``fused_step(..., scheduler=)`` on the
 fused steps).  Along the way it injects inf/NaN gradients, changes the clip
 threshold, reads step counts and the loss scale right after fused steps
 (which must already show a skipped step as skipped), and round-trips the
-optimizer's and the scaler's state dicts.
+optimizer's and the scaler's state dicts, or resumes from a checkpoint
+archive into new parameters, optimizer, scaler and schedule.
 
 The oracle composes ``scaler.unscale`` -> ``clip.clip_grad_norm`` ->
 ``adam.master_step`` / ``adam.adam_step`` with ``scaler.Scaler`` and the
@@ -54,7 +55,7 @@ def _close(label, got, want, loose):
 
 
 @pytest.mark.parametrize("seed", range(CASES))
-def test_random_amp_sequence(seed):
+def test_random_amp_sequence(seed, tmp_path):
     rng = np.random.default_rng(9000 + seed)
     master = bool(rng.random() < 0.6)
     dtype = "bfloat16" if master else "float32"
@@ -133,6 +134,18 @@ def test_random_amp_sequence(seed):
             optimizer.load_state_dict(optimizer.state_dict())
             scaler.load_state_dict(scaler.state_dict())
             log.append("reload")
+        if rng.random() < 0.12:
+            # Resume from a checkpoint archive into new parameters, optimizer,
+            # scaler and schedule (training/checkpoint.py:59-174).
+            path = str(tmp_path / f"step{step}.nt")
+            nt.save_checkpoint(path, {f"p{i}": p for i, p in enumerate(params)}, optimizer, scheduler,
+                               scaler=scaler, step=step + 1)
+            params = [nt.Parameter(np.zeros(s, np.float32), dtype=dtype, device=DEV) for s in shapes]
+            optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.05, master_weights=master)
+            scaler = nt.GradScaler(init_scale=1.0)
+            scheduler = nt.optim.WarmupCosine(optimizer, warmup_steps=2, total_steps=STEPS + 2, min_lr=1e-5)
+            nt.load_checkpoint(path, {f"p{i}": p for i, p in enumerate(params)}, optimizer, scheduler, scaler=scaler)
+            log.append("checkpoint")
         log.append(f"{path}{'' if finite else '!'}{'' if max_norm is None else 'c'}")
     print(f"case {seed}: master={master} g={gdtype} shapes={shapes} scale0={scale0} interval={interval} {log}",
           flush=True)
