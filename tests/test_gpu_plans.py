@@ -163,3 +163,45 @@ def test_destroying_a_plan_does_not_wait_and_its_memory_is_reused():
     done.synchronize()
     torch.cuda.synchronize()
     assert all(not bool(g.any()) for g in grads)
+
+
+def test_plan_cache_churn_across_streams_matches_oracle():
+    """24 optimizers stepped in shuffled order on two library streams for
+    three rounds: more (layout, stream, buffer) combinations than the plan
+    cache holds, so plans are evicted and rebuilt while earlier steps may
+    still be queued.  Every optimizer matches the oracle bit for bit."""
+    from oracle import adam as oadam
+    rng = np.random.default_rng(11)
+    streams = [nt.runtime.Stream(0), nt.runtime.Stream(0)]
+    runs = []
+    for _ in range(24):
+        sizes = [int(rng.choice([257, 2049, 4097, 12289])) for _ in range(int(rng.integers(1, 4)))]
+        hosts = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in sizes]
+        with nt.runtime.stream(streams[0]):
+            params = [nt.Parameter(h, device=DEV) for h in hosts]
+        optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.01)
+        runs.append((params, optimizer, [h.copy() for h in hosts], [np.zeros_like(h) for h in hosts],
+                     [np.zeros_like(h) for h in hosts]))
+    backend = nt.get_backend(DEV)
+    for round_ in range(1, 4):
+        for k in rng.permutation(len(runs)):
+            params, optimizer, ref_p, ref_m, ref_v = runs[k]
+            grads = [(rng.standard_normal(h.size) * 1e-3).astype(np.float32) for h in ref_p]
+            with nt.runtime.stream(streams[(int(k) + round_) % 2]):
+                for p, g in zip(params, grads):
+                    p.grad = nt.Tensor(g, device=DEV)
+                optimizer.step()
+            for i, g in enumerate(grads):
+                oadam.adam_step(ref_p[i], g, ref_m[i], ref_v[i], round_, lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+                                weight_decay=0.01)
+        # A caller that moves an optimizer to another stream orders the streams itself.
+        for stream in streams:
+            stream.synchronize()
+    assert len(backend._plans) <= 16
+    for params, optimizer, ref_p, ref_m, ref_v in runs:
+        for i, p in enumerate(params):
+            state = optimizer.state[id(p)]
+            assert p.numpy().tobytes() == ref_p[i].tobytes()
+            assert state["exp_avg"].numpy().tobytes() == ref_m[i].tobytes()
+            assert state["exp_avg_sq"].numpy().tobytes() == ref_v[i].tobytes()
+            assert state["step"] == 3
