@@ -221,3 +221,25 @@ def test_fused_steps_on_alternating_streams_match_one_stream():
     assert one[1] == two[1]
     for a, b in zip(one[2] + one[3], two[2] + two[3]):
         assert _bits_equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_clip_error_if_nonfinite_matches_reference(golden_dir, dtype):
+    """clip_grad_norm_(error_if_nonfinite=True) on an infinite norm raises the
+    reference's RuntimeError text (tests/golden/golden.json, clip_grad.py:104-105)
+    before anything is clipped; a NaN norm says nan; without the flag the
+    norm is returned and nothing is raised."""
+    want = json.loads((golden_dir / "golden.json").read_text())["errors"]["nonfinite_norm"]
+    values = (np.arange(5000, dtype=np.float32) % 7 - 3) * np.float32(0.25)
+    for poison, text in ((np.inf, want), (np.nan, want.replace("inf", "nan"))):
+        host = values.copy()
+        host[4097] = poison
+        param = nt.Parameter(np.zeros(5000, np.float32), dtype=dtype, device=DEV)
+        param.grad = nt.Tensor(host, dtype=dtype, device=DEV)
+        before = param.grad.bits().copy()
+        with pytest.raises(RuntimeError) as error:
+            nt.optim.clip_grad_norm_([param], 1.0, error_if_nonfinite=True)
+        assert str(error.value) == text
+        assert np.array_equal(param.grad.bits(), before)
+        norm = nt.optim.clip_grad_norm_([param], 1.0).item()
+        assert (math.isnan(norm) if poison != poison else norm == math.inf)
