@@ -109,6 +109,10 @@ class DeviceStep:
         except Exception:
             pass
 
+    def _forget(self) -> None:
+        """Leave the list of unsettled steps (every entry of this step)."""
+        _unsettled_steps[:] = [pending for pending in _unsettled_steps if pending is not self]
+
     def ctrl(self) -> _native.AmpCtrl:
         if self._ctrl is None:
             self.event.synchronize()
@@ -119,6 +123,7 @@ class DeviceStep:
 
     def reconcile(self) -> None:
         if self._reconciled:
+            self._forget()                    # settled: never left waiting in the unsettled list
             return
         ctrl = self.ctrl()
         if self.honor_skip and ctrl.skip:
@@ -142,10 +147,7 @@ class DeviceStep:
                         gradient._finite_version = version - 1
         self.records.clear()
         self._reconciled = True
-        for position, pending in enumerate(_unsettled_steps):
-            if pending is self:
-                del _unsettled_steps[position]
-                break
+        self._forget()
         if self.scheduler is not None and not (self.honor_skip and ctrl.skip):
             self.scheduler._advance()         # training/runner.py:252-253: only after an update
 
@@ -531,7 +533,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         scaler._device_steps.append(device_step)
         scaler._scale_used = False
     optimizer.step()                                      # the AdamW pass reads the control block
-    optimizer.__dict__.setdefault("_device_steps", []).append(device_step)
+    optimizer._track_device_step(device_step)
     _unsettled_steps.append(device_step)                  # version reads settle it first
     return StepResult(device_step)
 

@@ -31,7 +31,7 @@ import numpy as np
 from .. import _native, runtime
 from ..array import DeviceArray
 from ..device import Device
-from ..dtype import float32, int32, normalize_dtype, uint8
+from ..dtype import float32, float64, int32, normalize_dtype, uint8
 
 PLAN_CACHE_SIZE = 16
 INCOMING = 5          # plan pointer column of deferred incoming gradients
@@ -422,6 +422,15 @@ class HIPBackend:
                 self._neutral_ctrl = block
             return self._neutral_ctrl
 
+    def ctrl_norm(self, block: DeviceArray) -> DeviceArray:
+        """A 0-d float64 array holding the block's ``norm``, copied on the
+        device after the work queued so far (the host does not wait)."""
+        with self.context():
+            out = DeviceArray.empty((), float64, self.device)
+            _native.call("nt_memcpy_async", out.data_ptr(), block.data_ptr() + _native.AmpCtrl.norm.offset,
+                         ctypes.sizeof(ctypes.c_double), _native.NT_COPY_D2D, self.stream())
+        return out
+
     def read_ctrl(self, block: DeviceArray) -> _native.AmpCtrl:
         out = _native.AmpCtrl()
         with self.context():
@@ -514,7 +523,9 @@ def make_xform(transform, ctrl_ptr: int | None = None, honor_skip: bool = False)
     if device is not None:
         xform.unscale = int(device.unscale)
         xform.honor_skip = int(device.honor_skip)
-        xform.ctrl = device.block.data_ptr()
+        # The caller launches on its current stream: another stream than the
+        # one that wrote the block first waits for that step's finalize.
+        xform.ctrl = device.block_for_current_stream().data_ptr()
         return xform
     if transform is not None:
         if transform.scale is not None:

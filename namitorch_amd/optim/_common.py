@@ -309,6 +309,7 @@ class _FirstOrderOptimizer(Optimizer):
         if replay is not None:
             with no_grad():
                 if replay.run(self):
+                    self._track_consumed_device_steps()
                     return loss
             self._replay = None
         entries = list(self._grad_entries())
@@ -352,6 +353,7 @@ class _FirstOrderOptimizer(Optimizer):
         with no_grad():
             self._update_many(items)
         self._memoize_step(options)
+        self._track_consumed_device_steps()
         return loss
 
     def _memoize_step(self, options: dict) -> None:

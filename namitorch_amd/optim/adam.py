@@ -295,6 +295,7 @@ class Adam(_FirstOrderOptimizer):
                 device_step.records.append((parameter, state, first, second, master, step, bumped, moves))
         if device_step is not None:
             device_step.optimizers.add(self)
+            self._consume_device_step(device_step)
 
     def _memoize_step(self, options: dict) -> None:
         batches = self.__dict__.pop("_batches", None)
@@ -585,6 +586,7 @@ class _Replay:
             device_step.records.extend(zip(self.members, self.dicts, self.firsts, self.seconds, self.masters, steps,
                                            self.bumped, map(moves.__getitem__, self.member_groups)))
             device_step.optimizers.add(optimizer)
+            optimizer._consume_device_step(device_step)
         return True
 
 

@@ -18,7 +18,11 @@ reduction order is fixed, so the result is deterministic.
 Clipping multiplies each gradient by ``max_norm / (norm + 1e-6)`` in
 float64 and rounds once to the gradient dtype (clip_grad.py:106-111).  The
 rewrite is recorded on the gradients (see ``GradTransform``) and fused into
-the next kernel that reads them.
+the next kernel that reads them.  When nothing is pending on the gradients
+and ``error_if_nonfinite`` is False, the norm, the ``coefficient < 1``
+decision and the coefficient stay on the device (``_clip_on_device``): the
+call queues two kernels and returns without waiting, and the AdamW pass
+that follows reads the decision from the device.
 """
 
 from __future__ import annotations
@@ -289,12 +293,81 @@ def _require_writable(gradients: list[Tensor]) -> None:
         raise RuntimeError("Cannot clip read-only gradient storage.")
 
 
+_WRITABLE = attrgetter("_writable")
+_VALUE = attrgetter("value")
+# Device-decided clips not yet settled by an optimizer step or a version
+# read: past this many, the oldest is settled at the next clip (its finalize
+# ran long before), which bounds the host buffers they hold.
+_UNSETTLED_LIMIT = 64
+
+
+def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
+    """``clip_grad_norm_`` with the norm, the clip decision and the
+    coefficient left on the device, so the host does not wait: the pre-pass
+    and finalize of a fused step without a scaler, whose finalize applies
+    the reference's rule (clip when ``max_norm / (norm + 1e-6) < 1``, also
+    for a non-finite norm).  The gradients get a device-decided clip
+    transform that the next kernel reading them applies (the AdamW pass, or
+    the write-back when a gradient is read), and the result is the device's
+    norm.  The reference's version bump happens only when the coefficient is
+    below 1: it is taken optimistically and undone when the step is settled.
+
+    None (the host path decides) unless no host decision of the reference
+    can raise or differ: norm_type 2 or inf; one device and one float16,
+    bfloat16 or float32 gradient dtype; nothing pending on the gradients;
+    every gradient writable, so a rewrite cannot fail; and no cached
+    statistics for them (then the host path answers without waiting).
+    """
+    if order != 2.0 and not math.isinf(order):
+        return None
+    if not gradients or any(map(_PENDING, gradients)) or not all(map(_WRITABLE, gradients)):
+        return None
+    if _last_stats and _stats_key(gradients) in _last_stats:
+        return None
+    groups = _device_groups(gradients)
+    if len(groups) != 1:
+        return None
+    (backend, dtype), _ = next(iter(groups.items()))
+    if backend.adamw is None or dtype is float64:
+        return None
+    reject_during_capture("Host Tensor reads")           # as the host path: no clipping under capture
+    from ..amp import DeviceStep                         # the amp module imports this one
+    from ..tensor import _unsettled_steps
+    plan = backend.grad_plan(gradients, dtype, incoming=True)
+    neutral = backend.neutral_ctrl()
+    block = backend.empty_ctrl()                         # written whole by the finalize
+    backend.grad_prepass(plan, None, neutral.data_ptr())
+    backend.grad_finalize(plan, block.data_ptr(), order, maximum, 0, carry_ptr=neutral.data_ptr())
+    norm = backend.ctrl_norm(block)
+    clip_bumps: list = []
+    device_step = DeviceStep(backend, block, unscale=False, honor_skip=False, clip_bumps=clip_bumps)
+    device_step.clip_requested = True
+    device_step.capture()
+    transform = GradTransform(device=device_step)
+    counters = tuple(map(_COUNTER, gradients))
+    kept = tuple(map(eq, map(_FINITE_VERSION, gradients), map(_VALUE, counters)))
+    for gradient, counter, keep in zip(gradients, counters, kept):
+        gradient._pending = transform
+        counter.value += 1
+        if keep:
+            gradient._finite_version = counter.value
+    clip_bumps.extend(zip(gradients, map(_VALUE, counters)))
+    if len(_unsettled_steps) >= _UNSETTLED_LIMIT:
+        _unsettled_steps[0].reconcile()
+    _unsettled_steps.append(device_step)                 # version reads settle it first
+    return Tensor._from_storage(norm, False)
+
+
 def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_nonfinite: bool = False) -> Tensor:
     maximum = _nonnegative(max_norm, "max_norm")
     order = _norm_type(norm_type)
     if type(error_if_nonfinite) is not bool:
         raise TypeError("error_if_nonfinite must be a Python bool.")
     gradients = _gradients(parameters)
+    if not error_if_nonfinite:
+        result = _clip_on_device(gradients, maximum, order)
+        if result is not None:
+            return result
     norm = _total_norm(gradients, order)
     if error_if_nonfinite and not math.isfinite(norm):
         raise RuntimeError(f"Cannot clip gradients with nonfinite total norm {np.asarray(norm, dtype=np.float64)}.")

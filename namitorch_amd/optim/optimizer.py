@@ -247,6 +247,27 @@ class Optimizer:
                 device_step.reconcile()
             pending.clear()
 
+    def _track_device_step(self, device_step) -> None:
+        """Settle `device_step` (a device-decided step or clip whose gradient
+        transform a finished step of this optimizer consumed) before this
+        optimizer's next step or state read."""
+        pending = self.__dict__.setdefault("_device_steps", [])
+        if not any(map(is_, pending, repeat(device_step))):
+            pending.append(device_step)
+
+    def _consume_device_step(self, device_step) -> None:
+        """Note, during a step, that its pass reads `device_step`'s decisions.
+        It is tracked only once the step has finished
+        (``_track_consumed_device_steps``): the step's own state reads would
+        otherwise settle it before its bookkeeping is complete."""
+        self.__dict__.setdefault("_consumed_device_steps", []).append(device_step)
+
+    def _track_consumed_device_steps(self) -> None:
+        consumed = self.__dict__.pop("_consumed_device_steps", None)
+        if consumed:
+            for device_step in consumed:
+                self._track_device_step(device_step)
+
     # ---- hooks for subclasses ------------------------------------------------------------
     def _prepare_options(self, options: dict, path: str) -> dict:
         return _checked_options(options, path)

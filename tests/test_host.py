@@ -296,3 +296,22 @@ def test_clip_gradient_collection_bulk_path_matches_loop():
         clip_grad._gradients(integer)
     with pytest.raises(TypeError, match="parameters must contain only NamiTorch Tensors."):
         clip_grad._gradients(params(2) + [3])
+
+
+def test_settled_device_step_never_stalls_the_unsettled_list():
+    """A device-decided step that is already settled removes every entry of
+    itself from the unsettled list when asked again, so settling the list
+    (done by every version read) always ends."""
+    from namitorch_amd.amp import DeviceStep
+    from namitorch_amd.tensor import _settle_device_steps, _unsettled_steps
+    step = DeviceStep.__new__(DeviceStep)           # host state only: no control block, no snapshot
+    step._reconciled = True
+    step.snapshot = None
+    before = list(_unsettled_steps)
+    _unsettled_steps.extend([step, step])
+    try:
+        _settle_device_steps()
+        assert not any(pending is step for pending in _unsettled_steps)
+    finally:
+        _unsettled_steps[:] = [pending for pending in _unsettled_steps if pending is not step]
+    assert _unsettled_steps == before
