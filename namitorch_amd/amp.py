@@ -334,12 +334,19 @@ class GradScaler:
             for gradient in grads:
                 if gradient._pending is not None:
                     gradient._materialize()
-        for gradient in grads:
+        counters = tuple(map(_COUNTER, grads))
+        for gradient, counter in zip(grads, counters):
             gradient._pending = transform
-            gradient._version_counter.value += 1
-        state["finite"] = self._finite(gradients)
-        for gradient in grads:
-            gradient._finite_version = gradient._version_counter.value
+            counter.value += 1
+        # The check below is of these versions; they are stamped before its
+        # wait for the device (and restored if it raises).
+        stamped = tuple(map(_FINITE_VERSION, grads))
+        deque(map(setattr, grads, repeat("_finite_version"), map(_VALUE, counters)), 0)
+        try:
+            state["finite"] = self._finite(gradients)
+        except BaseException:
+            deque(map(setattr, grads, repeat("_finite_version"), stamped), 0)
+            raise
         state["stage"] = "unscaled"
         return state["finite"]
 

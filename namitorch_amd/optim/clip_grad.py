@@ -170,9 +170,11 @@ def _stats_key(gradients) -> frozenset:
     return frozenset(zip(map(id, gradients), map(_VERSION_VALUE, gradients), map(id, map(_PENDING, gradients))))
 
 
-def _remember_stats(gradients, stats: GradStats) -> None:
+def _remember_stats(key: frozenset, gradients, stats: GradStats) -> None:
+    """Cache `stats` under `key`, the ``_stats_key`` of `gradients` taken
+    when the pre-pass was queued."""
     _last_stats.clear()
-    _last_stats[_stats_key(gradients)] = (list(gradients), list(map(_PENDING, gradients)), stats)
+    _last_stats[key] = (list(gradients), list(map(_PENDING, gradients)), stats)
 
 
 _DEVICE = attrgetter("_device")
@@ -201,6 +203,7 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
     also, per (backend, dtype) group, its members, control block and scale."""
     stats = GradStats()
     blocks = {}
+    launched = []
     for (backend, dtype), members in _device_groups(gradients).items():
         if backend.adamw is None:
             backend._unsupported("Gradient norms")
@@ -221,11 +224,15 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
         block = backend.empty_ctrl()                     # written whole by the finalize
         backend.grad_prepass(plan, scale)
         backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0, carry_ptr=backend.neutral_ctrl().data_ptr())
+        launched.append((backend, dtype, members, block, scale))
+    # Host work that does not need the results runs while the device works.
+    key = _stats_key(gradients) if remember else None
+    for backend, dtype, members, block, scale in launched:
         ctrl = backend.read_ctrl(block)
         stats.merge(GradStats(ctrl.sumsq, ctrl.amax, bool(ctrl.has_nan), bool(ctrl.found_inf and not ctrl.has_nan)))
         blocks[(backend, dtype)] = (members, block, scale)
     if remember:
-        _remember_stats(gradients, stats)
+        _remember_stats(key, gradients, stats)
     return stats, blocks
 
 
