@@ -206,7 +206,9 @@ int32_t nt_empty_cache(int32_t device);
 int32_t nt_host_alloc(uint64_t bytes, void **out);
 int32_t nt_host_free(void *ptr);
 /* Streams are created at the default priority and do not synchronize with
- * the null stream. */
+ * the null stream.  nt_stream_destroy waits for the stream's work first;
+ * plans and pool blocks that were used on it may still be destroyed or
+ * freed afterwards, in any order. */
 int32_t nt_stream_create(int32_t device, void **out);
 int32_t nt_stream_destroy(void *stream);
 int32_t nt_stream_wait_event(void *stream, void *event);

@@ -58,7 +58,6 @@ class DeviceStep:
         self.unscale = unscale
         self.honor_skip = honor_skip
         self.records: list = []
-        self.optimizers: set = set()
         self.clip_bumps = clip_bumps          # (gradient, version after the optimistic clip bump)
         self.snapshot = runtime.take_pinned(ctypes.sizeof(_native.AmpCtrl))
         self.event = runtime.Event()
@@ -148,8 +147,9 @@ class DeviceStep:
         self.records.clear()
         self._reconciled = True
         self._forget()
-        if self.scheduler is not None and not (self.honor_skip and ctrl.skip):
-            self.scheduler._advance()         # training/runner.py:252-253: only after an update
+        scheduler, self.scheduler = self.scheduler, None    # no reference cycle through it once settled
+        if scheduler is not None and not (self.honor_skip and ctrl.skip):
+            scheduler._advance()              # training/runner.py:252-253: only after an update
 
 
 class StepResult:

@@ -138,6 +138,10 @@ HostPool &host_pool();
 // Validate a plan pointer.
 int32_t check_plan(const nt_plan *plan);
 
+// True when `stream` was destroyed by nt_stream_destroy (after all its work
+// completed) and its handle has not been handed out again.
+bool stream_destroyed(void *stream);
+
 // Remember that `stream` uses `plan` (see nt_plan::others).
 inline void note_stream(nt_plan *plan, void *stream) {
     const hipStream_t s = (hipStream_t)stream;

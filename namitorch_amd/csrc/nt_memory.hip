@@ -9,10 +9,40 @@
 // (they are never destroyed, so no HIP call runs during static teardown).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <unordered_set>
+
 #include "nt_internal.hpp"
 #include "nt_pool.hpp"
 
 namespace nt {
+namespace {
+
+// Streams that nt_stream_destroy has destroyed, each after waiting for all
+// its work, until HIP hands the same handle out again (nt_stream_create).
+// A plan or pool block used on such a stream may be released later (objects
+// are finalized in any order when a reference cycle is collected): its
+// release needs no ordering after that stream, and an event must not be
+// recorded on a destroyed handle.
+struct DestroyedStreams {
+    std::mutex lock;
+    std::unordered_set<void *> handles;
+};
+
+DestroyedStreams &destroyed_streams() {
+    static DestroyedStreams *streams = new DestroyedStreams();   // never destroyed, like the pools
+    return *streams;
+}
+
+}  // namespace
+
+bool stream_destroyed(void *stream) {
+    if (stream == nullptr) return false;
+    DestroyedStreams &d = destroyed_streams();
+    std::lock_guard<std::mutex> guard(d.lock);
+    return d.handles.count(stream) != 0;
+}
+
 namespace {
 
 class HipOps final : public PoolOps {
@@ -50,6 +80,9 @@ class HipOps final : public PoolOps {
             (void)hipGetLastError();
             return nullptr;
         }
+        // A destroyed stream's work has completed: an event never recorded
+        // reads as complete.
+        if (stream_destroyed(stream)) return event;
         if (hipEventRecord(event, (hipStream_t)stream) != hipSuccess) {
             (void)hipGetLastError();
             (void)hipEventDestroy(event);
@@ -198,13 +231,25 @@ int32_t nt_stream_create(int32_t device, void **out) {
     if (!guard.ok()) return hip_check(guard.error(), "hipSetDevice");
     hipStream_t s = nullptr;
     NT_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    {
+        DestroyedStreams &d = destroyed_streams();
+        std::lock_guard<std::mutex> lock(d.lock);
+        d.handles.erase(s);                         // the handle is live again
+    }
     *out = s;
     return NT_OK;
 }
 
 int32_t nt_stream_destroy(void *stream) {
     clear_error();
-    if (stream != nullptr) NT_HIP_TRY(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+    if (stream == nullptr) return NT_OK;
+    // Everything queued on the stream completes first, so the plans and pool
+    // blocks that were used on it need no ordering after it any more.
+    NT_HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    NT_HIP_TRY(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+    DestroyedStreams &d = destroyed_streams();
+    std::lock_guard<std::mutex> lock(d.lock);
+    d.handles.insert(stream);
     return NT_OK;
 }
 

@@ -267,7 +267,13 @@ int32_t nt_plan_destroy(nt_plan *plan) {
         (void)hipDeviceSynchronize();
     }
     host_pool().give(plan->h_staging, plan->host_bytes, std::move(after));
-    for (int r = 0; r < kRingSlots; ++r) (void)hipEventDestroy(plan->ring_events[r]);
+    // The ring's events were recorded on the plan's streams.  When one of
+    // those streams is already destroyed (a reference cycle finalized it
+    // first), the four events are left to the process rather than destroyed.
+    bool streams_alive = !stream_destroyed(plan->stream);
+    for (hipStream_t other : plan->others) streams_alive = streams_alive && !stream_destroyed(other);
+    if (streams_alive)
+        for (int r = 0; r < kRingSlots; ++r) (void)hipEventDestroy(plan->ring_events[r]);
     delete plan;
     (void)hipGetLastError();   // teardown is best effort; leave no error for a later launch check
     return NT_OK;

@@ -294,7 +294,6 @@ class Adam(_FirstOrderOptimizer):
                 # what to undo on the host if it was.
                 device_step.records.append((parameter, state, first, second, master, step, bumped, moves))
         if device_step is not None:
-            device_step.optimizers.add(self)
             self._consume_device_step(device_step)
 
     def _memoize_step(self, options: dict) -> None:
@@ -585,7 +584,6 @@ class _Replay:
         if device_step is not None:
             device_step.records.extend(zip(self.members, self.dicts, self.firsts, self.seconds, self.masters, steps,
                                            self.bumped, map(moves.__getitem__, self.member_groups)))
-            device_step.optimizers.add(optimizer)
             optimizer._consume_device_step(device_step)
         return True
 

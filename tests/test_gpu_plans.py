@@ -205,3 +205,47 @@ def test_plan_cache_churn_across_streams_matches_oracle():
             assert state["exp_avg"].numpy().tobytes() == ref_m[i].tobytes()
             assert state["exp_avg_sq"].numpy().tobytes() == ref_v[i].tobytes()
             assert state["step"] == 3
+
+
+def test_stream_destroyed_before_its_plan_and_block():
+    """When a reference cycle is collected, Python finalizes its objects in
+    any order, so a library stream can be destroyed before a plan built on it
+    and before a pool block used on it.  Destroying the plan and freeing the
+    block afterwards must not use the destroyed stream (nt_stream_destroy
+    waits for the stream's work, so they need no ordering after it).  A step
+    on a new stream, which may get the same handle, then matches the first."""
+    import gc
+    from namitorch_amd import _native
+    backend = nt.get_backend(DEV)
+    host = (np.random.default_rng(3).standard_normal(6000) * 0.02).astype(np.float32)
+    grad = np.full(6000, 1e-3, np.float32)
+
+    def two_steps():
+        param = nt.Parameter(host, device=DEV)
+        optimizer = nt.optim.AdamW([param], lr=1e-3)
+        for _ in range(2):
+            param.grad = nt.Tensor(grad, device=DEV)   # a new gradient: the plan's column is rewritten on the stream
+            optimizer.step()
+        return param, optimizer
+
+    stream = nt.runtime.Stream(0)
+    with nt.runtime.stream(stream):
+        param, optimizer = two_steps()
+        values = param.numpy()
+    block = nt.DeviceArray.empty((4096,), nt.float32, DEV)    # allocated on the default stream
+    block.record_stream(stream.handle)
+    keys = [key for key in backend._plans if key[2] == stream.handle]
+    assert keys
+    print(f"destroying stream {stream.handle:#x} before {len(keys)} plan(s) and one block", flush=True)
+    _native.call("nt_stream_destroy", stream.handle)          # what finalizing the Stream first does
+    stream._owned = False
+    for key in keys:
+        del backend._plans[key]
+    del optimizer, param                                       # the step memo held the plan
+    gc.collect()
+    del block
+    fresh = nt.runtime.Stream(0)
+    with nt.runtime.stream(fresh):
+        again, _ = two_steps()
+        assert again.numpy().tobytes() == values.tobytes()
+    fresh.synchronize()
