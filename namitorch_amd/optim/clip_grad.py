@@ -292,6 +292,9 @@ def _norm_tensor(norm: float, gradients) -> Tensor:
 def get_grad_norm(parameters, norm_type: float = 2) -> Tensor:
     order = _norm_type(norm_type)
     gradients = _gradients(parameters)
+    launched = _norm_on_device(gradients, order, -1.0)
+    if launched is not None:
+        return Tensor._from_storage(launched[2], False)       # read on the device; .item() waits
     return _norm_tensor(_total_norm(gradients, order), gradients)
 
 
@@ -308,26 +311,21 @@ _VALUE = attrgetter("value")
 _UNSETTLED_LIMIT = 64
 
 
-def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
-    """``clip_grad_norm_`` with the norm, the clip decision and the
-    coefficient left on the device, so the host does not wait: the pre-pass
-    and finalize of a fused step without a scaler, whose finalize applies
-    the reference's rule (clip when ``max_norm / (norm + 1e-6) < 1``, also
-    for a non-finite norm).  The gradients get a device-decided clip
-    transform that the next kernel reading them applies (the AdamW pass, or
-    the write-back when a gradient is read), and the result is the device's
-    norm.  The reference's version bump happens only when the coefficient is
-    below 1: it is taken optimistically and undone when the step is settled.
+def _norm_on_device(gradients, order: float, maximum: float):
+    """Queue the pre-pass and a finalize over `gradients` and a device copy
+    of the norm, with no host wait: (backend, control block, 0-d float64
+    norm array), or None when the host path must answer.  With `maximum`
+    >= 0 the finalize also takes the clip decision by the reference's rule
+    (clip when ``max_norm / (norm + 1e-6) < 1``, also for a non-finite
+    norm).
 
-    None (the host path decides) unless no host decision of the reference
-    can raise or differ: norm_type 2 or inf; one device and one float16,
-    bfloat16 or float32 gradient dtype; nothing pending on the gradients;
-    every gradient writable, so a rewrite cannot fail; and no cached
-    statistics for them (then the host path answers without waiting).
-    """
+    Eligible: norm_type 2 or inf; one device and one float16, bfloat16 or
+    float32 gradient dtype (float64 may need the prescaled second pass);
+    nothing pending on the gradients; and no cached statistics for them
+    (then the host path answers without waiting)."""
     if order != 2.0 and not math.isinf(order):
         return None
-    if not gradients or any(map(_PENDING, gradients)) or not all(map(_WRITABLE, gradients)):
+    if not gradients or any(map(_PENDING, gradients)):
         return None
     if _last_stats and _stats_key(gradients) in _last_stats:
         return None
@@ -337,15 +335,36 @@ def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
     (backend, dtype), _ = next(iter(groups.items()))
     if backend.adamw is None or dtype is float64:
         return None
-    reject_during_capture("Host Tensor reads")           # as the host path: no clipping under capture
-    from ..amp import DeviceStep                         # the amp module imports this one
-    from ..tensor import _unsettled_steps
+    reject_during_capture("Host Tensor reads")           # as the host path: nothing under capture
     plan = backend.grad_plan(gradients, dtype, incoming=True)
     neutral = backend.neutral_ctrl()
     block = backend.empty_ctrl()                         # written whole by the finalize
     backend.grad_prepass(plan, None, neutral.data_ptr())
     backend.grad_finalize(plan, block.data_ptr(), order, maximum, 0, carry_ptr=neutral.data_ptr())
-    norm = backend.ctrl_norm(block)
+    return backend, block, backend.ctrl_norm(block)
+
+
+def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
+    """``clip_grad_norm_`` with the norm, the clip decision and the
+    coefficient left on the device, so the host does not wait
+    (``_norm_on_device``).  The gradients get a device-decided clip
+    transform that the next kernel reading them applies (the AdamW pass, or
+    the write-back when a gradient is read), and the result is the device's
+    norm.  The reference's version bump happens only when the coefficient is
+    below 1: it is taken optimistically and undone when the step is settled.
+
+    None (the host path decides) unless no host decision of the reference
+    can raise or differ: ``_norm_on_device``'s conditions, and every
+    gradient writable, so a rewrite cannot fail.
+    """
+    if not all(map(_WRITABLE, gradients)):
+        return None
+    launched = _norm_on_device(gradients, order, maximum)
+    if launched is None:
+        return None
+    backend, block, norm = launched
+    from ..amp import DeviceStep                         # the amp module imports this one
+    from ..tensor import _unsettled_steps
     clip_bumps: list = []
     device_step = DeviceStep(backend, block, unscale=False, honor_skip=False, clip_bumps=clip_bumps)
     device_step.clip_requested = True

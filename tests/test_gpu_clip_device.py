@@ -261,3 +261,39 @@ def test_clip_on_one_stream_step_on_another():
     two_values, two_moments = run(True)
     for a, b in zip(one_values + one_moments, two_values + two_moments):
         assert _same(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("norm_type", [2.0, math.inf])
+@pytest.mark.parametrize("bad", [None, "inf", "nan"])
+def test_get_grad_norm_on_device(dtype, norm_type, bad):
+    """get_grad_norm without a host wait: the norm's bits equal the host
+    path's (an unclipping clip_grad_norm_ with error_if_nonfinite=True, or
+    the reference's NaN/inf), nothing is recorded on the gradients, and a
+    following clip_grad_norm_ gives the host path's result."""
+    grads = _grads(29, dtype)
+    if bad is not None:
+        grads[0].reshape(-1)[3] = float(bad)
+    params = _params(grads, dtype)
+    versions = [p.grad._version for p in params]
+    norm = nt.optim.get_grad_norm(params, norm_type=norm_type)
+    assert norm.dtype is nt.float64 and norm.shape == () and norm.device.type == "cuda"
+    assert all(p.grad._pending is None for p in params)
+    assert [p.grad._version for p in params] == versions
+    want = oclip.total_norm([g.astype(np.float64) for g in grads], norm_type)
+    got = norm.item()
+    if bad is None:
+        host = _params(grads, dtype)
+        host_norm = nt.optim.clip_grad_norm_(host, 1e300, norm_type=norm_type, error_if_nonfinite=True).item()
+        assert _bits(np.float64(got)) == _bits(np.float64(host_norm)), (got, host_norm)
+        assert abs(got - want) <= NORM_RTOL * want
+        clipped = nt.optim.clip_grad_norm_(params, want / 3, norm_type=norm_type).item()
+        assert _bits(np.float64(clipped)) == _bits(np.float64(got))
+        coefficient = oclip.clip_coefficient(want / 3, got)
+        for p, g in zip(params, grads):
+            expected = np.asarray(oclip.clip_apply(g.astype(np.float64), coefficient, dtype))
+            assert _same(p.grad.numpy(), expected.astype(p.grad.numpy().dtype))
+    elif bad == "nan":
+        assert math.isnan(got) and math.isnan(want)
+    else:
+        assert got == want == math.inf
