@@ -23,6 +23,8 @@ per run, so at most two elements per array may differ by one unit).
 
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 import pytest
 
@@ -164,3 +166,98 @@ def test_random_amp_sequence(seed, tmp_path):
         _close(f"v[{i}]", state["exp_avg_sq"].numpy(), v2[i], loose)
     assert scheduler.get_last_lr()[0] == rates_owner.param_groups[0]["lr"]
     assert optimizer.param_groups[0]["lr"] == rates_owner.param_groups[0]["lr"]
+
+
+CLIP_CASES = 24
+
+
+@pytest.mark.parametrize("seed", range(CLIP_CASES))
+def test_random_clip_sequence_without_scaler(seed, tmp_path):
+    """Seeded runs without a GradScaler, mixing per step ``clip_grad_norm_``
+    -> ``step`` (the clip decided on the device when nothing is pending),
+    ``fused_step(optimizer, None, max_norm=...)`` and plain steps.  Along the
+    way they read ``get_grad_norm``, step on a second library stream, and
+    round-trip state dicts or resume from a checkpoint archive into new
+    objects.  Oracle: ``clip.clip_grad_norm`` -> ``adam.master_step`` /
+    ``adam.adam_step``.  Bars as above; the returned norms within 1e-12 of
+    the oracle's."""
+    rng = np.random.default_rng(9500 + seed)
+    master = bool(rng.random() < 0.5)
+    dtype = "bfloat16" if master else "float32"
+    gdtype = str(rng.choice(["bfloat16", "float16"])) if master else "float32"
+    shapes = [(int(rng.choice(SIZES)),) for _ in range(int(rng.integers(1, 4)))]
+    hosts = [rng.standard_normal(s) * 0.02 for s in shapes]
+    hosts = [lowp.round_to("bfloat16", h) if master else h.astype(np.float32) for h in hosts]
+    params = [nt.Parameter(h, dtype=dtype, device=DEV) for h in hosts]
+    optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.05, master_weights=master)
+    values = [h.astype(np.float32).copy() for h in hosts]
+    m = [np.zeros_like(v) for v in values]
+    v2 = [np.zeros_like(v) for v in values]
+    side = nt.runtime.Stream(0)
+    count, loose, log = 0, False, []
+    for step in range(STEPS):
+        path = str(rng.choice(["api", "fused", "plain"]))
+        max_norm = None if path == "plain" else float(rng.choice([1e-3, 0.02, 10.0]))
+        grads = [rng.standard_normal(s) * 1e-3 for s in shapes]
+        stored = [lowp.round_to(gdtype, g) if gdtype != "float32" else g.astype(np.float32) for g in grads]
+        # Oracle.
+        used = [np.asarray(s, np.float64) for s in stored]
+        want_norm = oclip.total_norm(used)
+        if max_norm is not None:
+            norm, used = oclip.clip_grad_norm(used, max_norm, 2.0, gdtype)
+            loose |= oclip.clip_coefficient(max_norm, norm) < 1
+        count += 1
+        for i, g in enumerate(used):
+            kw = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.05)
+            if master:
+                oadam.master_step(values[i], np.asarray(g, np.float32), m[i], v2[i], count, **kw)
+            else:
+                oadam.adam_step(values[i], np.asarray(g, np.float32), m[i], v2[i], count, **kw)
+        # Device.
+        on_side = rng.random() < 0.2
+        if on_side:
+            # The caller orders its own streams: the side stream starts after the default stream's work.
+            side.wait_stream(nt.runtime.Stream.wrap(nt.runtime.current_stream(0)))
+        with (nt.runtime.stream(side) if on_side else contextlib.nullcontext()):
+            for p, s in zip(params, stored):
+                p.grad = nt.Tensor(s, dtype=gdtype, device=DEV)
+            if rng.random() < 0.3:
+                got = nt.optim.get_grad_norm(params).item()
+                assert abs(got - want_norm) <= 1e-12 * want_norm, (step, got, want_norm)
+            if path == "api":
+                got = nt.optim.clip_grad_norm_(params, max_norm)
+                optimizer.step()
+                if rng.random() < 0.5:
+                    assert abs(got.item() - want_norm) <= 1e-12 * want_norm, (step, got.item(), want_norm)
+            elif path == "fused":
+                result = nt.amp.fused_step(optimizer, None, max_norm=max_norm)
+                if rng.random() < 0.5:
+                    assert abs(result.norm - want_norm) <= 1e-12 * want_norm, (step, result.norm, want_norm)
+            else:
+                optimizer.step()
+        if on_side:
+            side.synchronize()
+        if rng.random() < 0.5:
+            assert optimizer.state[id(params[0])].get("step", 0) == count, (step, path)
+        if rng.random() < 0.15:
+            optimizer.load_state_dict(optimizer.state_dict())
+            log.append("reload")
+        if rng.random() < 0.12:
+            archive = str(tmp_path / f"step{step}.nt")
+            nt.save_checkpoint(archive, {f"p{i}": p for i, p in enumerate(params)}, optimizer, None, step=step + 1)
+            params = [nt.Parameter(np.zeros(s, np.float32), dtype=dtype, device=DEV) for s in shapes]
+            optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.05, master_weights=master)
+            nt.load_checkpoint(archive, {f"p{i}": p for i, p in enumerate(params)}, optimizer, None)
+            log.append("checkpoint")
+        log.append(f"{path}{'s' if on_side else ''}{'' if max_norm is None else 'c'}")
+    print(f"case {seed}: master={master} g={gdtype} shapes={shapes} {log}", flush=True)
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        assert state["step"] == count, i
+        if master:
+            _close(f"master[{i}]", state["master"].numpy(), values[i], loose)
+            _close(f"param[{i}] bf16", p.numpy(), lowp.round_to("bfloat16", values[i].astype(np.float64)), loose)
+        else:
+            _close(f"param[{i}]", p.numpy(), values[i], loose)
+        _close(f"m[{i}]", state["exp_avg"].numpy(), m[i], loose)
+        _close(f"v[{i}]", state["exp_avg_sq"].numpy(), v2[i], loose)
