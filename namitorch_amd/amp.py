@@ -45,6 +45,7 @@ _PARAMETER_AND_GRADIENT = itemgetter(1, 2)
 _THIRD_OF = itemgetter(2)
 _FINITE_VERSION = attrgetter("_finite_version")
 _VERSION_VALUE = attrgetter("_version_counter.value")
+_GRAD = attrgetter("_grad")
 
 
 class DeviceStep:
@@ -302,6 +303,22 @@ class GradScaler:
         return gradients
 
     @staticmethod
+    def _entry_inputs(optimizer):
+        """What an optimizer's gradient entries are a pure function of
+        (``Optimizer._grad_entries``): its registered-parameter cache (a new
+        object whenever the groups change), the parameters' requires_grad
+        flags and their gradient objects; None for an optimizer without that
+        cache."""
+        registered_of = getattr(optimizer, "_registered_parameters", None)
+        if not callable(registered_of) or not callable(getattr(optimizer, "_grad_entries", None)):
+            return None
+        registered = registered_of()
+        cache = getattr(optimizer, "__dict__", {}).get("_registered_cache")
+        if cache is None:
+            return None
+        return cache, tuple(map(_REQUIRES, registered)), tuple(map(_GRAD, registered))
+
+    @staticmethod
     def _finite(gradients) -> bool:
         """All elements of all gradients finite (amp.py:152-167), on the device."""
         stats, _ = grad_stats([gradient for _, gradient in gradients])
@@ -323,7 +340,8 @@ class GradScaler:
         previous = {id(parameter) for state in self._optimizer_states.values() for parameter, _ in state["gradients"]}
         if previous and any(id(parameter) in previous for parameter, _ in gradients):
             raise RuntimeError("Optimizers cannot share gradients in the same GradScaler iteration.")
-        state = {"optimizer": optimizer, "stage": "unscaling", "gradients": gradients, "finite": False}
+        state = {"optimizer": optimizer, "stage": "unscaling", "gradients": gradients, "finite": False,
+                 "inputs": self._entry_inputs(optimizer)}
         self._optimizer_states[identity] = state
         transform = GradTransform(scale=self._scale)
         grads = tuple(map(_SECOND_OF, gradients))
@@ -361,12 +379,23 @@ class GradScaler:
         state = self._optimizer_states[identity]
         if state["stage"] != "unscaled":
             raise RuntimeError("step() may be called only once per optimizer before update().")
-        current = self._gradients(optimizer)
         previous = state["gradients"]
-        grads = tuple(map(_SECOND_OF, current))
-        if len(current) != len(previous) or not (all(map(is_, map(_FIRST_OF, current), map(_FIRST_OF, previous)))
-                                                 and all(map(is_, grads, map(_SECOND_OF, previous)))):
-            raise RuntimeError("Optimizer gradients changed after unscale_; clipping must modify the existing gradients in-place.")
+        inputs, current = state["inputs"], None
+        if inputs is not None:
+            # The entries are those of unscale_ when what they are a function
+            # of is unchanged (three passes instead of collecting them again).
+            now = self._entry_inputs(optimizer)
+            if now is not None and now[0] is inputs[0] and now[1] == inputs[1] and all(map(is_, now[2], inputs[2])):
+                current = previous
+                grads = tuple(map(_SECOND_OF, current))
+                if any(map(_REQUIRES, grads)):
+                    raise RuntimeError("GradScaler requires detached floating gradients.")
+        if current is None:
+            current = self._gradients(optimizer)
+            grads = tuple(map(_SECOND_OF, current))
+            if len(current) != len(previous) or not (all(map(is_, map(_FIRST_OF, current), map(_FIRST_OF, previous)))
+                                                     and all(map(is_, grads, map(_SECOND_OF, previous)))):
+                raise RuntimeError("Optimizer gradients changed after unscale_; clipping must modify the existing gradients in-place.")
         # Finite as checked by unscale_ unless something else wrote a gradient since.
         unchanged = all(map(eq, map(_FINITE_VERSION, grads), map(_VERSION_VALUE, grads)))
         now_finite = state["finite"] if unchanged else self._finite(current)

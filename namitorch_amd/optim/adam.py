@@ -312,6 +312,7 @@ _GRAD = attrgetter("_grad")
 _REQUIRES = attrgetter("_requires_grad")
 _WRITABLE = attrgetter("_writable")
 _PENDING = attrgetter("_pending")
+_INCOMING = attrgetter("_incoming")
 _CLEAN = attrgetter("_clean_version")
 _VALUE = attrgetter("value")
 _COUNTER = attrgetter("_version_counter")
@@ -482,10 +483,10 @@ class _Replay:
         if tuple(map(_REQUIRES, registered)) != self.requires:
             return False
         current = tuple(map(_GRAD, registered))
-        if any(map(getattr, current, repeat("_incoming"), repeat(None))):
-            return False                                        # the full step adds deferred accumulations
         if not all(map(is_, current, self.grads)) and not self._adopt(optimizer, current):
             return False
+        if any(map(_INCOMING, self.member_grads)):
+            return False                                        # the full step adds deferred accumulations
         state = optimizer.state
         if state is not self.state:
             return False
