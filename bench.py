@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c1,c3,c4,c5,c4s8,c5s8,ceilings] [--no-cpu]
 
-Headline (the JSON line's ``value``): BASELINE config 2 — multi-tensor fp32
+Headline (the JSON line's ``value``): configuration C2 — multi-tensor fp32
 AdamW over the GPT-2-124M parameter list (148 tensors, 124,439,808 params,
 weight decay 0.1 on matrices and 0 on vectors, lr 3e-4, betas (0.9, 0.999),
 eps 1e-8), one ``optimizer.step()`` through the public API per step, inputs
@@ -17,7 +17,7 @@ rocprofv3 PMC summary when present.  ``cpu_baseline`` times the NumPy oracle
 (the reference's NumPy path restated op for op) on a bounded sample of the
 same workload on this host, one core.
 
-The other BASELINE configs (C1 flat 4M fp32 hot and MALL-flushed, C3 AMP
+The other configurations (C1 flat 4M fp32 hot and MALL-flushed, C3 AMP
 GPT-2, C4 GPT-1.3B bf16 + clip, C5 Llama-7B AMP + clip) are reported under
 ``extra`` with their own B/param accounting, together with one GPU's share
 of an 8-way sharded C4 and C5 step (``c4s8``, ``c5s8``: every tensor split
@@ -66,7 +66,10 @@ def parse_args():
                         help="with --kernel-only or --profile: also run 3 plain 1 GiB device copies (known bytes, "
                              "for PMC scaling)")
     parser.add_argument("--profile", default=None, choices=sorted(MIXED),
-                        help="only this config's fused step (for profilers): --warmup untimed, --steps timed")
+                        help="only this config's step (for profilers): --warmup untimed, --steps timed")
+    parser.add_argument("--profile-modes", default="fused",
+                        help="with --profile: the step paths to run in turn, 'fused' and/or 'api' (the reference "
+                             "call sequence), comma-separated")
     return parser.parse_args()
 
 
@@ -538,7 +541,7 @@ def bench_shape_sweep(nt, torch, launches=8, warmup=2, rounds=5):
 def bench_chunks(nt, torch, launches=20, reps=4):
     """The AdamW pass with 4096- and 2048-element tasks, timed alternately in
     one process on the same buffers (so both see the same physical
-    placement), for each BASELINE layout; the optimizer picks the chunk per
+    placement), for each configuration's layout; the optimizer picks the chunk per
     layout (optim/adam.py _pass_chunk).  Both run the same one-wave
     256-element workgroups; the task size sets the task map and the tails.  Random N(0, 0.02) params, N(0, 1e-3)
     grads, zero moments; C4/C5 launches carry their clip (and unscale)
@@ -831,9 +834,12 @@ def main():
     extra = {}
     if args.profile:
         key, spec = _mixed_configs(nt)[args.profile]
-        spec = dict(spec, modes=("fused",))
+        modes = tuple(args.profile_modes.split(","))
+        if not modes or any(mode not in ("fused", "api") for mode in modes):
+            raise SystemExit("--profile-modes takes 'fused' and/or 'api', comma-separated")
+        spec = dict(spec, modes=modes)
         shapes = spec.pop("shapes")
-        log(f"{args.profile} fused step only ({args.warmup} untimed, {args.steps} timed)")
+        log(f"{args.profile} {' then '.join(modes)} steps only ({args.warmup} untimed, {args.steps} timed each)")
         if args.calibrate:
             log(f"calibration copies: {calibration_copies(torch)}")
         print(json.dumps({key: bench_mixed(nt, torch, args.profile, shapes, steps=args.steps, warmup=args.warmup,

@@ -17,7 +17,7 @@ pool by ``oracle.parallel``, which gives the oracle's bits):
   with 2 layers (207.9 M parameters): float32 master, bfloat16
   parameters/moments/gradients, clip_grad_norm_ at 1.0 (active every step).
 
-Bars: found_inf flags, skip decisions and the
+Bars (the path's target tolerances): found_inf flags, skip decisions and the
 loss-scale sequence bit-exact; norms within 1e-12 relative; float32 master,
 parameters and moments bit-exact, and model copies and bfloat16 moments
 equal to the oracle's RNE values.  A clip coefficient one float64 ulp away
