@@ -73,7 +73,7 @@ def _norm_type(value: object) -> float:
 
 _GRAD_OF = attrgetter("_grad")
 _DEVICE_OF = attrgetter("_device")
-_SHAPE_OF = attrgetter("shape")
+_SHAPE_OF = attrgetter("_shape")
 _FLOATING_OF = attrgetter("_dtype._floating")
 
 
@@ -153,7 +153,8 @@ class GradStats:
 
 
 # Statistics of the last device pre-pass, reused by clip_grad_norm_ when it
-# sees the same gradients at the same versions with the same pending transform.
+# sees the same gradients at the same versions with the same pending
+# transform: at most one entry, (snapshot, stats) under the key "last".
 _last_stats: dict = {}
 
 
@@ -161,20 +162,35 @@ _PENDING = attrgetter("_pending")
 _VERSION_VALUE = attrgetter("_version_counter.value")
 _FINITE_VERSION = attrgetter("_finite_version")
 _COUNTER = attrgetter("_version_counter")
+_VALUE_OF = attrgetter("value")
 
 
-def _stats_key(gradients) -> frozenset:
-    """(gradient, version, pending transform) of every gradient, by identity.
-    The cache entry holds the gradients and their transforms, so the
-    identities in a stored key cannot be reused by other objects."""
-    return frozenset(zip(map(id, gradients), map(_VERSION_VALUE, gradients), map(id, map(_PENDING, gradients))))
+def _stats_snapshot(gradients) -> tuple:
+    """The gradients (held, so their identities cannot be reused), the set
+    of their identities, their version counters with the values they hold,
+    and their pending transforms."""
+    held = tuple(gradients)
+    counters = tuple(map(_COUNTER, held))
+    return held, frozenset(map(id, held)), counters, tuple(map(_VALUE_OF, counters)), tuple(map(_PENDING, held))
 
 
-def _remember_stats(key: frozenset, gradients, stats: GradStats) -> None:
-    """Cache `stats` under `key`, the ``_stats_key`` of `gradients` taken
-    when the pre-pass was queued."""
+def _remember_stats(snapshot: tuple, stats: GradStats) -> None:
+    """Cache `stats` with the ``_stats_snapshot`` taken when the pre-pass was queued."""
     _last_stats.clear()
-    _last_stats[key] = (list(gradients), list(map(_PENDING, gradients)), stats)
+    _last_stats["last"] = (snapshot, stats)
+
+
+def _cached_stats(gradients) -> GradStats | None:
+    """The cached statistics when `gradients` are the cached set (in any
+    order) at the same versions with the same pending transforms."""
+    entry = _last_stats.get("last")
+    if entry is None:
+        return None
+    (held, ids, counters, versions, pendings), stats = entry
+    if (len(gradients) != len(held) or frozenset(map(id, gradients)) != ids
+            or tuple(map(_VALUE_OF, counters)) != versions or not all(map(is_, map(_PENDING, held), pendings))):
+        return None
+    return stats
 
 
 _DEVICE = attrgetter("_device")
@@ -226,13 +242,13 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
         backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0, carry_ptr=backend.neutral_ctrl().data_ptr())
         launched.append((backend, dtype, members, block, scale))
     # Host work that does not need the results runs while the device works.
-    key = _stats_key(gradients) if remember else None
+    snapshot = _stats_snapshot(gradients) if remember else None
     for backend, dtype, members, block, scale in launched:
         ctrl = backend.read_ctrl(block)
         stats.merge(GradStats(ctrl.sumsq, ctrl.amax, bool(ctrl.has_nan), bool(ctrl.found_inf and not ctrl.has_nan)))
         blocks[(backend, dtype)] = (members, block, scale)
     if remember:
-        _remember_stats(key, gradients, stats)
+        _remember_stats(snapshot, stats)
     return stats, blocks
 
 
@@ -256,10 +272,9 @@ def _total_norm(gradients: list[Tensor], norm_type: float) -> float:
     reject_during_capture("Host Tensor reads")          # the norm comes back to the host
     if not gradients:
         return 0.0
-    key = _stats_key(gradients)
-    cached = _last_stats.get(key)
+    cached = _cached_stats(gradients)
     if cached is not None and (norm_type == 2 or math.isinf(norm_type)):
-        stats, blocks = cached[2], None
+        stats, blocks = cached, None
     else:
         stats, blocks = grad_stats(gradients)
     scale = stats.prescale()
@@ -327,7 +342,7 @@ def _norm_on_device(gradients, order: float, maximum: float):
         return None
     if not gradients or any(map(_PENDING, gradients)):
         return None
-    if _last_stats and _stats_key(gradients) in _last_stats:
+    if _cached_stats(gradients) is not None:
         return None
     groups = _device_groups(gradients)
     if len(groups) != 1:

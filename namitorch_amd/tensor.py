@@ -295,8 +295,8 @@ def _assign_host(target: np.ndarray, source: object, dtype: DType, source_dtype:
 class Tensor:
     __slots__ = (
         "_storage", "_dtype", "_device", "_requires_grad", "_grad", "_version_counter",
-        "_writable", "_pending", "_incoming", "_is_leaf", "_ptr", "_numel", "_clean_version", "_finite_version",
-        "__weakref__",
+        "_writable", "_pending", "_incoming", "_is_leaf", "_ptr", "_numel", "_shape", "_clean_version",
+        "_finite_version", "__weakref__",
     )
 
     def __init__(self, data: object, dtype: object = None, requires_grad: builtins.bool = False, *, device=None):
@@ -331,6 +331,7 @@ class Tensor:
             self._ptr = storage.data_ptr()
             self._numel = storage.numel()
         self._storage = storage
+        self._shape = tuple(storage.shape)     # storage is fixed for the Tensor's life
         self._dtype = kind
         if requires_grad and not self._dtype.can_require_grad:
             raise TypeError(f"Only floating Tensors can require gradients, got {self._dtype.name}.")
@@ -380,11 +381,11 @@ class Tensor:
 
     @property
     def shape(self) -> tuple[int, ...]:
-        return tuple(self._storage.shape)
+        return self._shape
 
     @property
     def ndim(self) -> int:
-        return len(self._storage.shape)
+        return len(self._shape)
 
     @property
     def size(self) -> int:
