@@ -45,7 +45,7 @@ _REQUIRES = attrgetter("_requires_grad")
 _GRAD = attrgetter("_grad")
 _DTYPE = attrgetter("_dtype")
 _DEVICE = attrgetter("_device")
-_STORAGE_SHAPE = attrgetter("_storage.shape")
+_SHAPE = attrgetter("_shape")
 _PARAMS = itemgetter("params")
 _FIRST_OF = itemgetter(0)
 _SECOND_OF = itemgetter(1)
@@ -351,7 +351,7 @@ class Optimizer:
         devices = tuple(map(_DEVICE, gradients)), tuple(map(_DEVICE, parameters))
         if not (all(map(is_, *devices)) or all(map(eq, *devices))):
             return None
-        if not (all(map(eq, map(_STORAGE_SHAPE, gradients), map(_STORAGE_SHAPE, parameters)))
+        if not (all(map(eq, map(_SHAPE, gradients), map(_SHAPE, parameters)))
                 and self._gradient_dtypes_ok(parameters, gradients)):
             return None
         groups = self.param_groups
@@ -380,7 +380,7 @@ class Optimizer:
             raise TypeError("Parameter gradients must be NamiTorch Tensors.")
         if gradient._device is not parameter._device and gradient._device != parameter._device:
             ensure_same_device(parameter, gradient)       # raises the device mismatch
-        if gradient._storage.shape != parameter._storage.shape:
+        if gradient._shape != parameter._shape:
             raise ValueError(f"Gradient shape {gradient.shape} does not match parameter shape {parameter.shape}.")
         if not self._gradient_dtype_ok(parameter, gradient):
             raise TypeError(f"Gradient dtype {gradient.dtype} does not match parameter dtype {parameter.dtype}.")
