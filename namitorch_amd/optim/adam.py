@@ -37,7 +37,7 @@ from ..backends import get_backend
 from ..backends._settings import fused_kernels_enabled
 from ..backends.hip import INCOMING, incoming_pointers, make_xform
 from ..dtype import DType, bfloat16, float16, float32, float64, normalize_dtype
-from ..tensor import Tensor, _assign_host
+from ..tensor import Tensor, _assign_host, _requires_grad_changes
 from ._common import _FirstOrderOptimizer, _real_option, _round_scalar, _zeros_views
 
 _LOW_PRECISION = (float16, bfloat16, float32)
@@ -402,8 +402,8 @@ class _Replay:
     and the caller runs the full step, which builds a new memo.
     """
 
-    __slots__ = ("registered_cache", "registered", "requires", "grads", "state", "ids", "dicts", "lens", "firsts",
-                 "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
+    __slots__ = ("registered_cache", "registered", "requires", "requires_checked", "grads", "state", "ids", "dicts",
+                 "lens", "firsts", "seconds", "masters", "master_mode", "steps", "buffers", "members", "member_grads",
                  "second_counters", "fused_options", "enabled", "validate", "slots", "backend", "plan", "compute",
                  "record_type", "moment_buffers", "moment_counters", "move_counters", "member_groups", "bumped", "stream", "options_key",
                  "prepared", "adoptable", "spans", "sizes", "records")
@@ -412,6 +412,7 @@ class _Replay:
         self.registered_cache = cached
         self.registered = cached[1]
         self.requires = tuple(map(_REQUIRES, self.registered))
+        self.requires_checked = _requires_grad_changes.value     # the flags above hold at this count
         self.grads = tuple(map(_GRAD, self.registered))
         self.state = optimizer.state
         self.members = tuple(entry[0] for entry in bookkeeping)
@@ -480,7 +481,12 @@ class _Replay:
         if optimizer.__dict__.get("_registered_cache") is not self.registered_cache:
             return False
         registered = self.registered
-        if tuple(map(_REQUIRES, registered)) != self.requires:
+        # requires_grad flags are re-read only when one changed somewhere
+        # since they were last seen to hold (parameters as memoized, state
+        # buffers all False).
+        changes = _requires_grad_changes.value
+        flags_seen = changes == self.requires_checked
+        if not flags_seen and tuple(map(_REQUIRES, registered)) != self.requires:
             return False
         current = tuple(map(_GRAD, registered))
         if not all(map(is_, current, self.grads)) and not self._adopt(optimizer, current):
@@ -504,8 +510,10 @@ class _Replay:
         except KeyError:
             return False
         buffers = self.buffers
-        if any(map(_REQUIRES, buffers)) or not all(map(_WRITABLE, buffers)) or not all(map(_WRITABLE, self.members)):
+        if (not flags_seen and any(map(_REQUIRES, buffers))) or not all(map(_WRITABLE, buffers)) \
+                or not all(map(_WRITABLE, self.members)):
             return False
+        self.requires_checked = changes
         if not all(map(eq, map(_CLEAN, self.seconds), map(_VALUE, self.second_counters))):
             return False
         # Equal transforms, as the full step compares; usually one shared object.

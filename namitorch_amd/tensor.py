@@ -73,6 +73,12 @@ class _VersionCounter:
 _unsettled_steps: list = []
 
 
+# Bumped whenever ``requires_grad`` changes on an existing Tensor (its only
+# route after creation), so memoized checks of the flag can skip re-reading
+# it while the count is unchanged.
+_requires_grad_changes = _VersionCounter()
+
+
 def _settle_device_steps() -> None:
     while _unsettled_steps:
         _unsettled_steps[0].reconcile()
@@ -415,6 +421,7 @@ class Tensor:
         if not self._is_leaf:
             raise ValueError("requires_grad can only be changed on leaf tensors.")
         self._requires_grad = value
+        _requires_grad_changes.value += 1
 
     def requires_grad_(self, mode: builtins.bool = True) -> "Tensor":
         self.requires_grad = mode

@@ -315,3 +315,14 @@ def test_settled_device_step_never_stalls_the_unsettled_list():
     finally:
         _unsettled_steps[:] = [pending for pending in _unsettled_steps if pending is not step]
     assert _unsettled_steps == before
+
+
+def test_requires_grad_changes_are_counted():
+    """Every change of requires_grad on an existing Tensor moves the count
+    that memoized flag checks (the optimizer's step replay) compare."""
+    from namitorch_amd.tensor import _requires_grad_changes
+    tensor = nt.Tensor(np.zeros(3, np.float32))
+    before = _requires_grad_changes.value
+    tensor.requires_grad = True
+    tensor.requires_grad_(False)
+    assert _requires_grad_changes.value == before + 2
