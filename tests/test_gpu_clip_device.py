@@ -297,3 +297,32 @@ def test_get_grad_norm_on_device(dtype, norm_type, bad):
         assert math.isnan(got) and math.isnan(want)
     else:
         assert got == want == math.inf
+
+
+@pytest.mark.parametrize("case", ["max_norm_zero", "all_zero", "all_empty"])
+def test_device_clip_edge_cases(case):
+    """max_norm 0 (coefficient 0: every gradient becomes a signed zero), all-zero
+    gradients (norm 0: coefficient 1e6, no clip) and gradients that are all
+    empty (norm 0 over no elements): norm bits, gradients and versions as on
+    the host path and the oracle."""
+    if case == "all_empty":
+        grads = [np.zeros((0,), np.float32), np.zeros((0,), np.float32)]
+    elif case == "all_zero":
+        grads = [np.zeros(s, np.float32) for s in SHAPES]
+    else:
+        grads = _grads(31, "float32")
+    max_norm = 0.0 if case == "max_norm_zero" else 1.0
+    device = _params(grads, "float32")
+    host = _params(grads, "float32")
+    before = [p.grad._version for p in device]
+    got = nt.optim.clip_grad_norm_(device, max_norm)
+    assert all(p.grad._pending is not None and p.grad._pending.device is not None for p in device)
+    want = oclip.total_norm([g.astype(np.float64) for g in grads])
+    host_norm = nt.optim.clip_grad_norm_(host, max_norm, error_if_nonfinite=True).item()
+    assert _bits(np.float64(got.item())) == _bits(np.float64(host_norm)) and abs(got.item() - want) <= NORM_RTOL * want
+    coefficient = oclip.clip_coefficient(max_norm, got.item())
+    bump = 1 if coefficient < 1 else 0
+    assert [p.grad._version for p in device] == [b + bump for b in before] == [p.grad._version for p in host]
+    for p, q, g in zip(device, host, grads):
+        expected = oclip.clip_apply(g.astype(np.float64), coefficient, "float32") if bump else g
+        assert _same(p.grad.numpy(), expected) and _same(p.grad.numpy(), q.grad.numpy())
