@@ -561,3 +561,47 @@ def test_bf16_grad_norm_paths(scale, magnitude):
         norm = nt.optim.clip_grad_norm_([param], 1e30).item()
         want = oclip.total_norm([unscaled.astype(np.float64)])
     assert abs(norm - want) <= NORM_RTOL * want, (norm, want)
+
+
+@pytest.mark.parametrize("edit", ["new_gradient", "gradient_requires_grad", "parameter_frozen", "gradient_to_none",
+                                  "inf_written"])
+def test_scaler_step_checks_edits_after_unscale(edit):
+    """GradScaler.step after unscale_ (amp.py:196-217): a replaced, removed
+    or re-attached gradient, or a frozen parameter, raises the reference's
+    error before anything is stepped; a gradient rewritten in place (here
+    with an inf) is checked for finiteness again and skips the step, so the
+    scale backs off."""
+    import re
+    params = [nt.Parameter(np.full(300, 0.5, np.float32), device=DEV) for _ in range(3)]
+    for p in params:
+        p.grad = nt.Tensor(np.full(300, 1e-2 * 1024, np.float32), device=DEV)
+    optimizer = nt.optim.AdamW(params, lr=1e-3)
+    scaler = nt.GradScaler(init_scale=1024.0)
+    scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+    assert scaler.unscale_(optimizer) is True
+    before = [p.numpy().copy() for p in params]
+    changed = re.escape("Optimizer gradients changed after unscale_; clipping must modify the existing gradients in-place.")
+    if edit == "new_gradient":
+        params[1].grad = nt.Tensor(np.full(300, 1e-2, np.float32), device=DEV)
+        with pytest.raises(RuntimeError, match=changed):
+            scaler.step(optimizer)
+    elif edit == "gradient_requires_grad":
+        params[1].grad.requires_grad = True
+        with pytest.raises(RuntimeError, match=re.escape("GradScaler requires detached floating gradients.")):
+            scaler.step(optimizer)
+    elif edit == "parameter_frozen":
+        params[2].requires_grad = False
+        with pytest.raises(RuntimeError, match=changed):
+            scaler.step(optimizer)
+    elif edit == "gradient_to_none":
+        params[0].grad = None
+        with pytest.raises(RuntimeError, match=changed):
+            scaler.step(optimizer)
+    else:
+        params[1].grad[...] = nt.Tensor(np.full(300, np.inf, np.float32), device=DEV)
+        assert scaler.step(optimizer) is False
+        scaler.update()
+        assert scaler.get_scale() == 512.0
+    for p, b in zip(params, before):
+        assert np.array_equal(p.numpy(), b)
+    assert all(optimizer.state.get(id(p), {}).get("step", 0) == 0 for p in params)
