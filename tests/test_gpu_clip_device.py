@@ -326,3 +326,34 @@ def test_device_clip_edge_cases(case):
     for p, q, g in zip(device, host, grads):
         expected = oclip.clip_apply(g.astype(np.float64), coefficient, "float32") if bump else g
         assert _same(p.grad.numpy(), expected) and _same(p.grad.numpy(), q.grad.numpy())
+
+
+def test_device_clip_then_unscale_then_step():
+    """A device-decided clip followed by GradScaler.unscale_ (clipping the
+    scaled gradients, an unusual but legal order): unscale_ writes the clip
+    back first, so the step uses unscale(clip(g)) as the reference computes
+    it, bit for bit against the oracle."""
+    from oracle import scaler as oscaler
+    rng = np.random.default_rng(37)
+    hosts = [(rng.standard_normal(s) * 0.02).astype(np.float32) for s in SHAPES]
+    params = [nt.Parameter(h, device=DEV) for h in hosts]
+    optimizer = nt.optim.AdamW(params, lr=1e-3, weight_decay=0.1)
+    scaler = nt.GradScaler(init_scale=1024.0)
+    grads = [(rng.standard_normal(s) * 1e-3 * 1024).astype(np.float32) for s in SHAPES]
+    for p, g in zip(params, grads):
+        p.grad = nt.Tensor(g, device=DEV)
+    scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+    want_norm = oclip.total_norm([g.astype(np.float64) for g in grads])
+    norm = nt.optim.clip_grad_norm_(params, want_norm / 2)
+    assert params[0].grad._pending is not None and params[0].grad._pending.device is not None
+    assert scaler.unscale_(optimizer) is True
+    assert scaler.step(optimizer) is True
+    scaler.update()
+    coefficient = oclip.clip_coefficient(want_norm / 2, norm.item())
+    for p, h, g in zip(params, hosts, grads):
+        clipped = oclip.clip_apply(g.astype(np.float64), coefficient, "float32")
+        unscaled = oscaler.unscale(clipped, 1024.0, "float32")
+        value, m, v = h.copy(), np.zeros_like(h), np.zeros_like(h)
+        oadam.adam_step(value, np.asarray(unscaled, np.float32), m, v, 1, lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+                        weight_decay=0.1)
+        assert _same(p.numpy(), value)
