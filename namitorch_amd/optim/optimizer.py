@@ -288,13 +288,31 @@ class Optimizer:
         except TypeError:
             return None
 
+    def _groups_unchanged(self, cached) -> bool:
+        """The groups hold what they held when `cached` was built: the same
+        dict objects with the same params list objects, each of the same
+        length and with the same items (by identity).  Equivalent to an equal
+        fingerprint, without building one."""
+        groups, lists, lengths = cached[2], cached[3], cached[4]
+        current = self.param_groups
+        if type(current) is not list or len(current) != len(groups) or not all(map(is_, current, groups)):
+            return False
+        try:
+            if not all(map(is_, map(_PARAMS, groups), lists)):
+                return False
+        except KeyError:
+            return False
+        return tuple(map(len, lists)) == lengths and all(map(is_, chain.from_iterable(lists), cached[1]))
+
     def _registered_parameters(self) -> list:
         if not self.param_groups:
             raise ValueError("Optimizer must contain at least one parameter group.")
         # The structure check is a pure function of which objects the groups
         # hold; it is skipped while that is unchanged since the last call.
-        fingerprint = self._group_fingerprint()
         cached = self.__dict__.get("_registered_cache")
+        if cached is not None and self._groups_unchanged(cached):
+            return list(cached[1])
+        fingerprint = self._group_fingerprint()
         if fingerprint is not None and cached is not None and cached[0] == fingerprint:
             return list(cached[1])
         registered: list = []
@@ -310,7 +328,9 @@ class Optimizer:
                 owners.add(id(parameter))
                 registered.append(parameter)
         if fingerprint is not None and None not in fingerprint:
-            self._registered_cache = (fingerprint, tuple(registered))
+            groups = tuple(self.param_groups)
+            lists = tuple(map(_PARAMS, groups))
+            self._registered_cache = (fingerprint, tuple(registered), groups, lists, tuple(map(len, lists)))
         return registered
 
     def add_param_group(self, param_group: dict) -> None:

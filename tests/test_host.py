@@ -326,3 +326,22 @@ def test_requires_grad_changes_are_counted():
     tensor.requires_grad = True
     tensor.requires_grad_(False)
     assert _requires_grad_changes.value == before + 2
+
+
+def test_registered_cache_sees_a_parameter_moved_between_groups():
+    """Moving the last parameter of one group to the front of the next keeps
+    the flattened order but changes group membership (and so the options a
+    parameter steps with): the registered-parameter cache, whose identity the
+    step replay compares, must be rebuilt."""
+    params = [nt.Parameter(np.zeros(4, np.float32)) for _ in range(6)]
+    optimizer = nt.optim.AdamW([{"params": params[:3], "weight_decay": 0.1}, {"params": params[3:], "weight_decay": 0.0}])
+    assert optimizer._registered_parameters() == params
+    cache = optimizer.__dict__["_registered_cache"]
+    assert optimizer._registered_parameters() == params and optimizer.__dict__["_registered_cache"] is cache
+    optimizer.param_groups[1]["params"].insert(0, optimizer.param_groups[0]["params"].pop())
+    assert optimizer._registered_parameters() == params
+    assert optimizer.__dict__["_registered_cache"] is not cache
+    optimizer.param_groups[0]["params"][0] = nt.Parameter(np.zeros(4, np.float32))     # an item replaced in place
+    cache = optimizer.__dict__["_registered_cache"]
+    assert optimizer._registered_parameters()[0] is optimizer.param_groups[0]["params"][0]
+    assert optimizer.__dict__["_registered_cache"] is not cache
