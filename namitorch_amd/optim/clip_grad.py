@@ -22,7 +22,9 @@ the next kernel that reads them.  When nothing is pending on the gradients
 and ``error_if_nonfinite`` is False, the norm, the ``coefficient < 1``
 decision and the coefficient stay on the device (``_clip_on_device``): the
 call queues two kernels and returns without waiting, and the AdamW pass
-that follows reads the decision from the device.
+that follows reads the decision from the device.  ``get_grad_norm`` takes
+the same device path (``_norm_on_device``) and records nothing on the
+gradients; ``.item()`` on either result waits for it.
 """
 
 from __future__ import annotations
