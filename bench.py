@@ -59,7 +59,7 @@ def parse_args():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--configs", default="c2,c1,c3,c4,c5,c4s8,c5s8,ceilings,sweep")
+    parser.add_argument("--configs", default="c2,c1,c3,c4,c5,c4s8,c5s8,ceilings")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--kernel-only", action="store_true", help="only the C2 kernel loop (for profilers)")
     parser.add_argument("--calibrate", action="store_true",
@@ -269,8 +269,34 @@ def fresh_gradients(grads):
         gradient._version_counter.value += 1
 
 
+def evicted_step_ms(torch, one_step, steps: int, rounds: int = 5) -> dict:
+    """ms per step when the MALL holds nothing of the step's data as it
+    starts: the median over `rounds` of [steps x (1 GiB read + step) -
+    steps x 1 GiB read].  The read (an ordinary-load reduction) leaves the
+    MALL full of clean, unrelated lines, so the step keeps only what it makes
+    resident itself (the pre-pass's gradient window), and nothing from the
+    step before."""
+    flush = torch.ones(1 << 28, device="cuda")
+    sink = torch.empty((), device="cuda")
+
+    def loop(with_step: bool) -> float:
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(steps):
+            torch.sum(flush, dim=0, out=sink)
+            if with_step:
+                one_step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - start) * 1e3 / steps
+
+    differences = [loop(True) - loop(False) for _ in range(rounds)]
+    del flush, sink
+    return dict(ms_per_step=statistics.median(differences), rounds_ms=differences,
+                method="median over rounds of [steps x (1 GiB ordinary read + step) - steps x 1 GiB read]")
+
+
 def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype, amp, max_norm, bytes_per_param,
-                steps, warmup, modes=("fused", "api"), mask=None):
+                steps, warmup, modes=("fused", "api"), mask=None, evict=False):
     from namitorch_amd.param_lists import total_params
     n = total_params(shapes)
     params = make_params(nt, torch, shapes, param_dtype)
@@ -310,6 +336,11 @@ def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype
                             median_pct_hbm_peak=100 * bytes_per_param * n / median_ms / 1e6 / HBM_PEAK_GBPS,
                             scale=None if scaler is None else scaler.get_scale())
         log(f"{name} {mode}: {wall_ms:.3f} ms/step (median {median_ms:.3f})")
+        if evict and mode == "fused":
+            evicted = evicted_step_ms(torch, one_step, max(10, steps // 4))
+            evicted["pct_hbm_peak"] = 100 * bytes_per_param * n / evicted["ms_per_step"] / 1e6 / HBM_PEAK_GBPS
+            result[mode]["mall_evicted"] = evicted
+            log(f"{name} {mode} after a MALL eviction: {evicted['ms_per_step']:.3f} ms/step")
         for p in params:
             p._grad = None
         del optimizer, scaler
@@ -479,61 +510,6 @@ def bench_ceilings(nt, torch, steps, warmup):
             log(f"probe {name}: {gbps:.0f} GB/s")
         del wide, narrow
         release(nt, torch)
-    return result
-
-
-# ---- launch shapes of the pass's mixes --------------------------------------------------------------------
-SHAPES = (("wave (the pass)", 0), ("wave, XCD-contiguous tiles", 1), ("wave, 2 groups per lane", 2),
-          ("128 lanes", 3), ("256 lanes", 4), ("256 lanes, 2 groups", 5), ("512 lanes", 6),
-          ("persistent 64 lanes", 7), ("persistent 64 lanes, pipelined", 8),
-          ("persistent 256 lanes, pipelined", 9), ("persistent 64 lanes x2 groups, pipelined", 10),
-          ("direct-to-LDS loads", 11), ("temporal loads/stores", 12))
-
-
-def bench_shape_sweep(nt, torch, launches=8, warmup=2, rounds=5):
-    """The pass's two in-place mixes (fp32: 28 B/element; GPT-1.3B: fp32
-    master + bf16 g/m/v + bf16 copy, 20 B/element) under every launch shape
-    of nt_stream_probe_shape, at the C2 size and at 1 GiB per fp32 stream;
-    persistent shapes at 8 and 16 workgroups per CU.  The shapes take turns
-    over `rounds` rounds on the same buffers (so they share one physical
-    placement); each round times `launches` back-to-back launches with HIP
-    events on the launch stream; the median round is reported."""
-    import ctypes
-    from namitorch_amd import _native
-    handle = torch.cuda.current_stream().cuda_stream
-    result = {}
-    for size_name, count in (("c2_size", C2_STREAM), ("large", LARGE_STREAM)):
-        for mix, bytes_per_element, dtypes in ((0, 28, (torch.float32,) * 4),
-                                              (1, 20, (torch.float32,) + (torch.bfloat16,) * 4)):
-            buffers = [torch.zeros(count, dtype=dtype, device="cuda") for dtype in dtypes]
-            table = (ctypes.c_void_p * len(buffers))(*[b.data_ptr() for b in buffers])
-            variants = [(label if per_cu == 1 else f"{label}, {per_cu}/CU", (mix, shape, table, count, per_cu, handle))
-                        for label, shape in SHAPES if not (shape == 11 and mix == 1)
-                        for per_cu in ((8, 16) if 7 <= shape <= 10 else (1,))]
-            times = {name: [] for name, _ in variants}
-            for _ in range(rounds):
-                for name, args in variants:
-                    for _ in range(warmup):
-                        _native.call("nt_stream_probe_shape", *args)
-                    start, stop = event_pair(torch)
-                    start.record()
-                    for _ in range(launches):
-                        _native.call("nt_stream_probe_shape", *args)
-                    stop.record()
-                    stop.synchronize()
-                    times[name].append(start.elapsed_time(stop) / launches)
-            rows = {}
-            for name, values in times.items():
-                middle = sorted(values)[len(values) // 2]
-                rows[name] = dict(median_ms=middle, GBps=bytes_per_element * count / middle / 1e6,
-                                  best_GBps=bytes_per_element * count / min(values) / 1e6)
-            best = max(rows, key=lambda key: rows[key]["GBps"])
-            result[f"mix{mix}_{size_name}"] = dict(elements=count, bytes_per_element=bytes_per_element, shapes=rows,
-                                                   fastest=best)
-            log(f"shape sweep mix{mix} {size_name}: pass shape {rows['wave (the pass)']['GBps']:.0f} GB/s, "
-                f"fastest {best} {rows[best]['GBps']:.0f} GB/s")
-            del buffers
-            release(nt, torch)
     return result
 
 
@@ -799,17 +775,19 @@ def _mixed_configs(nt):
     from namitorch_amd.param_lists import decay_mask, gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes, shard_shapes
     return {
         "c3": ("c3_gpt2_amp", dict(shapes=gpt2_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.float16,
-                                   state_dtype=None, amp=True, max_norm=None, bytes_per_param=30)),
+                                   state_dtype=None, amp=True, max_norm=None, bytes_per_param=30, evict=True)),
         "c4": ("c4_gpt1p3b_bf16_clip", dict(shapes=gpt_1p3b_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.bfloat16,
                                             state_dtype=nt.bfloat16, amp=False, max_norm=1.0, bytes_per_param=22)),
         "c5": ("c5_llama7b_amp_clip", dict(shapes=llama7b_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.bfloat16,
                                            state_dtype=None, amp=True, max_norm=1.0, bytes_per_param=30)),
         "c4s8": ("c4_shard8", dict(shapes=shard_shapes(gpt_1p3b_shapes(), 8), param_dtype=nt.bfloat16,
                                    grad_dtype=nt.bfloat16, state_dtype=nt.bfloat16, amp=False, max_norm=1.0,
-                                   bytes_per_param=22, modes=("fused",), mask=decay_mask(gpt_1p3b_shapes()))),
+                                   bytes_per_param=22, modes=("fused",), mask=decay_mask(gpt_1p3b_shapes()),
+                                   evict=True)),
         "c5s8": ("c5_shard8", dict(shapes=shard_shapes(llama7b_shapes(), 8), param_dtype=nt.bfloat16,
                                    grad_dtype=nt.bfloat16, state_dtype=None, amp=True, max_norm=1.0,
-                                   bytes_per_param=30, modes=("fused",), mask=decay_mask(llama7b_shapes()))),
+                                   bytes_per_param=30, modes=("fused",), mask=decay_mask(llama7b_shapes()),
+                                   evict=True)),
     }
 
 
@@ -837,7 +815,7 @@ def main():
         modes = tuple(args.profile_modes.split(","))
         if not modes or any(mode not in ("fused", "api") for mode in modes):
             raise SystemExit("--profile-modes takes 'fused' and/or 'api', comma-separated")
-        spec = dict(spec, modes=modes)
+        spec = dict(spec, modes=modes, evict=False)
         shapes = spec.pop("shapes")
         log(f"{args.profile} {' then '.join(modes)} steps only ({args.warmup} untimed, {args.steps} timed each)")
         if args.calibrate:
@@ -889,9 +867,6 @@ def main():
     if "edges" in wanted:
         log("gradient edges: accumulate and zero over the gpt-1.3b list (bf16)")
         extra["grad_edges_gpt1p3b"] = bench_edges(nt, torch, gpt_1p3b_shapes(), max(5, args.steps // 2), args.warmup)
-    if "sweep" in wanted:
-        log("launch shapes of the pass's in-place mixes (nt_stream_probe_shape)")
-        extra["shape_sweep"] = bench_shape_sweep(nt, torch)
     ceilings = None
     if "ceilings" in wanted:
         log("streaming ceilings of the read/write mixes (nt_stream_probe)")

@@ -54,6 +54,7 @@ extern "C" {
 
 /* ---- multi-tensor plan limits ------------------------------------------ */
 #define NT_MAX_SLOTS 16     /* coefficient sets per nt_adamw_mt launch */
+#define NT_MAX_COMBINE 8    /* control blocks per nt_amp_combine call */
 
 /*
  * One tensor of a multi-tensor plan.  `param` is the array the update is
@@ -349,6 +350,31 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *car
                         int32_t growth_interval, void *stream);
 
 /*
+ * One GradScaler iteration over several optimizers (amp.py:169-233 called
+ * for each optimizer, then update() once).  `blocks[0..n)` (device memory,
+ * 1 <= n <= NT_MAX_COMBINE, pairwise distinct) hold each optimizer's
+ * statistics from nt_amp_prepass + nt_amp_finalize with max_norm < 0 and no
+ * flags; `carry` is the previous iteration's block they all carried from.
+ * The sums of squares add in block order and the maxima and NaN/inf flags
+ * combine into the norm of all their gradients (norm_type 2 or +inf), from
+ * which the clip decision is taken as nt_amp_finalize takes it
+ * (NT_FINALIZE_CLIP_IF_FINITE: no clip when any optimizer's gradients are
+ * non-finite, the reference loop clipping only after every unscale_
+ * returned True, training/runner.py:248-249); NT_FINALIZE_SCALER_UPDATE
+ * runs one scaler update, backing off when any optimizer found a non-finite
+ * gradient (amp.py:224-233).  Every block then holds the global norm, clip
+ * flag and coefficient and the new scaler state, and keeps its own
+ * sumsq/amax/found_inf/has_nan with skip = its own found_inf: each
+ * optimizer's step checks only its own gradients (GradScaler.step,
+ * amp.py:209-217).  No single reference function: it is the composition the
+ * reference runs on the host.
+ */
+int32_t nt_amp_combine(nt_amp_ctrl *const *blocks, int32_t n, const nt_amp_ctrl *carry,
+                       double norm_type, double max_norm, int32_t flags,
+                       double growth_factor, double backoff_factor,
+                       int32_t growth_interval, void *stream);
+
+/*
  * General p-norm (0 < p < inf) of optim/clip_grad.py:70-79: sum over
  * grads of (|g'|/amax)^p in fp64, with amax from the previous prepass
  * already in `ctrl`; leaves the norm in ctrl->norm, the raw sum in
@@ -476,34 +502,6 @@ int32_t nt_any_negative(const void *array, int32_t dtype, uint64_t count,
 int32_t nt_stream_probe(const void *const *reads, int32_t nreads, int32_t nreads16,
                         void *const *writes, int32_t nwrites, int32_t nwrites16,
                         uint64_t count, void *stream);
-
-/*
- * Launch-shape probe, no counterpart in the reference: a measurement aid.
- * Runs one of the AdamW pass's in-place read/write mixes with AdamW-like
- * arithmetic under launch shape `shape`, so a benchmark can compare the
- * shapes the pass could use.  Mix 0 (the float32 pass, 28 B/element):
- * streams[0..3] = p, g, m, v (fp32); p, m, v are rewritten in place.  Mix 1
- * (the GPT-1.3B pass, 20 B/element): streams[0] = fp32 master, [1..3] =
- * bfloat16 g, m, v, [4] = bfloat16 copy; master, m, v rewritten in place, the
- * copy written.  `count` elements per stream, a positive multiple of 8192;
- * streams 16-byte aligned.  `per_cu` (1..64) sizes persistent grids in
- * workgroups per compute unit.
- */
-#define NT_SHAPE_WAVE 0               /* 64 lanes x 1 group: the pass's shape */
-#define NT_SHAPE_WAVE_XCD 1           /* the same, tile order contiguous per XCD */
-#define NT_SHAPE_WAVE_U2 2            /* 64 lanes x 2 groups per lane */
-#define NT_SHAPE_B128 3               /* 128 lanes x 1 group */
-#define NT_SHAPE_B256 4               /* 256 lanes x 1 group */
-#define NT_SHAPE_B256_U2 5            /* 256 lanes x 2 groups */
-#define NT_SHAPE_B512 6               /* 512 lanes x 1 group */
-#define NT_SHAPE_PERSISTENT 7         /* 64 lanes, per_cu workgroups per CU walk the tiles */
-#define NT_SHAPE_PERSISTENT_PIPE 8    /* the same, next tile loaded before this tile is stored */
-#define NT_SHAPE_PERSISTENT_B256_PIPE 9
-#define NT_SHAPE_PERSISTENT_U2_PIPE 10
-#define NT_SHAPE_DIRECT_TO_LDS 11     /* mix 0 only: global_load_lds_dwordx4, nontemporal */
-#define NT_SHAPE_TEMPORAL 12          /* NT_SHAPE_WAVE with ordinary (temporal) loads and stores */
-int32_t nt_stream_probe_shape(int32_t mix, int32_t shape, void *const *streams, uint64_t count,
-                              int32_t per_cu, void *stream);
 
 #ifdef __cplusplus
 }

@@ -140,6 +140,8 @@ SIGNATURES = {
     "nt_amp_prepass": (c_int32, [c_void_p, c_float, c_int32, c_void_p, c_void_p]),
     "nt_amp_finalize": (c_int32, [c_void_p, c_void_p, c_void_p, c_double, c_double, c_int32, c_double, c_double, c_int32,
                                   c_void_p]),
+    "nt_amp_combine": (c_int32, [ctypes.POINTER(c_void_p), c_int32, c_void_p, c_double, c_double, c_int32, c_double,
+                                 c_double, c_int32, c_void_p]),
     "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_int32, c_void_p]),
     "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
     "nt_grad_zero": (c_int32, [c_void_p, c_void_p]),
@@ -153,7 +155,6 @@ SIGNATURES = {
                                             c_double, c_double, c_int32, c_double, c_double, c_int32, c_void_p]),
     "nt_stream_probe": (c_int32, [ctypes.POINTER(c_void_p), c_int32, c_int32, ctypes.POINTER(c_void_p), c_int32, c_int32,
                                   c_uint64, c_void_p]),
-    "nt_stream_probe_shape": (c_int32, [c_int32, c_int32, ctypes.POINTER(c_void_p), c_uint64, c_int32, c_void_p]),
     "nt_malloc": (c_int32, [c_int32, c_uint64, c_void_p, ctypes.POINTER(c_void_p)]),
     "nt_free": (c_int32, [c_void_p]),
     "nt_record_stream": (c_int32, [c_void_p, c_void_p]),

@@ -29,6 +29,7 @@ from . import _native, runtime
 from .backends import get_backend
 from .backends._graph_capture import reject_during_capture
 from .dtype import float32, float64, promote_with_scalar
+from .optim import clip_grad
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
 from .tensor import GradTransform, _unsettled_steps, check_addends, is_grad_enabled
 
@@ -139,12 +140,21 @@ class DeviceStep:
                         parameter._version_counter.value -= 1
                         if master is not None:
                             master._version_counter.value -= 1
-        if not ctrl.clip:
-            for gradient, version in self.clip_bumps:
-                if gradient._version_counter.value == version:
-                    gradient._version_counter.value -= 1
-                    if gradient._finite_version == version:
-                        gradient._finite_version = version - 1
+        if not ctrl.clip and self.clip_bumps:
+            # The clip's one bump is taken back whatever was written since
+            # (the reference counts one write per clip actually applied).
+            for gradient, _ in self.clip_bumps:
+                counter = gradient._version_counter
+                counter.value -= 1
+                stamp = gradient._finite_version
+                if stamp == counter.value + 1:
+                    gradient._finite_version = counter.value       # the same contents, renumbered
+                elif stamp is not None and stamp >= counter.value:
+                    gradient._finite_version = None                # would name other contents later
+            # A lowered counter reaches its old values again at the next
+            # writes, with other contents: statistics cached under them must
+            # not match then.
+            clip_grad._last_stats.clear()
         self.records.clear()
         self._reconciled = True
         self._forget()
@@ -478,6 +488,11 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     the next step, ``get_scale``/``state_dict`` or ``StepResult`` access.
     ``error_if_nonfinite`` has no equivalent here (it would need the host).
 
+    ``optimizer`` may also be a list or tuple of optimizers that share the
+    scaler's iteration (``_fused_step_many``): ``scheduler`` is then None or
+    a sequence with one entry (None or a scheduler) per optimizer, and the
+    result is a list with one StepResult per optimizer.
+
     ``scheduler`` (an ``optim.lr_scheduler.LRScheduler`` of ``optimizer``) is
     stepped when this step turns out to have updated, as the training loop
     does after ``scaler.step`` (runner.py:250-253).  The outcome is known on
@@ -486,22 +501,10 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     the schedule.
     """
     reject_during_capture("Optimizer steps")
-    if scheduler is not None:
-        from .optim.lr_scheduler import LRScheduler
-        if not isinstance(scheduler, LRScheduler):
-            raise TypeError("scheduler must be a NamiTorch LRScheduler or None.")
-        if scheduler.optimizer is not optimizer:
-            raise ValueError("scheduler must belong to the supplied optimizer.")
-    amp = scaler is not None and scaler._enabled
-    if amp:
-        if not scaler._scale_used:
-            raise RuntimeError("Call scale(loss) and backward before unscale_.")
-        if scaler._optimizer_states:
-            raise RuntimeError("fused_step cannot follow unscale_ or step in the same iteration; call update() first.")
-    maximum = None if max_norm is None else _nonnegative(max_norm, "max_norm")
-    order = _norm_type(norm_type)
-    if order != 2.0 and not math.isinf(order):
-        raise ValueError("fused_step supports norm_type 2 and inf; use clip_grad_norm_ for other norms.")
+    if isinstance(optimizer, (list, tuple)):
+        return _fused_step_many(list(optimizer), scaler, max_norm, norm_type, scheduler)
+    _check_scheduler(scheduler, optimizer)
+    amp, maximum, order = _fused_arguments(scaler, max_norm, norm_type)
     pairs = GradScaler._gradients(optimizer)
     gradients = list(map(_SECOND_OF, pairs))
     if not gradients:
@@ -572,6 +575,164 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     optimizer._track_device_step(device_step)
     _unsettled_steps.append(device_step)                  # version reads settle it first
     return StepResult(device_step)
+
+
+def _check_scheduler(scheduler, optimizer) -> None:
+    if scheduler is not None:
+        from .optim.lr_scheduler import LRScheduler
+        if not isinstance(scheduler, LRScheduler):
+            raise TypeError("scheduler must be a NamiTorch LRScheduler or None.")
+        if scheduler.optimizer is not optimizer:
+            raise ValueError("scheduler must belong to the supplied optimizer.")
+
+
+def _fused_arguments(scaler, max_norm, norm_type) -> tuple:
+    """(amp, max_norm, norm_type) after fused_step's checks of the scaler
+    state and the clip arguments."""
+    amp = scaler is not None and scaler._enabled
+    if amp:
+        if not scaler._scale_used:
+            raise RuntimeError("Call scale(loss) and backward before unscale_.")
+        if scaler._optimizer_states:
+            raise RuntimeError("fused_step cannot follow unscale_ or step in the same iteration; call update() first.")
+    maximum = None if max_norm is None else _nonnegative(max_norm, "max_norm")
+    order = _norm_type(norm_type)
+    if order != 2.0 and not math.isinf(order):
+        raise ValueError("fused_step supports norm_type 2 and inf; use clip_grad_norm_ for other norms.")
+    return amp, maximum, order
+
+
+def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers) -> list:
+    """``fused_step`` over several optimizers in one scaler iteration: the
+    reference loop's ``unscale_`` of every optimizer, ``clip_grad_norm_`` of
+    all their parameters when every ``unscale_`` returned True (when
+    ``max_norm`` is given), ``step`` of every optimizer and one ``update``
+    (amp.py:169-233, training/runner.py:248-251).  As there, each optimizer
+    steps unless its own gradients are non-finite (GradScaler.step checks
+    only them), the scale backs off once if any optimizer's are, and
+    optimizers may not share gradients (``unscale_``'s error).  Every check
+    runs before anything changes.
+
+    One pre-pass and finalize per optimizer, then one ``nt_amp_combine``
+    that takes the global norm, clip and scaler decisions and gives each
+    optimizer's control block its own skip flag; the AdamW passes read
+    their blocks, so the host does not wait.  Returns one StepResult per
+    optimizer (its own ``finite`` and ``updated``; the global ``norm`` and
+    the next ``scale``)."""
+    if not optimizers:
+        raise ValueError("fused_step needs at least one optimizer.")
+    if schedulers is None:
+        schedulers = [None] * len(optimizers)
+    elif not isinstance(schedulers, (list, tuple)) or len(schedulers) != len(optimizers):
+        raise TypeError("With several optimizers, scheduler must be None or a sequence with one entry per optimizer.")
+    for optimizer, scheduler in zip(optimizers, schedulers):
+        _check_scheduler(scheduler, optimizer)
+    amp, maximum, order = _fused_arguments(scaler, max_norm, norm_type)
+    if amp:
+        seen: set = set()
+        for optimizer in optimizers:
+            if id(optimizer) in seen:
+                raise RuntimeError("unscale_ may be called only once per optimizer between update() calls.")
+            seen.add(id(optimizer))
+    gathered = []
+    shared: set = set()
+    for optimizer in optimizers:
+        pairs = GradScaler._gradients(optimizer)
+        if not pairs:
+            raise RuntimeError("No gradients were found for this optimizer.")
+        if amp:
+            if any(id(parameter) in shared for parameter, _ in pairs):
+                raise RuntimeError("Optimizers cannot share gradients in the same GradScaler iteration.")
+            shared.update(id(parameter) for parameter, _ in pairs)
+        gathered.append(list(map(_SECOND_OF, pairs)))
+    groups = [_device_groups(gradients) for gradients in gathered]
+    keys = [next(iter(g)) if len(g) == 1 else None for g in groups]
+    distinct = len({id(optimizer) for optimizer in optimizers}) == len(optimizers)
+    if (not distinct or len(optimizers) > _native.NT_MAX_COMBINE or any(key is None for key in keys)
+            or len({id(key[0]) for key in keys}) != 1 or any(key[1] is float64 for key in keys)
+            or keys[0][0].adamw is None):
+        # Several devices, mixed dtypes within an optimizer, float64 (its
+        # guarded second norm pass), repeated optimizers or more optimizers
+        # than one combine takes: the synchronizing API gives the same results.
+        return _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers)
+    backend = keys[0][0]
+    for gradients in gathered:
+        if (any(map(_REQUIRES, gradients)) and is_grad_enabled()) or not all(map(_WRITABLE, gradients)):
+            for gradient in gradients:
+                gradient._ensure_inplace_allowed()        # raises the matching error
+        check_addends(gradients)                          # before any bookkeeping changes
+    if amp:
+        latest = scaler._device_blocks.get(backend) if scaler._device_steps else None
+        previous = backend.new_ctrl(scaler._scale, scaler._growth_tracker) if latest is None \
+            else latest.block_for_current_stream()
+    else:
+        previous = backend.neutral_ctrl()
+    device_steps = []
+    for gradients, (_, dtype), scheduler in zip(gathered, keys, schedulers):
+        block = backend.empty_ctrl()
+        clip_bumps: list = []
+        device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps)
+        device_step.clip_requested = maximum is not None
+        device_step.scheduler = scheduler
+        transform = GradTransform(device=device_step)
+        if any(map(_PENDING, gradients)):
+            for gradient in gradients:
+                if gradient._pending is not None:
+                    gradient._materialize()
+        bumps = int(amp) + int(maximum is not None)
+        deque(map(setattr, gradients, repeat("_pending"), repeat(transform)), 0)
+        counters = tuple(map(_COUNTER, gradients))
+        for counter in counters:
+            counter.value += bumps
+        deque(map(setattr, gradients, repeat("_finite_version"), map(_VALUE, counters)), 0)
+        if maximum is not None:
+            clip_bumps.extend(zip(gradients, map(_VALUE, counters)))
+        plan = backend.grad_plan(gradients, dtype, incoming=True)
+        backend.grad_prepass(plan, None, previous.data_ptr(), unscale=amp)
+        backend.grad_finalize(plan, block.data_ptr(), order, -1.0, 0, carry_ptr=previous.data_ptr())
+        device_steps.append(device_step)
+    flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
+    growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp \
+        else (2.0, 0.5, 1)
+    backend.grad_combine([device_step.block for device_step in device_steps], previous, order,
+                         -1.0 if maximum is None else maximum, flags, growth, backoff, interval)
+    for device_step in device_steps:
+        device_step.capture()
+    if amp:
+        scaler._reconcile()                               # earlier fused steps: their finalize already ran
+        scaler._device_blocks[backend] = device_steps[0]  # every block holds the same scaler state
+        scaler._device_steps.append(device_steps[0])
+        scaler._scale_used = False
+    for optimizer, device_step in zip(optimizers, device_steps):
+        optimizer.step()                                  # each AdamW pass reads its own control block
+        optimizer._track_device_step(device_step)
+        _unsettled_steps.append(device_step)
+    return [StepResult(device_step) for device_step in device_steps]
+
+
+def _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers) -> list:
+    """``_fused_step_many`` through the host-synchronizing API."""
+    parameters = [parameter for optimizer in optimizers for parameter, _ in GradScaler._gradients(optimizer)]
+    norm = None
+    if amp:
+        finite = [scaler.unscale_(optimizer) for optimizer in optimizers]
+        if all(finite) and maximum is not None:
+            norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+        updated = [scaler.step(optimizer) for optimizer in optimizers]
+        scaler.update()
+        scale = scaler.get_scale()
+        results = [StepResult(finite=f, updated=u, norm=norm, scale=scale) for f, u in zip(finite, updated)]
+    else:
+        if maximum is not None:
+            norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+        for optimizer in optimizers:
+            optimizer.step()
+        finite = None if norm is None else math.isfinite(norm)
+        results = [StepResult(finite=finite, updated=True, norm=norm, scale=1.0) for _ in optimizers]
+    for scheduler, result in zip(schedulers, results):
+        if scheduler is not None and result.updated:
+            scheduler.step()
+    return results
 
 
 def _fused_step_host(optimizer, scaler, amp, maximum, order, parameters) -> StepResult:

@@ -386,6 +386,14 @@ class HIPBackend:
             _native.call("nt_amp_finalize", plan.handle, ctrl_ptr, carry_ptr, norm_type, max_norm, int(flags),
                          growth, backoff, interval, self.stream())
 
+    def grad_combine(self, blocks, carry, norm_type: float, max_norm: float, flags: int, growth: float,
+                     backoff: float, interval: int) -> None:
+        """nt_amp_combine over the finalized blocks (DeviceArrays), all carried from `carry`."""
+        pointers = (ctypes.c_void_p * len(blocks))(*[block.data_ptr() for block in blocks])
+        with self.context():
+            _native.call("nt_amp_combine", pointers, len(blocks), carry.data_ptr(), norm_type, max_norm, int(flags),
+                         growth, backoff, interval, self.stream())
+
     def grad_norm_pow(self, plan: Plan, ctrl_ptr: int, norm_type: float, max_norm: float,
                       scale: float | None, scale_from_ctrl: bool = False, flags: int = 0) -> None:
         with self.context():

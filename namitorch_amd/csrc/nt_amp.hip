@@ -216,6 +216,68 @@ __device__ __forceinline__ void add_incoming(float (&g)[kPrepassUnroll][kVec], c
         for (int k = 0; k < kVec; ++k) g[u][k] = G::round_f32(g[u][k] + h[u][k]);
 }
 
+// ---- whole-task loads with a chosen cache policy ----------------------------------
+// A whole, aligned pre-pass task is read through a buffer resource over its
+// bytes, so the cache policy is an immediate of each load instruction:
+// temporal loads allocate in the MALL (the gradients stay resident for the
+// AdamW pass that follows), nontemporal ones do not.  (The same choice made
+// between two ordinary loads is not kept: the compiler merges loads that
+// differ only in their nontemporal marking.)
+constexpr int kCpolNontemporal = 2;     // the nt bit of the cache-policy operand
+
+template <class T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t task_rsrc(const T *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(base), (short)0, (int)(kPrepassTile * sizeof(T)),
+                                             0x00020000);
+}
+
+// The kPrepassUnroll pairs of 32-bit words of this lane (4 16-bit values each).
+__device__ __forceinline__ void task_words(__amdgpu_buffer_rsrc_t r, u32x2 (&w)[kPrepassUnroll], bool keep) {
+    const int lane = (int)threadIdx.x * kVec * 2;
+    if (keep) {
+#pragma unroll
+        for (int u = 0; u < kPrepassUnroll; ++u)
+            w[u] = __builtin_amdgcn_raw_buffer_load_b64(r, lane + u * kBlock * kVec * 2, 0, 0);
+    } else {
+#pragma unroll
+        for (int u = 0; u < kPrepassUnroll; ++u)
+            w[u] = __builtin_amdgcn_raw_buffer_load_b64(r, lane + u * kBlock * kVec * 2, 0, kCpolNontemporal);
+    }
+}
+
+// This lane's kPrepassUnroll groups of 4 values, widened to fp32.
+template <class G>
+__device__ __forceinline__ void task_values(__amdgpu_buffer_rsrc_t r, float (&g)[kPrepassUnroll][kVec], bool keep) {
+    if constexpr (sizeof(typename G::raw) == 2) {
+        u32x2 w[kPrepassUnroll];
+        task_words(r, w, keep);
+#pragma unroll
+        for (int u = 0; u < kPrepassUnroll; ++u) {
+            g[u][0] = G::to_f32((uint16_t)(w[u].x & 0xffffu));
+            g[u][1] = G::to_f32((uint16_t)(w[u].x >> 16));
+            g[u][2] = G::to_f32((uint16_t)(w[u].y & 0xffffu));
+            g[u][3] = G::to_f32((uint16_t)(w[u].y >> 16));
+        }
+    } else {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 w[kPrepassUnroll];
+        const int lane = (int)threadIdx.x * kVec * 4;
+        if (keep) {
+#pragma unroll
+            for (int u = 0; u < kPrepassUnroll; ++u)
+                w[u] = __builtin_amdgcn_raw_buffer_load_b128(r, lane + u * kBlock * kVec * 4, 0, 0);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kPrepassUnroll; ++u)
+                w[u] = __builtin_amdgcn_raw_buffer_load_b128(r, lane + u * kBlock * kVec * 4, 0, kCpolNontemporal);
+        }
+#pragma unroll
+        for (int u = 0; u < kPrepassUnroll; ++u)
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) g[u][k] = bits_f32(w[u][k]);
+    }
+}
+
 // No raw-word visitor (prepass_visit's default).
 struct NoRaw {};
 
@@ -229,9 +291,11 @@ struct NoRaw {};
 // covers its lanes' share of each task.
 template <class G, class Vec, class One, class Raw = NoRaw>
 __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tensors, const Task *__restrict__ tasks,
-                                              int64_t first, int ntask, int64_t chunk, Vec vec, One one,
-                                              Raw raw = Raw()) {
+                                              int64_t first, int ntask, int64_t chunk, int64_t keep_from, Vec vec,
+                                              One one, Raw raw = Raw()) {
     for (int j = 0; j < ntask; ++j) {
+        // Tasks from keep_from on are read with temporal loads (keep_from_task).
+        const bool keep = first + j >= keep_from;
         const Task task = tasks[first + j];
         const DevTensor d = tensors[task.tensor];
         const uint64_t start = (uint64_t)task.chunk * (uint64_t)chunk;
@@ -245,10 +309,7 @@ __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tens
             if constexpr (!std::is_same<Raw, NoRaw>::value) {
                 if (ip == nullptr) {
                     u32x2 w[kPrepassUnroll];
-#pragma unroll
-                    for (int u = 0; u < kPrepassUnroll; ++u)
-                        w[u] = gload<true, u32x2, gu32x2>(gp + start + (uint64_t)u * kBlock * kVec +
-                                                          (uint64_t)threadIdx.x * kVec);
+                    task_words(task_rsrc(gp + start), w, keep);
                     // All loads issue before any of them is consumed.
                     __builtin_amdgcn_sched_barrier(0);
                     raw(w);
@@ -256,14 +317,10 @@ __device__ __forceinline__ void prepass_visit(const DevTensor *__restrict__ tens
                 }
             }
             float g[kPrepassUnroll][kVec];
-#pragma unroll
-            for (int u = 0; u < kPrepassUnroll; ++u)
-                Vec4IO<G, true>::load(gp + start, (uint64_t)u * kBlock * kVec + (uint64_t)threadIdx.x * kVec, g[u]);
+            task_values<G>(task_rsrc(gp + start), g, keep);
             if (ip != nullptr) {
                 float h[kPrepassUnroll][kVec];
-#pragma unroll
-                for (int u = 0; u < kPrepassUnroll; ++u)
-                    Vec4IO<G, true>::load(ip + start, (uint64_t)u * kBlock * kVec + (uint64_t)threadIdx.x * kVec, h[u]);
+                task_values<G>(task_rsrc(ip + start), h, keep);
                 add_incoming<G>(g, h);
             }
             vec(g);
@@ -338,8 +395,8 @@ __device__ __forceinline__ void visit_f16(half2_t inv2, ushort2_t &max2, PAcc &a
 template <class G>
 __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__restrict__ tensors,
                                                          const Task *__restrict__ tasks, int64_t ntasks,
-                                                         int64_t chunk, Xform xf, const nt_amp_ctrl *ctrl,
-                                                         Partial *__restrict__ partials) {
+                                                         int64_t chunk, int64_t keep_from, Xform xf,
+                                                         const nt_amp_ctrl *ctrl, Partial *__restrict__ partials) {
     __shared__ WaveJoin join;
     wave_join_init(join);
     if (ctrl != nullptr && xf.unscale) xf.scale = ctrl_scale_inv(ctrl->scale, xf.unscale, xf.inv_scale);
@@ -357,7 +414,7 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
     // wave that fails the check recomputes its elements one by one.
     const bool raw = G::code == NT_BF16 && (xf.unscale == 0 || (xf.unscale == 2 && xf.inv_scale <= 1.0f));
     if (raw) {
-        prepass_visit<G>(tensors, tasks, first, ntask, chunk,
+        prepass_visit<G>(tensors, tasks, first, ntask, chunk, keep_from,
                          [&](const float (&g)[kPrepassUnroll][kVec]) { pacc_fast<G>(acc, mn, g); },
                          [&](float v) { pacc_fast1(acc, mn, v, true); });
         const uint32_t mx = wave_max_u32(acc.amax_bits);
@@ -373,7 +430,7 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
         Partial mine;
         if (redo) {
             acc = PAcc();
-            prepass_visit<G>(tensors, tasks, first, ntask, chunk,
+            prepass_visit<G>(tensors, tasks, first, ntask, chunk, keep_from,
                              [&](const float (&g)[kPrepassUnroll][kVec]) {
 #pragma unroll
                                  for (int u = 0; u < kPrepassUnroll; ++u)
@@ -398,7 +455,7 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
     // element loop, so no element pays a test of it (the compiler does not
     // hoist the test out of the unrolled loop by itself).
     auto visit = [&](auto unscale) {
-        prepass_visit<G>(tensors, tasks, first, ntask, chunk,
+        prepass_visit<G>(tensors, tasks, first, ntask, chunk, keep_from,
                          [&](const float (&g)[kPrepassUnroll][kVec]) {
                              float h[kPrepassUnroll][kVec];
 #pragma unroll
@@ -423,7 +480,7 @@ __global__ __launch_bounds__(kBlock) void prepass_kernel(const DevTensor *__rest
             const half2_t inv2 = {(_Float16)xf.inv_scale, (_Float16)xf.inv_scale};
             ushort2_t max2 = {0, 0};
             visit_f16(inv2, max2, acc, [&](auto unscale, auto raw) {
-                prepass_visit<G>(tensors, tasks, first, ntask, chunk,
+                prepass_visit<G>(tensors, tasks, first, ntask, chunk, keep_from,
                                  [&](const float (&g)[kPrepassUnroll][kVec]) {
                                      float h[kPrepassUnroll][kVec];
 #pragma unroll
@@ -542,6 +599,10 @@ __device__ __forceinline__ nt_amp_ctrl carried_ctrl(const nt_amp_ctrl &s) {
     return c;
 }
 
+__device__ __forceinline__ void decide_iteration(nt_amp_ctrl &c, double sumsq, double amax, int32_t nan, int32_t inf,
+                                                 double norm_type, double max_norm, int32_t flags, double growth,
+                                                 double backoff, int32_t interval);
+
 // `carry` (optional): start from carried_ctrl(*carry) instead of *ctrl, so a
 // new iteration's block needs no separate carry kernel.
 __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restrict__ partials, int64_t n,
@@ -551,21 +612,30 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restr
                                                           int32_t interval) {
     Acc r = reduce_partials(partials, 0, n);
     if (threadIdx.x != 0) return;
-    const double nanv = __builtin_nan("");
-    const double infv = __builtin_inf();
+    nt_amp_ctrl c = carry != nullptr ? carried_ctrl(*carry) : *ctrl;
+    decide_iteration(c, r.sumsq, r.amax, r.nan, r.inf, norm_type, max_norm, flags, growth, backoff, interval);
+    *ctrl = c;
+}
+
+// One iteration's decisions from its merged statistics (fp64 sum of squares
+// and max |g'| of the finite unscaled gradients, NaN/inf seen), starting
+// from `c` (the carried scaler state): the norm, the clip decision, the skip
+// flag and, with NT_FINALIZE_SCALER_UPDATE, the scaler update.
+__device__ __forceinline__ void decide_iteration(nt_amp_ctrl &c, double sumsq, double amax, int32_t nan, int32_t inf,
+                                                 double norm_type, double max_norm, int32_t flags, double growth,
+                                                 double backoff, int32_t interval) {
     // _total_norm (optim/clip_grad.py:63-79): the max-abs prescale is
     // non-finite or zero => return it; else scale * total^(1/p).
     double norm;
-    if (r.nan) norm = nanv;
-    else if (r.inf) norm = infv;
-    else if (r.amax == 0.0 || __builtin_isinf(norm_type)) norm = r.amax;
-    else norm = __builtin_sqrt(r.sumsq);   // p == 2; other p: nt_grad_norm_pow
-    nt_amp_ctrl c = carry != nullptr ? carried_ctrl(*carry) : *ctrl;
-    c.sumsq = r.sumsq;
-    c.amax = r.amax;
+    if (nan) norm = __builtin_nan("");
+    else if (inf) norm = __builtin_inf();
+    else if (amax == 0.0 || __builtin_isinf(norm_type)) norm = amax;
+    else norm = __builtin_sqrt(sumsq);   // p == 2; other p: nt_grad_norm_pow
+    c.sumsq = sumsq;
+    c.amax = amax;
     c.norm = norm;
-    c.has_nan = r.nan;
-    c.found_inf = r.nan | r.inf;
+    c.has_nan = nan;
+    c.found_inf = nan | inf;
     if (max_norm >= 0.0) {
         c.clip_coef = max_norm / (norm + 1e-6);
         c.clip = c.clip_coef < 1.0 ? 1 : 0;
@@ -579,7 +649,41 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restr
     c.iterations += 1;
     c.skipped += c.found_inf;
     if (flags & NT_FINALIZE_SCALER_UPDATE) scaler_update(&c, c.found_inf, growth, backoff, interval);
-    *ctrl = c;
+}
+
+// Several optimizers in one scaler iteration: blocks[0..n) hold each one's
+// finalized statistics.  Their sums add in block order, the maxima and the
+// NaN/inf flags combine, and one set of decisions (global norm and clip,
+// one scaler update over all) goes into every block, which keeps its own
+// statistics and skip flag.
+struct CombineBlocks {
+    nt_amp_ctrl *block[NT_MAX_COMBINE];
+};
+
+__global__ void combine_kernel(CombineBlocks blocks, int32_t n, const nt_amp_ctrl *carry, double norm_type,
+                               double max_norm, int32_t flags, double growth, double backoff, int32_t interval) {
+    if (threadIdx.x != 0) return;
+    double sumsq = 0.0, amax = 0.0;
+    int32_t nan = 0, inf = 0;
+    for (int32_t i = 0; i < n; ++i) {
+        const nt_amp_ctrl &b = *blocks.block[i];
+        sumsq += b.sumsq;
+        amax = b.amax > amax ? b.amax : amax;
+        nan |= b.has_nan;
+        inf |= b.found_inf;          // with has_nan somewhere, the norm is NaN whatever inf says
+    }
+    nt_amp_ctrl c = carried_ctrl(*carry);
+    decide_iteration(c, sumsq, amax, nan, inf, norm_type, max_norm, flags, growth, backoff, interval);
+    for (int32_t i = 0; i < n; ++i) {
+        nt_amp_ctrl out = c;
+        const nt_amp_ctrl own = *blocks.block[i];
+        out.sumsq = own.sumsq;
+        out.amax = own.amax;
+        out.found_inf = own.found_inf;
+        out.has_nan = own.has_nan;
+        out.skip = own.found_inf;    // GradScaler.step checks its own optimizer's gradients (amp.py:209-217)
+        *blocks.block[i] = out;
+    }
 }
 
 // With `guard`, the p = 2 prescaled pass runs only when the finalize's
@@ -832,6 +936,17 @@ static int32_t grad_dispatch(int32_t gdt, dim3 grid, hipStream_t s, Args... args
     return NT_OK;
 }
 
+// First pre-pass task read with temporal loads: the plan's last tasks that
+// hold at most kMallKeepBytes of gradient data (counting a deferred addend
+// stream too), so the AdamW pass re-reads them from the MALL.
+static int64_t keep_from_task(const nt_plan *plan) {
+    const int32_t gdt = plan->layout.grad_dtype;
+    const uint64_t size = gdt == NT_F16 || gdt == NT_BF16 ? 2u : 4u;
+    const uint64_t per_task = (uint64_t)plan->chunk * size * (plan->n_incoming > 0 ? 2u : 1u);
+    const int64_t keep = (int64_t)(kMallKeepBytes / per_task);
+    return plan->ntasks > keep ? plan->ntasks - keep : 0;
+}
+
 template <class G> struct PrepassL {
     template <class... A> static void launch(dim3 g, hipStream_t s, A... a) {
         prepass_kernel<G><<<g, dim3(kBlock), 0, s>>>(a...);
@@ -960,8 +1075,8 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale, const nt_amp
                                                          xf, ctrl, plan->d_partials);
     } else {
         rc = grad_dispatch<PrepassL>(plan->layout.grad_dtype, grid, s, (const DevTensor *)plan->d_tensors,
-                                     (const Task *)plan->d_tasks, plan->ntasks, plan->chunk, xf, ctrl,
-                                     plan->d_partials);
+                                     (const Task *)plan->d_tasks, plan->ntasks, plan->chunk, keep_from_task(plan),
+                                     xf, ctrl, plan->d_partials);
         if (rc != NT_OK) return rc;
     }
     NT_LAUNCH_CHECK("prepass_kernel launch");
@@ -996,6 +1111,34 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *car
         src, count, ctrl, carry, norm_type, max_norm, flags, growth_factor,
         backoff_factor, growth_interval);
     NT_LAUNCH_CHECK("finalize_kernel launch");
+    return NT_OK;
+}
+
+int32_t nt_amp_combine(nt_amp_ctrl *const *blocks, int32_t n, const nt_amp_ctrl *carry, double norm_type,
+                       double max_norm, int32_t flags, double growth_factor, double backoff_factor,
+                       int32_t growth_interval, void *stream) {
+    clear_error();
+    if (blocks == nullptr || n < 1 || n > NT_MAX_COMBINE)
+        return fail(NT_ERR_VALUE, "nt_amp_combine: 1 to " + std::to_string(NT_MAX_COMBINE) + " control blocks required");
+    if (carry == nullptr) return fail(NT_ERR_VALUE, "nt_amp_combine: carry block is NULL");
+    CombineBlocks list{};
+    for (int32_t i = 0; i < n; ++i) {
+        if (blocks[i] == nullptr) return fail(NT_ERR_VALUE, "control block is NULL");
+        if (blocks[i] == carry) return fail(NT_ERR_VALUE, "nt_amp_combine: carry and a combined block must differ");
+        for (int32_t j = 0; j < i; ++j)
+            if (blocks[j] == blocks[i]) return fail(NT_ERR_VALUE, "nt_amp_combine: a control block is listed twice");
+        list.block[i] = blocks[i];
+    }
+    if (!(norm_type == 2.0 || (__builtin_isinf(norm_type) && norm_type > 0.0)))
+        return fail(NT_ERR_VALUE, "nt_amp_combine: norm_type must be 2 or positive infinity");
+    if (flags & ~(NT_FINALIZE_SCALER_UPDATE | NT_FINALIZE_CLIP_IF_FINITE))
+        return fail(NT_ERR_VALUE, "nt_amp_combine: unknown flags");
+    if ((flags & NT_FINALIZE_SCALER_UPDATE) &&
+        (growth_interval <= 0 || !(growth_factor > 1.0) || !(backoff_factor > 0.0 && backoff_factor < 1.0)))
+        return fail(NT_ERR_VALUE, "invalid GradScaler growth/backoff settings");
+    combine_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>(list, n, carry, norm_type, max_norm, flags,
+                                                                  growth_factor, backoff_factor, growth_interval);
+    NT_LAUNCH_CHECK("combine_kernel launch");
     return NT_OK;
 }
 

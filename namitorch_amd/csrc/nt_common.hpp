@@ -23,6 +23,14 @@ constexpr int kPass2Unroll = 4;    // groups in flight per lane in the multi-ten
 constexpr int kPass2Tile = kBlock * kVec * kPass2Unroll;
 constexpr int kPassSlice = 256;    // elements per one-wave workgroup of the split multi-tensor pass
 constexpr uint32_t kFp32XcdGroup = 256;   // workgroups per XCD per group, all-float32 pass layout
+// Gradient bytes the pre-pass leaves resident in the MI355X's 256 MB Infinity
+// Cache (MALL) for the AdamW pass that follows it: the pre-pass reads its last
+// tasks, up to this many bytes, with temporal loads (which allocate in the
+// MALL) and the rest nontemporally (which do not).  The pass's own accesses are
+// nontemporal, so they find those gradients still resident.  Timed against
+// 128-4096 MiB windows at either end of the task list (same buffers, one
+// process): a 320 MiB window at the end was the best or level on every layout.
+constexpr uint64_t kMallKeepBytes = 320ull << 20;
 
 // ---- bit casts ---------------------------------------------------------------
 __device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }

@@ -177,9 +177,14 @@ def _stats_snapshot(gradients) -> tuple:
 
 
 def _remember_stats(snapshot: tuple, stats: GradStats) -> None:
-    """Cache `stats` with the ``_stats_snapshot`` taken when the pre-pass was queued."""
+    """Cache `stats` with the ``_stats_snapshot`` taken when the pre-pass was
+    queued, unless a version counter has moved since the snapshot (a settled
+    device step may lower one, after which the snapshot's value could come
+    back with other contents)."""
     _last_stats.clear()
-    _last_stats["last"] = (snapshot, stats)
+    held, ids, counters, versions, pendings = snapshot
+    if tuple(map(_VALUE_OF, counters)) == versions:
+        _last_stats["last"] = (snapshot, stats)
 
 
 def _cached_stats(gradients) -> GradStats | None:

@@ -64,6 +64,11 @@ class _VersionCounter:
         self.value = value
 
     def increment(self) -> None:
+        """One in-place write.  Device-decided steps still pending settle
+        first, so the optimistic bumps they undo are never mixed with this
+        write's."""
+        if _unsettled_steps:
+            _settle_device_steps()
         self.value += 1
 
 

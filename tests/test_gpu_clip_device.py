@@ -357,3 +357,83 @@ def test_device_clip_then_unscale_then_step():
         oadam.adam_step(value, np.asarray(unscaled, np.float32), m, v, 1, lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
                         weight_decay=0.1)
         assert _same(p.numpy(), value)
+
+
+@pytest.mark.parametrize("consumer", ["step", "version read"])
+def test_cached_norm_after_an_undone_clip_bump(consumer):
+    """A device clip that decides not to clip bumps the gradients' versions
+    before the decision is known; settling the step lowers them again.  Norm
+    statistics cached in between (get_grad_norm over the pending transform
+    takes the host path and caches them under the bumped version) must not
+    answer for the values written after the settle, whose version equals the
+    bumped one again."""
+    grads = _grads(23, "float32")
+    params = _params(grads, "float32")
+    optimizer = nt.optim.AdamW(params, lr=1e-3)
+    before = [p.grad._version for p in params]
+    want = oclip.total_norm([g.astype(np.float64) for g in grads])
+    nt.optim.clip_grad_norm_(params, want * 4)                  # coefficient > 1: no clip, decided on the device
+    assert params[0].grad._pending is not None and params[0].grad._pending.device is not None
+    cached = nt.optim.get_grad_norm(params).item()              # host path over the pending transform
+    assert abs(cached - want) <= NORM_RTOL * want
+    if consumer == "step":
+        optimizer.step()
+        optimizer.state[id(params[0])]["exp_avg"].numpy()
+    assert [p.grad._version for p in params] == before          # settled: the bump is undone
+    fresh = _grads(29, "float32", sigma=3e-2)
+    with nt.no_grad():
+        for p, g in zip(params, fresh):
+            p.grad.copy_(nt.Tensor(g, device=DEV))
+    assert [p.grad._version for p in params] == [b + 1 for b in before]
+    want_fresh = oclip.total_norm([g.astype(np.float64) for g in fresh])
+    assert abs(want_fresh - want) > 0.5 * want                  # a stale norm would be detected
+    got = nt.optim.get_grad_norm(params).item()
+    assert abs(got - want_fresh) <= NORM_RTOL * want_fresh, (got, want_fresh, cached)
+    host = nt.optim.clip_grad_norm_(params, want_fresh / 2, error_if_nonfinite=True).item()
+    assert abs(host - want_fresh) <= NORM_RTOL * want_fresh, (host, want_fresh)
+    coefficient = oclip.clip_coefficient(want_fresh / 2, host)
+    for p, g in zip(params, fresh):
+        assert _same(p.grad.numpy(), oclip.clip_apply(g.astype(np.float64), coefficient, "float32"))
+
+
+@pytest.mark.parametrize("write", ["copy_", "zero_", "accumulate", "clip"])
+def test_versions_when_a_write_lands_before_the_clip_settles(write):
+    """A device clip that decides not to clip, followed, before anything
+    settles it, by one more write of the gradients: the versions count that
+    one write only, as the reference's do (a clip with coefficient >= 1 does
+    not write, optim/clip_grad.py:108-111; every other write is one
+    copy_, tensor.py:1283-1287)."""
+    from namitorch_amd.grads import accumulate_grads
+    grads = _grads(31, "float32")
+    params = _params(grads, "float32")
+    before = [p.grad._version_counter.value for p in params]
+    want = oclip.total_norm([g.astype(np.float64) for g in grads])
+    nt.optim.clip_grad_norm_(params, want * 4)                  # no clip, decided on the device
+    assert params[0].grad._pending is not None and params[0].grad._pending.device is not None
+    fresh = _grads(37, "float32")
+    if write == "copy_":
+        with nt.no_grad():
+            for p, g in zip(params, fresh):
+                p.grad.copy_(nt.Tensor(g, device=DEV))
+        expected = fresh
+    elif write == "zero_":
+        for p in params:
+            p.grad.zero_()
+        expected = [np.zeros_like(g) for g in grads]
+    elif write == "accumulate":
+        accumulate_grads(params, [nt.Tensor(g, device=DEV) for g in fresh])
+        expected = [np.float32(a) + np.float32(b) for a, b in zip(grads, fresh)]
+    else:
+        # a second clip that clips: over the pending device transform it
+        # decides on the host (one write)
+        nt.optim.clip_grad_norm_(params, want / 2)
+        coefficient = oclip.clip_coefficient(want / 2, want)
+        expected = [oclip.clip_apply(g.astype(np.float64), coefficient, "float32") for g in grads]
+    assert [p.grad._version for p in params] == [b + 1 for b in before], write
+    for p, g in zip(params, expected):
+        got = p.grad.numpy()
+        if write == "clip":
+            # the norm itself is the oracle's within NORM_RTOL, so the coefficient may differ in its last bits
+            assert np.allclose(got, np.asarray(g, np.float32), rtol=1e-6, atol=0), write
+        else:
+            assert _same(got, np.asarray(g, np.float32)), write

@@ -79,32 +79,3 @@ def test_probe_rejects_bad_arguments():
         call(None, 1, 0, _pointers([b]), 1, 0)
     torch.cuda.synchronize()
     assert torch.all(b == 1.0)
-
-
-@pytest.mark.parametrize("mix", [0, 1])
-def test_every_launch_shape_updates_each_element_once(mix):
-    """nt_stream_probe_shape: every shape applies the same per-element
-    update exactly once, so all shapes leave identical bytes (persistent
-    grids larger than the tile count included)."""
-    count = 8192 * 3
-    stream = torch.cuda.current_stream().cuda_stream
-    gen = torch.Generator(device="cuda").manual_seed(5)
-    dtypes = (torch.float32,) * 4 if mix == 0 else (torch.float32,) + (torch.bfloat16,) * 4
-    start = [torch.rand(count, generator=gen, device="cuda").to(dtype) for dtype in dtypes]
-    direct_to_lds = 11                                     # NT_SHAPE_DIRECT_TO_LDS: fp32 streams only
-    shapes = [shape for shape in range(13) if not (mix == 1 and shape == direct_to_lds)]
-    results = []
-    for shape in shapes:
-        buffers = [t.clone() for t in start]
-        table = _pointers(buffers)
-        _native.call("nt_stream_probe_shape", mix, shape, table, count, 8, stream)
-        torch.cuda.synchronize()
-        results.append([b.view(torch.int16 if b.dtype == torch.bfloat16 else torch.int32).cpu() for b in buffers])
-    for shape, result in zip(shapes[1:], results[1:]):
-        for k, (a, b) in enumerate(zip(results[0], result)):
-            assert torch.equal(a, b), (mix, shape, k)
-    assert not torch.equal(results[0][0], start[0].view(torch.int32).cpu())       # it did update
-    with pytest.raises(ValueError, match="no variant"):
-        _native.call("nt_stream_probe_shape", 1, 11, _pointers([t.clone() for t in start]), count, 8, stream)
-    with pytest.raises(ValueError, match="multiple of 8192"):
-        _native.call("nt_stream_probe_shape", mix, 0, _pointers(start), 4096, 8, stream)
