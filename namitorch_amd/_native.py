@@ -30,6 +30,7 @@ NT_BF16 = 2
 NT_F64 = 3
 
 NT_MAX_SLOTS = 16
+NT_MAX_COMBINE = 8
 NT_FINALIZE_SCALER_UPDATE = 1
 NT_FINALIZE_CLIP_IF_FINITE = 2
 ABI_VERSION = 3

@@ -255,6 +255,45 @@ def test_control_blocks_and_small_kernels():
     assert int(flag.item()) == 0                                          # cleared before the checks failed
 
 
+def test_combine_arguments():
+    size = ctypes.sizeof(_native.AmpCtrl)
+    blocks = [torch.zeros(size, dtype=torch.uint8, device=DEV) for _ in range(_native.NT_MAX_COMBINE + 2)]
+    carry = blocks[-1].data_ptr()
+
+    def table(*tensors):
+        return (ctypes.c_void_p * max(1, len(tensors)))(*[t if isinstance(t, int) or t is None else t.data_ptr()
+                                                          for t in tensors])
+
+    def combine(pointers, n, carry_ptr=carry, norm_type=2.0, flags=0, growth=2.0, backoff=0.5, interval=2000):
+        _call("nt_amp_combine", pointers, n, carry_ptr, norm_type, 1.0, flags, growth, backoff, interval, _stream())
+
+    two = table(blocks[0], blocks[1])
+    for n in (0, -1, _native.NT_MAX_COMBINE + 1):
+        with pytest.raises(ValueError, match="control blocks required"):
+            combine(table(*blocks[:max(n, 1)]), n)
+    with pytest.raises(ValueError, match="control blocks required"):
+        combine(None, 2)
+    with pytest.raises(ValueError, match="carry block is NULL"):
+        combine(two, 2, carry_ptr=None)
+    with pytest.raises(ValueError, match="control block is NULL"):
+        combine(table(blocks[0], None), 2)
+    with pytest.raises(ValueError, match="carry and a combined block"):
+        combine(table(blocks[0], carry), 2)
+    with pytest.raises(ValueError, match="listed twice"):
+        combine(table(blocks[0], blocks[1], blocks[0]), 3)
+    for norm_type in (1.0, 3.0, float("-inf"), float("nan")):
+        with pytest.raises(ValueError, match="norm_type must be 2 or positive infinity"):
+            combine(two, 2, norm_type=norm_type)
+    with pytest.raises(ValueError, match="unknown flags"):
+        combine(two, 2, flags=4)
+    update = _native.NT_FINALIZE_SCALER_UPDATE
+    for growth, backoff, interval in ((1.0, 0.5, 10), (2.0, 1.0, 10), (2.0, 0.5, 0)):
+        with pytest.raises(ValueError, match="growth/backoff"):
+            combine(two, 2, flags=update, growth=growth, backoff=backoff, interval=interval)
+    torch.cuda.synchronize()
+    assert all(int(b.sum().item()) == 0 for b in blocks)                  # nothing was launched
+
+
 def test_gradient_edges_and_pointer_columns(plans):
     grads = plans((NONE, BF16, NONE, NONE), [4096, 100])
     with pytest.raises(ValueError, match="plan is NULL"):
