@@ -68,6 +68,11 @@ class DeviceStep:
         self.scheduler = None                 # advanced at reconciliation iff the step updated
         self.ready = None                     # event after the finalize, on `stream`
         self.stream = None
+        # fused_step(error_if_nonfinite=True) without a scaler: a non-finite
+        # norm skipped the clip and the step on the device; the reference's
+        # error is kept here once the outcome is known.
+        self.error_if_nonfinite = False
+        self.error: RuntimeError | None = None
 
     def block_for_current_stream(self):
         """The control block, safe to read from work queued next on the
@@ -161,6 +166,30 @@ class DeviceStep:
         scheduler, self.scheduler = self.scheduler, None    # no reference cycle through it once settled
         if scheduler is not None and not (self.honor_skip and ctrl.skip):
             scheduler._advance()              # training/runner.py:252-253: only after an update
+        if self.error_if_nonfinite and not math.isfinite(ctrl.norm):
+            # optim/clip_grad.py:104-105, with the norm printed as there (a 0-d float64 array)
+            self.error = RuntimeError(
+                f"Cannot clip gradients with nonfinite total norm {np.asarray(ctrl.norm, dtype=np.float64)}.")
+
+    def raise_error(self) -> None:
+        """Settle; raise the deferred ``error_if_nonfinite`` error, if any
+        (raised here, it is not raised again by the next fused_step)."""
+        if self.error_if_nonfinite:
+            self.reconcile()
+            if self.error is not None:
+                _error_watch[:] = [step for step in _error_watch if step is not self]
+                raise self.error
+
+
+# Fused steps taken with error_if_nonfinite=True whose error (if any) has not
+# been raised yet: the next fused_step raises it before doing anything.
+_error_watch: list = []
+
+
+def _raise_deferred_errors() -> None:
+    while _error_watch:
+        device_step = _error_watch.pop(0)
+        device_step.raise_error()
 
 
 class StepResult:
@@ -171,35 +200,42 @@ class StepResult:
         self._device_step = device_step
         self._eager = (finite, updated, norm, scale)
 
+    def _ctrl(self):
+        """The step's control block; raises the deferred error_if_nonfinite
+        error of a step whose clip found a non-finite norm."""
+        self._device_step.raise_error()
+        return self._device_step.ctrl()
+
     @property
     def finite(self) -> bool:
         if self._device_step is None:
             return self._eager[0]
-        return not self._device_step.ctrl().found_inf
+        return not self._ctrl().found_inf
 
     @property
     def updated(self) -> bool:
         if self._device_step is None:
             return self._eager[1]
-        return not (self._device_step.honor_skip and self._device_step.ctrl().skip)
+        return not (self._device_step.honor_skip and self._ctrl().skip)
 
     @property
     def norm(self):
         """Global grad norm (float), or None when no norm was requested."""
         if self._device_step is None:
             return self._eager[2]
-        return self._device_step.ctrl().norm if self._device_step.clip_requested else None
+        return self._ctrl().norm if self._device_step.clip_requested else None
 
     @property
     def scale(self) -> float:
         """Loss scale for the next iteration."""
         if self._device_step is None:
             return self._eager[3]
-        return float(self._device_step.ctrl().scale)
+        return float(self._ctrl().scale)
 
     def synchronize(self) -> "StepResult":
         if self._device_step is not None:
             self._device_step.reconcile()
+            self._device_step.raise_error()
         return self
 
 
@@ -471,7 +507,7 @@ class GradScaler:
 
 
 def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, norm_type=2.0,
-               scheduler=None) -> StepResult:
+               scheduler=None, error_if_nonfinite: bool = False) -> StepResult:
     """One optimizer step with the reference training loop's AMP/clip
     semantics and no host synchronization.
 
@@ -486,7 +522,14 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     asynchronous snapshot of the control block and reconciles its
     bookkeeping (``state['step']``, version counters, the scale mirror) at
     the next step, ``get_scale``/``state_dict`` or ``StepResult`` access.
-    ``error_if_nonfinite`` has no equivalent here (it would need the host).
+
+    ``error_if_nonfinite`` is ``clip_grad_norm_``'s.  With a scaler the clip
+    only runs after a finite unscale, whose norm is finite, so it never
+    raises.  Without one, a non-finite norm leaves the gradients, parameters
+    and state untouched on the device (the clip and the step are skipped, as
+    the reference's raise prevents both), and the reference's RuntimeError
+    is raised once the host learns the outcome: at the first access to the
+    returned StepResult, or else at the start of the next ``fused_step``.
 
     ``optimizer`` may also be a list or tuple of optimizers that share the
     scaler's iteration (``_fused_step_many``): ``scheduler`` is then None or
@@ -501,8 +544,11 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     the schedule.
     """
     reject_during_capture("Optimizer steps")
+    if type(error_if_nonfinite) is not bool:
+        raise TypeError("error_if_nonfinite must be a Python bool.")
+    _raise_deferred_errors()
     if isinstance(optimizer, (list, tuple)):
-        return _fused_step_many(list(optimizer), scaler, max_norm, norm_type, scheduler)
+        return _fused_step_many(list(optimizer), scaler, max_norm, norm_type, scheduler, error_if_nonfinite)
     _check_scheduler(scheduler, optimizer)
     amp, maximum, order = _fused_arguments(scaler, max_norm, norm_type)
     pairs = GradScaler._gradients(optimizer)
@@ -511,7 +557,8 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         raise RuntimeError("No gradients were found for this optimizer.")
     groups = _device_groups(gradients)
     if len(groups) != 1:
-        result = _fused_step_host(optimizer, scaler, amp, maximum, order, [p for p, _ in pairs])
+        result = _fused_step_host(optimizer, scaler, amp, maximum, order, [p for p, _ in pairs],
+                                  error_if_nonfinite)
         if scheduler is not None and result.updated:
             scheduler.step()
         return result
@@ -531,9 +578,12 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         previous = backend.neutral_ctrl()
     block = backend.empty_ctrl()
     clip_bumps: list = []
-    device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps)
+    # error_if_nonfinite without a scaler: a non-finite norm skips the clip and the step.
+    refuse = error_if_nonfinite and not amp and maximum is not None
+    device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp or refuse, clip_bumps=clip_bumps)
     device_step.clip_requested = maximum is not None
     device_step.scheduler = scheduler
+    device_step.error_if_nonfinite = refuse
     transform = GradTransform(device=device_step)
     if (any(map(_REQUIRES, gradients)) and is_grad_enabled()) or not all(map(_WRITABLE, gradients)):
         for gradient in gradients:
@@ -556,6 +606,8 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     plan = backend.grad_plan(gradients, dtype, incoming=True)
     backend.grad_prepass(plan, None, previous.data_ptr(), unscale=amp)
     flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
+    if refuse:
+        flags |= _native.NT_FINALIZE_CLIP_IF_FINITE
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)
     backend.grad_finalize(plan, block.data_ptr(), order, -1.0 if maximum is None else maximum, flags,
                           growth, backoff, interval, carry_ptr=previous.data_ptr())
@@ -574,6 +626,8 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     optimizer.step()                                      # the AdamW pass reads the control block
     optimizer._track_device_step(device_step)
     _unsettled_steps.append(device_step)                  # version reads settle it first
+    if refuse:
+        _error_watch.append(device_step)
     return StepResult(device_step)
 
 
@@ -602,7 +656,7 @@ def _fused_arguments(scaler, max_norm, norm_type) -> tuple:
     return amp, maximum, order
 
 
-def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers) -> list:
+def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers, error_if_nonfinite=False) -> list:
     """``fused_step`` over several optimizers in one scaler iteration: the
     reference loop's ``unscale_`` of every optimizer, ``clip_grad_norm_`` of
     all their parameters when every ``unscale_`` returned True (when
@@ -648,13 +702,15 @@ def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers) 
     groups = [_device_groups(gradients) for gradients in gathered]
     keys = [next(iter(g)) if len(g) == 1 else None for g in groups]
     distinct = len({id(optimizer) for optimizer in optimizers}) == len(optimizers)
-    if (not distinct or len(optimizers) > _native.NT_MAX_COMBINE or any(key is None for key in keys)
+    refuse = error_if_nonfinite and not amp and maximum is not None
+    if (refuse or not distinct or len(optimizers) > _native.NT_MAX_COMBINE or any(key is None for key in keys)
             or len({id(key[0]) for key in keys}) != 1 or any(key[1] is float64 for key in keys)
             or keys[0][0].adamw is None):
         # Several devices, mixed dtypes within an optimizer, float64 (its
-        # guarded second norm pass), repeated optimizers or more optimizers
-        # than one combine takes: the synchronizing API gives the same results.
-        return _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers)
+        # guarded second norm pass), repeated optimizers, more optimizers
+        # than one combine takes, or a clip that may raise without a scaler:
+        # the synchronizing API gives the same results.
+        return _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers, error_if_nonfinite)
     backend = keys[0][0]
     for gradients in gathered:
         if (any(map(_REQUIRES, gradients)) and is_grad_enabled()) or not all(map(_WRITABLE, gradients)):
@@ -710,21 +766,21 @@ def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers) 
     return [StepResult(device_step) for device_step in device_steps]
 
 
-def _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers) -> list:
+def _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers, error_if_nonfinite=False) -> list:
     """``_fused_step_many`` through the host-synchronizing API."""
     parameters = [parameter for optimizer in optimizers for parameter, _ in GradScaler._gradients(optimizer)]
     norm = None
     if amp:
         finite = [scaler.unscale_(optimizer) for optimizer in optimizers]
         if all(finite) and maximum is not None:
-            norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+            norm = clip_grad_norm_(parameters, maximum, norm_type=order, error_if_nonfinite=error_if_nonfinite).item()
         updated = [scaler.step(optimizer) for optimizer in optimizers]
         scaler.update()
         scale = scaler.get_scale()
         results = [StepResult(finite=f, updated=u, norm=norm, scale=scale) for f, u in zip(finite, updated)]
     else:
         if maximum is not None:
-            norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+            norm = clip_grad_norm_(parameters, maximum, norm_type=order, error_if_nonfinite=error_if_nonfinite).item()
         for optimizer in optimizers:
             optimizer.step()
         finite = None if norm is None else math.isfinite(norm)
@@ -735,19 +791,19 @@ def _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers) -
     return results
 
 
-def _fused_step_host(optimizer, scaler, amp, maximum, order, parameters) -> StepResult:
+def _fused_step_host(optimizer, scaler, amp, maximum, order, parameters, error_if_nonfinite=False) -> StepResult:
     """Several devices or gradient dtypes: the same sequence through the
     host-synchronizing API (identical results)."""
     norm = None
     if amp:
         finite = scaler.unscale_(optimizer)
         if finite and maximum is not None:
-            norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+            norm = clip_grad_norm_(parameters, maximum, norm_type=order, error_if_nonfinite=error_if_nonfinite).item()
         updated = scaler.step(optimizer)
         scaler.update()
         return StepResult(finite=finite, updated=updated, norm=norm, scale=scaler.get_scale())
     if maximum is not None:
-        norm = clip_grad_norm_(parameters, maximum, norm_type=order).item()
+        norm = clip_grad_norm_(parameters, maximum, norm_type=order, error_if_nonfinite=error_if_nonfinite).item()
     optimizer.step()
     return StepResult(finite=None if norm is None else math.isfinite(norm), updated=True, norm=norm, scale=1.0)
 
