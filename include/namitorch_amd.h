@@ -132,6 +132,23 @@ typedef struct nt_amp_ctrl {
 } nt_amp_ctrl; /* 72 bytes */
 
 /*
+ * Page-locked host mirror of one control block.  nt_amp_finalize and
+ * nt_amp_combine, given a mirror, store the block's final contents in
+ * `ctrl` and then set `ready` to 1 with a system-scope release, so the
+ * host reads the iteration's decisions (skip, scale, norm) without an event
+ * on the launch stream: the host clears `ready` before the launch and reads
+ * `ctrl` once `ready` is 1.  Mirrors come from nt_mirror_alloc
+ * (fine-grained page-locked memory, which the device writes through to the
+ * host).  No reference counterpart: the reference reads these values with
+ * blocking device-to-host copies (amp.py:152-167, .item()).
+ */
+typedef struct nt_amp_mirror {
+    nt_amp_ctrl ctrl;
+    int32_t ready;
+    int32_t reserved;
+} nt_amp_mirror; /* 80 bytes */
+
+/*
  * How pass 2 turns a stored grad into the one AdamW consumes.  With
  * `ctrl == NULL` the host-known values below are used: unscale divides by
  * `scale` in fp32 and rounds to the grad dtype (amp.py:190-191); clip
@@ -206,6 +223,15 @@ int32_t nt_empty_cache(int32_t device);
 /* Page-locked host memory (hipHostMalloc). */
 int32_t nt_host_alloc(uint64_t bytes, void **out);
 int32_t nt_host_free(void *ptr);
+/* `count` zeroed control-block mirrors in one fine-grained page-locked
+ * allocation (hipHostMallocCoherent); nt_mirror_free releases it. */
+int32_t nt_mirror_alloc(int32_t count, nt_amp_mirror **out);
+int32_t nt_mirror_free(nt_amp_mirror *mirrors);
+/* Wait for `mirror`'s flag, set by a kernel queued on `stream`: polls the
+ * flag, querying the stream every 64 polls; NT_ERR_RUNTIME when all the
+ * stream's work completed and the flag is still clear.  Records nothing on
+ * the stream. */
+int32_t nt_mirror_wait(const nt_amp_mirror *mirror, void *stream);
 /* Streams are created at the default priority and do not synchronize with
  * the null stream.  nt_stream_destroy waits for the stream's work first;
  * plans and pool blocks that were used on it may still be destroyed or
@@ -343,11 +369,12 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale,
  * from *carry as nt_ctrl_carry(ctrl, carry) would set it, so a new
  * iteration's block needs no carry launch; with NULL it starts from *ctrl.
  * The pre-pass of such an iteration reads the scale from `carry`'s block.
+ * `mirror` (may be NULL) receives a host copy of the finished block.
  */
 int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry,
                         double norm_type, double max_norm, int32_t flags,
                         double growth_factor, double backoff_factor,
-                        int32_t growth_interval, void *stream);
+                        int32_t growth_interval, nt_amp_mirror *mirror, void *stream);
 
 /*
  * One GradScaler iteration over several optimizers (amp.py:169-233 called
@@ -367,12 +394,13 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *car
  * sumsq/amax/found_inf/has_nan with skip = its own found_inf: each
  * optimizer's step checks only its own gradients (GradScaler.step,
  * amp.py:209-217).  No single reference function: it is the composition the
- * reference runs on the host.
+ * reference runs on the host.  `mirrors` (may be NULL, else n entries, each
+ * may be NULL) receive host copies of the finished blocks.
  */
 int32_t nt_amp_combine(nt_amp_ctrl *const *blocks, int32_t n, const nt_amp_ctrl *carry,
                        double norm_type, double max_norm, int32_t flags,
                        double growth_factor, double backoff_factor,
-                       int32_t growth_interval, void *stream);
+                       int32_t growth_interval, nt_amp_mirror *const *mirrors, void *stream);
 
 /*
  * General p-norm (0 < p < inf) of optim/clip_grad.py:70-79: sum over

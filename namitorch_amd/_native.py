@@ -33,7 +33,7 @@ NT_MAX_SLOTS = 16
 NT_MAX_COMBINE = 8
 NT_FINALIZE_SCALER_UPDATE = 1
 NT_FINALIZE_CLIP_IF_FINITE = 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 NT_NORM_POW_GUARD = 1
 NT_OP_MUL = 0
 NT_OP_DIV = 1
@@ -105,6 +105,12 @@ class AmpCtrl(ctypes.Structure):
     ]
 
 
+class AmpMirror(ctypes.Structure):
+    """Page-locked host copy of a control block (``nt_amp_mirror``): the
+    finalize stores ``ctrl``, then sets ``ready`` to 1."""
+    _fields_ = [("ctrl", AmpCtrl), ("ready", c_int32), ("reserved", c_int32)]
+
+
 class GradXform(ctypes.Structure):
     _fields_ = [
         ("scale", c_float),
@@ -120,6 +126,7 @@ assert ctypes.sizeof(MtTensor) == 56
 assert ctypes.sizeof(AdamWCoefs) == 56
 assert ctypes.sizeof(AdamWCoefs64) == 96
 assert ctypes.sizeof(AmpCtrl) == 72
+assert ctypes.sizeof(AmpMirror) == 80
 assert ctypes.sizeof(GradXform) == 32
 
 # name -> (restype, argtypes); every entry point returns an int32 status.
@@ -140,9 +147,9 @@ SIGNATURES = {
     "nt_adamw_mt": (c_int32, [c_void_p, c_void_p, c_int32, ctypes.POINTER(GradXform), c_void_p]),
     "nt_amp_prepass": (c_int32, [c_void_p, c_float, c_int32, c_void_p, c_void_p]),
     "nt_amp_finalize": (c_int32, [c_void_p, c_void_p, c_void_p, c_double, c_double, c_int32, c_double, c_double, c_int32,
-                                  c_void_p]),
+                                  c_void_p, c_void_p]),
     "nt_amp_combine": (c_int32, [ctypes.POINTER(c_void_p), c_int32, c_void_p, c_double, c_double, c_int32, c_double,
-                                 c_double, c_int32, c_void_p]),
+                                 c_double, c_int32, ctypes.POINTER(c_void_p), c_void_p]),
     "nt_grad_norm_pow": (c_int32, [c_void_p, c_void_p, c_double, c_double, c_float, c_int32, c_int32, c_int32, c_void_p]),
     "nt_grad_apply": (c_int32, [c_void_p, ctypes.POINTER(GradXform), c_void_p]),
     "nt_grad_zero": (c_int32, [c_void_p, c_void_p]),
@@ -163,6 +170,9 @@ SIGNATURES = {
     "nt_empty_cache": (c_int32, [c_int32]),
     "nt_host_alloc": (c_int32, [c_uint64, ctypes.POINTER(c_void_p)]),
     "nt_host_free": (c_int32, [c_void_p]),
+    "nt_mirror_alloc": (c_int32, [c_int32, ctypes.POINTER(c_void_p)]),
+    "nt_mirror_free": (c_int32, [c_void_p]),
+    "nt_mirror_wait": (c_int32, [c_void_p, c_void_p]),
     "nt_stream_create": (c_int32, [c_int32, ctypes.POINTER(c_void_p)]),
     "nt_stream_destroy": (c_int32, [c_void_p]),
     "nt_stream_wait_event": (c_int32, [c_void_p, c_void_p]),

@@ -51,22 +51,25 @@ _GRAD = attrgetter("_grad")
 
 class DeviceStep:
     """One iteration whose unscale/finite/clip/skip/scale decisions were taken
-    on the device: its control block, an asynchronous host snapshot of that
-    block, and the host-side bookkeeping to undo if the step was skipped."""
+    on the device: its control block, the page-locked host mirror that the
+    block's last writer fills, and the host-side bookkeeping to undo if the
+    step was skipped."""
 
-    def __init__(self, backend, block, unscale: bool, honor_skip: bool, clip_bumps: list):
+    def __init__(self, backend, block, unscale: bool, honor_skip: bool, clip_bumps: list, mirror=None):
         self.backend = backend
         self.block = block
         self.unscale = unscale
         self.honor_skip = honor_skip
         self.records: list = []
         self.clip_bumps = clip_bumps          # (gradient, version after the optimistic clip bump)
-        self.snapshot = runtime.take_pinned(ctypes.sizeof(_native.AmpCtrl))
-        self.event = runtime.Event()
+        # runtime.take_mirror(), passed to the block's last writer (finalize or
+        # combine); None: the block is read back with a copy after an event.
+        self.mirror = mirror
+        self.launched = False                 # a kernel that writes `mirror` was queued
         self._ctrl = None
         self._reconciled = False
         self.scheduler = None                 # advanced at reconciliation iff the step updated
-        self.ready = None                     # event after the finalize, on `stream`
+        self.ready = None                     # event on `stream` after the block's last writer, once needed
         self.stream = None
         # fused_step(error_if_nonfinite=True) without a scaler: a non-finite
         # norm skipped the clip and the step on the device; the reference's
@@ -82,36 +85,39 @@ class DeviceStep:
         current = self.backend.stream()
         if self.stream is not None and current != self.stream:
             with self.backend.context():
-                _native.call("nt_stream_wait_event", current, self.ready.handle)
+                _native.call("nt_stream_wait_event", current, self._ready_event().handle)
                 self.block.record_stream(current)
         return self.block
 
+    def _ready_event(self):
+        """An event on the step's stream after the block's last writer.  It is
+        recorded when first needed (another stream reads the block, or the
+        host needs the block before its mirror is written), later than the
+        writer but never before it: an event on the launch stream is a
+        marker that idles the device for several microseconds, so a step
+        whose mirror arrives in time records none."""
+        if self.ready is None:
+            with self.backend.context():
+                self.ready = runtime.Event().record(self.stream)
+        return self.ready
+
     def capture(self) -> None:
-        """Queue the copy of the control block to pinned host memory.  The
-        copy runs on the backend's side stream once the work queued so far
-        on the current stream is done, so the AdamW pass queued next does not
-        wait behind it.  Nothing writes the block after the finalize kernel."""
-        with self.backend.context():
-            self.stream = self.backend.stream()
-            # Work on another stream that reads this block waits on `ready`.
-            self.ready = runtime.Event().record(self.stream)
-            side = self.backend.side_stream()
-            side.wait_event(self.ready)
-            _native.call("nt_memcpy_async", self.snapshot.ctypes.data, self.block.data_ptr(), self.snapshot.nbytes,
-                         _native.NT_COPY_D2H, side.handle)
-            self.event.record(side.handle)
-            self.block.record_stream(side.handle)    # not reused before the copy has read it
+        """Note the stream the block's last writer was queued on; that
+        kernel also fills the host mirror.  Nothing writes the block after
+        it.  Without a mirror the block is read back after an event recorded
+        here."""
+        self.stream = self.backend.stream()
+        self.launched = True
+        if self.mirror is None:
+            self._ready_event()
 
     def __del__(self):
-        # A step dropped before its snapshot was read: wait for the copy into
-        # the page-locked buffer (it ran right after the finalize), then
-        # return the buffer to the pool rather than free it, which would wait
-        # for the whole device.
+        # A step dropped before its mirror was read: the mirror returns to
+        # the pool, which reuses it once its flag shows the write done.
         try:
-            if self.snapshot is not None and not _native.shutting_down():
-                self.event.synchronize()
-                runtime.give_pinned(self.snapshot)
-                self.snapshot = None
+            if self.mirror is not None and not _native.shutting_down():
+                runtime.give_mirror(self.mirror, self.launched)
+                self.mirror = None
         except Exception:
             pass
 
@@ -121,10 +127,17 @@ class DeviceStep:
 
     def ctrl(self) -> _native.AmpCtrl:
         if self._ctrl is None:
-            self.event.synchronize()
-            self._ctrl = _native.AmpCtrl.from_buffer_copy(self.snapshot.tobytes())
-            runtime.give_pinned(self.snapshot)       # the copy into it has completed
-            self.snapshot = None
+            mirror = self.mirror
+            if mirror is None:
+                self._ready_event().synchronize()      # the block's last writer has completed
+                self._ctrl = self.backend.read_ctrl(self.block)
+            else:
+                if not mirror.ready:
+                    with self.backend.context():
+                        _native.call("nt_mirror_wait", ctypes.addressof(mirror), self.stream)
+                self._ctrl = _native.AmpCtrl.from_buffer_copy(mirror)
+                runtime.give_mirror(mirror)
+                self.mirror = None
         return self._ctrl
 
     def reconcile(self) -> None:
@@ -580,7 +593,11 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     clip_bumps: list = []
     # error_if_nonfinite without a scaler: a non-finite norm skips the clip and the step.
     refuse = error_if_nonfinite and not amp and maximum is not None
-    device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp or refuse, clip_bumps=clip_bumps)
+    # float64 gradients may get a second norm pass after the finalize: that
+    # block is read back with a copy instead of the finalize's mirror.
+    mirror = None if dtype is float64 and order == 2.0 else runtime.take_mirror()
+    device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp or refuse, clip_bumps=clip_bumps,
+                             mirror=mirror)
     device_step.clip_requested = maximum is not None
     device_step.scheduler = scheduler
     device_step.error_if_nonfinite = refuse
@@ -610,7 +627,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         flags |= _native.NT_FINALIZE_CLIP_IF_FINITE
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)
     backend.grad_finalize(plan, block.data_ptr(), order, -1.0 if maximum is None else maximum, flags,
-                          growth, backoff, interval, carry_ptr=previous.data_ptr())
+                          growth, backoff, interval, carry_ptr=previous.data_ptr(), mirror=mirror)
     if dtype is float64 and order == 2.0:
         # fp64 squares can overflow or underflow: where max|g| says they may
         # have, the device redoes the norm with the reference's max-abs
@@ -727,7 +744,8 @@ def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers, 
     for gradients, (_, dtype), scheduler in zip(gathered, keys, schedulers):
         block = backend.empty_ctrl()
         clip_bumps: list = []
-        device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps)
+        device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps,
+                                 mirror=runtime.take_mirror())
         device_step.clip_requested = maximum is not None
         device_step.scheduler = scheduler
         transform = GradTransform(device=device_step)
@@ -751,7 +769,8 @@ def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers, 
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp \
         else (2.0, 0.5, 1)
     backend.grad_combine([device_step.block for device_step in device_steps], previous, order,
-                         -1.0 if maximum is None else maximum, flags, growth, backoff, interval)
+                         -1.0 if maximum is None else maximum, flags, growth, backoff, interval,
+                         mirrors=[device_step.mirror for device_step in device_steps])
     for device_step in device_steps:
         device_step.capture()
     if amp:

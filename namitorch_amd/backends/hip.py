@@ -213,7 +213,6 @@ class HIPBackend:
         self.adamw = AdamWHIPKernel(self)
         self._plans: OrderedDict = OrderedDict()
         self._lock = threading.RLock()
-        self._side_stream = None
         self._neutral_ctrl = None
         _backends_alive.add(self)
 
@@ -276,14 +275,6 @@ class HIPBackend:
     def synchronize(self) -> None:
         with self.context():
             _native.call("nt_stream_synchronize", self.stream())
-
-    def side_stream(self) -> runtime.Stream:
-        """A stream of this device (default priority) for small copies that
-        work queued on the caller's stream should not wait behind."""
-        with self._lock:
-            if self._side_stream is None:
-                self._side_stream = runtime.Stream(self.device.index)
-            return self._side_stream
 
     # ---- plans -----------------------------------------------------------------------------
     def plan(self, rows: list[tuple], layout: tuple, chunk: int = 0, pointers: dict | None = None) -> Plan:
@@ -379,20 +370,26 @@ class HIPBackend:
 
     def grad_finalize(self, plan: Plan, ctrl_ptr: int, norm_type: float = 2.0, max_norm: float = -1.0,
                       flags: int = 0, growth: float = 2.0, backoff: float = 0.5, interval: int = 2000,
-                      carry_ptr: int | None = None) -> None:
+                      carry_ptr: int | None = None, mirror=None) -> None:
         """Finalize into `ctrl_ptr`; with `carry_ptr` the block starts from
-        that block's scaler state (no separate carry launch)."""
+        that block's scaler state (no separate carry launch); `mirror` (a
+        ``runtime.take_mirror()``) receives the finished block on the host."""
         with self.context():
             _native.call("nt_amp_finalize", plan.handle, ctrl_ptr, carry_ptr, norm_type, max_norm, int(flags),
-                         growth, backoff, interval, self.stream())
+                         growth, backoff, interval, None if mirror is None else ctypes.addressof(mirror),
+                         self.stream())
 
     def grad_combine(self, blocks, carry, norm_type: float, max_norm: float, flags: int, growth: float,
-                     backoff: float, interval: int) -> None:
-        """nt_amp_combine over the finalized blocks (DeviceArrays), all carried from `carry`."""
+                     backoff: float, interval: int, mirrors=None) -> None:
+        """nt_amp_combine over the finalized blocks (DeviceArrays), all
+        carried from `carry`; `mirrors` (None, or one mirror or None per
+        block) receive the finished blocks on the host."""
         pointers = (ctypes.c_void_p * len(blocks))(*[block.data_ptr() for block in blocks])
+        hosts = None if mirrors is None else (ctypes.c_void_p * len(blocks))(
+            *[None if mirror is None else ctypes.addressof(mirror) for mirror in mirrors])
         with self.context():
             _native.call("nt_amp_combine", pointers, len(blocks), carry.data_ptr(), norm_type, max_norm, int(flags),
-                         growth, backoff, interval, self.stream())
+                         growth, backoff, interval, hosts, self.stream())
 
     def grad_norm_pow(self, plan: Plan, ctrl_ptr: int, norm_type: float, max_norm: float,
                       scale: float | None, scale_from_ctrl: bool = False, flags: int = 0) -> None:

@@ -279,6 +279,26 @@ struct TNone {
     __device__ static float round_f32(float x) { return x; }
 };
 
+// Occupancy cap of the one-wave pass for layouts with fp32 moments.  Each
+// workgroup reserves this many bytes of LDS that it never touches, so at most
+// 160 KiB / bytes one-wave workgroups are resident on a CU of the MI355X,
+// against 32 without it (8 waves per SIMD at the pass's 38-42 VGPRs).  With
+// 16 to 20 waves per CU in flight instead of 32, these mixes (28 bytes per
+// element of which 16 read) stream faster; bf16 moments (20 bytes per element)
+// stream slower with any cap.  Timed against no cap on the same buffers in
+// one process (fused steps, four rounds):
+//   all fp32 (GPT-2-124M):                 10240 B (16 per CU) -2.1 %
+//   fp16 gradients, GPT-2 AMP:              9216 B (17 per CU) -3.2 %
+//   bf16 gradients, Llama-7B and its 1/8:   8192 B (20 per CU) -1.0 % / -2.1 %
+//   bf16 moments, GPT-1.3B and its 1/8:     5 KiB level, 6-12 KiB +1.5 to +30 %
+template <class P, class G, class S>
+constexpr size_t pass_lds_cap() {
+    if constexpr (!std::is_same<P, TF32>::value || !std::is_same<S, TF32>::value) return 0;
+    else if constexpr (std::is_same<G, TF16>::value) return 9216;
+    else if constexpr (std::is_same<G, TBF16>::value) return 8192;
+    else return 10240;
+}
+
 // Launch shape of the pass.  A task whose size is a power-of-two multiple of
 // kPassSlice is split over one-wave workgroups of kPassSlice elements, one
 // 4-element group per lane: many short workgroups stream the pass's
@@ -299,8 +319,9 @@ static int32_t launch_mt(nt_plan *plan, const MtArgs &args, hipStream_t stream) 
     a.xcd_group = all_fp32 && a.split_shift > 0 ? kFp32XcdGroup : 0u;
     if (a.split_shift > 0) {
         static_assert(kPassSlice == 64 * kVec, "one 4-element group per lane of one wave");
-        adamw_mt_kernel<P, G, S, C, R, HAS_COPY, 64, 1><<<dim3((unsigned)(plan->ntasks << a.split_shift)), dim3(64), 0,
-                                                          stream>>>(plan->d_tensors, plan->d_tasks, a);
+        adamw_mt_kernel<P, G, S, C, R, HAS_COPY, 64, 1><<<dim3((unsigned)(plan->ntasks << a.split_shift)), dim3(64),
+                                                          pass_lds_cap<P, G, S>(), stream>>>(plan->d_tensors,
+                                                                                             plan->d_tasks, a);
     } else {
         adamw_mt_kernel<P, G, S, C, R, HAS_COPY, kBlock, kPass2Unroll><<<dim3((unsigned)plan->ntasks), dim3(kBlock), 0,
                                                                          stream>>>(plan->d_tensors, plan->d_tasks, a);

@@ -603,18 +603,29 @@ __device__ __forceinline__ void decide_iteration(nt_amp_ctrl &c, double sumsq, d
                                                  double norm_type, double max_norm, int32_t flags, double growth,
                                                  double backoff, int32_t interval);
 
+// Host copy of a finished block: the block's bytes go to the page-locked
+// mirror (fine-grained memory: the stores reach host memory, no device cache
+// keeps them), then a system-scope release orders them before `ready` = 1,
+// which the host reads before the block.
+__device__ __forceinline__ void publish(nt_amp_mirror *mirror, const nt_amp_ctrl &c) {
+    mirror->ctrl = c;
+    __hip_atomic_store(&mirror->ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // `carry` (optional): start from carried_ctrl(*carry) instead of *ctrl, so a
-// new iteration's block needs no separate carry kernel.
+// new iteration's block needs no separate carry kernel.  `mirror` (optional):
+// publish the finished block to the host.
 __global__ __launch_bounds__(kBlock) void finalize_kernel(const Partial *__restrict__ partials, int64_t n,
                                                           nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry,
                                                           double norm_type, double max_norm,
                                                           int32_t flags, double growth, double backoff,
-                                                          int32_t interval) {
+                                                          int32_t interval, nt_amp_mirror *mirror) {
     Acc r = reduce_partials(partials, 0, n);
     if (threadIdx.x != 0) return;
     nt_amp_ctrl c = carry != nullptr ? carried_ctrl(*carry) : *ctrl;
     decide_iteration(c, r.sumsq, r.amax, r.nan, r.inf, norm_type, max_norm, flags, growth, backoff, interval);
     *ctrl = c;
+    if (mirror != nullptr) publish(mirror, c);
 }
 
 // One iteration's decisions from its merged statistics (fp64 sum of squares
@@ -658,6 +669,7 @@ __device__ __forceinline__ void decide_iteration(nt_amp_ctrl &c, double sumsq, d
 // statistics and skip flag.
 struct CombineBlocks {
     nt_amp_ctrl *block[NT_MAX_COMBINE];
+    nt_amp_mirror *mirror[NT_MAX_COMBINE];   // NULL: no host copy of that block
 };
 
 __global__ void combine_kernel(CombineBlocks blocks, int32_t n, const nt_amp_ctrl *carry, double norm_type,
@@ -683,6 +695,7 @@ __global__ void combine_kernel(CombineBlocks blocks, int32_t n, const nt_amp_ctr
         out.has_nan = own.has_nan;
         out.skip = own.found_inf;    // GradScaler.step checks its own optimizer's gradients (amp.py:209-217)
         *blocks.block[i] = out;
+        if (blocks.mirror[i] != nullptr) publish(blocks.mirror[i], out);
     }
 }
 
@@ -1090,7 +1103,7 @@ int32_t nt_amp_prepass(nt_plan *plan, float scale, int32_t unscale, const nt_amp
 
 int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *carry, double norm_type,
                         double max_norm, int32_t flags, double growth_factor, double backoff_factor,
-                        int32_t growth_interval, void *stream) {
+                        int32_t growth_interval, nt_amp_mirror *mirror, void *stream) {
     clear_error();
     int32_t rc = check_plan(plan);
     if (rc != NT_OK) return rc;
@@ -1109,14 +1122,14 @@ int32_t nt_amp_finalize(nt_plan *plan, nt_amp_ctrl *ctrl, const nt_amp_ctrl *car
     const int64_t count = plan->nstage2 > 0 ? plan->nstage2 : plan->npartials;
     finalize_kernel<<<dim3(1), dim3(kBlock), 0, (hipStream_t)stream>>>(
         src, count, ctrl, carry, norm_type, max_norm, flags, growth_factor,
-        backoff_factor, growth_interval);
+        backoff_factor, growth_interval, mirror);
     NT_LAUNCH_CHECK("finalize_kernel launch");
     return NT_OK;
 }
 
 int32_t nt_amp_combine(nt_amp_ctrl *const *blocks, int32_t n, const nt_amp_ctrl *carry, double norm_type,
                        double max_norm, int32_t flags, double growth_factor, double backoff_factor,
-                       int32_t growth_interval, void *stream) {
+                       int32_t growth_interval, nt_amp_mirror *const *mirrors, void *stream) {
     clear_error();
     if (blocks == nullptr || n < 1 || n > NT_MAX_COMBINE)
         return fail(NT_ERR_VALUE, "nt_amp_combine: 1 to " + std::to_string(NT_MAX_COMBINE) + " control blocks required");
@@ -1128,6 +1141,7 @@ int32_t nt_amp_combine(nt_amp_ctrl *const *blocks, int32_t n, const nt_amp_ctrl 
         for (int32_t j = 0; j < i; ++j)
             if (blocks[j] == blocks[i]) return fail(NT_ERR_VALUE, "nt_amp_combine: a control block is listed twice");
         list.block[i] = blocks[i];
+        list.mirror[i] = mirrors != nullptr ? mirrors[i] : nullptr;
     }
     if (!(norm_type == 2.0 || (__builtin_isinf(norm_type) && norm_type > 0.0)))
         return fail(NT_ERR_VALUE, "nt_amp_combine: norm_type must be 2 or positive infinity");
@@ -1319,7 +1333,7 @@ int32_t nt_amp_flat_stats_noalloc(int32_t device, const void *grad, int32_t grad
         NT_LAUNCH_CHECK("flat_prepass_kernel launch");
     }
     finalize_kernel<<<dim3(1), dim3(kBlock), 0, s>>>(partials, (int64_t)groups, ctrl, carry, norm_type, max_norm,
-                                                     flags, growth_factor, backoff_factor, growth_interval);
+                                                     flags, growth_factor, backoff_factor, growth_interval, nullptr);
     NT_LAUNCH_CHECK("finalize_kernel launch");
     return NT_OK;
 }

@@ -9,7 +9,9 @@
 // (they are never destroyed, so no HIP call runs during static teardown).
 #include <hip/hip_runtime.h>
 
+#include <cstring>
 #include <mutex>
+#include <thread>
 #include <unordered_set>
 
 #include "nt_internal.hpp"
@@ -220,6 +222,58 @@ int32_t nt_host_alloc(uint64_t bytes, void **out) {
 int32_t nt_host_free(void *ptr) {
     clear_error();
     if (ptr != nullptr) NT_HIP_TRY(hipHostFree(ptr), "hipHostFree");
+    return NT_OK;
+}
+
+int32_t nt_mirror_alloc(int32_t count, nt_amp_mirror **out) {
+    clear_error();
+    if (out == nullptr) return fail(NT_ERR_VALUE, "nt_mirror_alloc: output pointer is NULL");
+    *out = nullptr;
+    if (count < 1 || count > (1 << 20)) return fail(NT_ERR_VALUE, "nt_mirror_alloc: count must be in [1, 2**20]");
+    void *memory = nullptr;
+    const size_t bytes = (size_t)count * sizeof(nt_amp_mirror);
+    NT_HIP_TRY(hipHostMalloc(&memory, bytes, hipHostMallocCoherent), "hipHostMalloc(coherent)");
+    std::memset(memory, 0, bytes);
+    *out = static_cast<nt_amp_mirror *>(memory);
+    return NT_OK;
+}
+
+// Wait until the kernel queued on `stream` to fill `mirror` has set its
+// flag.  The flag is polled; every 64 polls the stream is queried, and once
+// all its work has completed with the flag still clear, no queued kernel was
+// going to write it (an error, not a hang).  Nothing is recorded on the
+// stream, so waiting adds no marker to it.
+int32_t nt_mirror_wait(const nt_amp_mirror *mirror, void *stream) {
+    clear_error();
+    if (mirror == nullptr) return fail(NT_ERR_VALUE, "nt_mirror_wait: mirror is NULL");
+    for (uint32_t poll = 1;; ++poll) {
+        if (__atomic_load_n(&mirror->ready, __ATOMIC_ACQUIRE) != 0) return NT_OK;
+        if (poll % 64u == 0u) {
+            bool idle = stream_destroyed(stream);
+            if (!idle) {
+                const hipError_t status = hipStreamQuery((hipStream_t)stream);
+                if (status == hipSuccess) {
+                    idle = true;
+                } else if (status == hipErrorNotReady) {
+                    (void)hipGetLastError();
+                } else {
+                    return hip_check(status, "hipStreamQuery");
+                }
+            }
+            if (idle) {
+                if (__atomic_load_n(&mirror->ready, __ATOMIC_ACQUIRE) != 0) return NT_OK;
+                return fail(NT_ERR_RUNTIME, "nt_mirror_wait: the stream completed without writing the mirror");
+            }
+            std::this_thread::yield();
+        } else {
+            __builtin_ia32_pause();
+        }
+    }
+}
+
+int32_t nt_mirror_free(nt_amp_mirror *mirrors) {
+    clear_error();
+    if (mirrors != nullptr) NT_HIP_TRY(hipHostFree(mirrors), "hipHostFree");
     return NT_OK;
 }
 

@@ -90,7 +90,7 @@ extern "C" {
 
 const char *nt_last_error(void) { return g_last_error.c_str(); }
 
-int32_t nt_abi_version(void) { return 3; }
+int32_t nt_abi_version(void) { return 4; }
 
 int32_t nt_device_count(int32_t *count) {
     clear_error();

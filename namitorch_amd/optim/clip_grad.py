@@ -36,6 +36,7 @@ from operator import attrgetter, eq, is_
 
 import numpy as np
 
+from .. import runtime
 from ..array import DeviceArray
 from ..backends import ensure_same_device, get_backend
 from ..backends._graph_capture import reject_during_capture
@@ -333,13 +334,14 @@ _VALUE = attrgetter("value")
 _UNSETTLED_LIMIT = 64
 
 
-def _norm_on_device(gradients, order: float, maximum: float):
+def _norm_on_device(gradients, order: float, maximum: float, with_mirror: bool = False):
     """Queue the pre-pass and a finalize over `gradients` and a device copy
     of the norm, with no host wait: (backend, control block, 0-d float64
-    norm array), or None when the host path must answer.  With `maximum`
-    >= 0 the finalize also takes the clip decision by the reference's rule
-    (clip when ``max_norm / (norm + 1e-6) < 1``, also for a non-finite
-    norm).
+    norm array, host mirror of the block or None), or None when the host
+    path must answer.  With `maximum` >= 0 the finalize also takes the clip
+    decision by the reference's rule (clip when ``max_norm / (norm + 1e-6)
+    < 1``, also for a non-finite norm).  With `with_mirror` the finalize
+    also writes the finished block to a ``runtime.take_mirror()``.
 
     Eligible: norm_type 2 or inf; one device and one float16, bfloat16 or
     float32 gradient dtype (float64 may need the prescaled second pass);
@@ -362,8 +364,9 @@ def _norm_on_device(gradients, order: float, maximum: float):
     neutral = backend.neutral_ctrl()
     block = backend.empty_ctrl()                         # written whole by the finalize
     backend.grad_prepass(plan, None, neutral.data_ptr())
-    backend.grad_finalize(plan, block.data_ptr(), order, maximum, 0, carry_ptr=neutral.data_ptr())
-    return backend, block, backend.ctrl_norm(block)
+    mirror = runtime.take_mirror() if with_mirror else None
+    backend.grad_finalize(plan, block.data_ptr(), order, maximum, 0, carry_ptr=neutral.data_ptr(), mirror=mirror)
+    return backend, block, backend.ctrl_norm(block), mirror
 
 
 def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
@@ -381,14 +384,14 @@ def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
     """
     if not all(map(_WRITABLE, gradients)):
         return None
-    launched = _norm_on_device(gradients, order, maximum)
+    launched = _norm_on_device(gradients, order, maximum, with_mirror=True)
     if launched is None:
         return None
-    backend, block, norm = launched
+    backend, block, norm, mirror = launched
     from ..amp import DeviceStep                         # the amp module imports this one
     from ..tensor import _unsettled_steps
     clip_bumps: list = []
-    device_step = DeviceStep(backend, block, unscale=False, honor_skip=False, clip_bumps=clip_bumps)
+    device_step = DeviceStep(backend, block, unscale=False, honor_skip=False, clip_bumps=clip_bumps, mirror=mirror)
     device_step.clip_requested = True
     device_step.capture()
     transform = GradTransform(device=device_step)

@@ -229,6 +229,48 @@ def give_pinned(array: np.ndarray) -> None:
         idle.append(array)
 
 
+# ---- control-block mirrors -------------------------------------------------------------------
+# Fine-grained page-locked host copies of control blocks (``nt_amp_mirror``),
+# written by the finalize kernel itself so that reading an iteration's
+# decisions needs no event on the launch stream.  Slabs are allocated once
+# and kept (releasing page-locked memory waits for the device).  A mirror is
+# reused only after its ``ready`` flag was seen set: no earlier launch still
+# writes it then.
+_MIRROR_SLAB = 256
+_mirror_lock = threading.Lock()
+_mirror_idle: list = []            # addresses free for reuse
+_mirror_waiting: list = []         # given back before their writer was seen to finish
+_mirror_slabs: list = []
+
+
+def take_mirror():
+    """A cleared ``_native.AmpMirror`` (``ready`` == 0) for the next finalize."""
+    with _mirror_lock:
+        if not _mirror_idle and _mirror_waiting:
+            still = []
+            for address in _mirror_waiting:
+                (_mirror_idle if _native.AmpMirror.from_address(address).ready else still).append(address)
+            _mirror_waiting[:] = still
+        if not _mirror_idle:
+            slab = ctypes.c_void_p()
+            _native.call("nt_mirror_alloc", _MIRROR_SLAB, ctypes.byref(slab))
+            _mirror_slabs.append(slab.value)
+            size = ctypes.sizeof(_native.AmpMirror)
+            _mirror_idle.extend(slab.value + k * size for k in reversed(range(_MIRROR_SLAB)))
+        address = _mirror_idle.pop()
+    mirror = _native.AmpMirror.from_address(address)
+    mirror.ready = 0
+    return mirror
+
+
+def give_mirror(mirror, launched: bool = True) -> None:
+    """Return a mirror of :func:`take_mirror`.  `launched`: a kernel was
+    queued to write it (it is reused once its flag shows that write done)."""
+    address = ctypes.addressof(mirror)
+    with _mirror_lock:
+        (_mirror_idle if mirror.ready or not launched else _mirror_waiting).append(address)
+
+
 def memory_stats(device: int = 0) -> dict:
     """Bytes of device memory handed out and held by the library's pool."""
     in_use = ctypes.c_uint64()
@@ -243,4 +285,4 @@ def empty_cache(device: int = 0) -> None:
 
 
 __all__ = ["Stream", "Event", "stream", "current_stream", "current_stream_owner", "set_stream_provider", "pinned",
-           "take_pinned", "give_pinned", "memory_stats", "empty_cache", "device_scope"]
+           "take_pinned", "give_pinned", "take_mirror", "give_mirror", "memory_stats", "empty_cache", "device_scope"]

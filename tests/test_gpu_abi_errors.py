@@ -198,18 +198,18 @@ def test_prepass_finalize_norm_and_apply(plans):
     with pytest.raises(ValueError, match="plan is NULL"):
         _call("nt_amp_prepass", None, 1.0, 0, None, _stream())
     with pytest.raises(ValueError, match="control block is NULL"):
-        _call("nt_amp_finalize", plan, None, None, 2.0, -1.0, 0, 2.0, 0.5, 2000, _stream())
+        _call("nt_amp_finalize", plan, None, None, 2.0, -1.0, 0, 2.0, 0.5, 2000, None, _stream())
     with pytest.raises(ValueError, match="carry and ctrl must be different"):
-        _call("nt_amp_finalize", plan, c, c, 2.0, -1.0, 0, 2.0, 0.5, 2000, _stream())
+        _call("nt_amp_finalize", plan, c, c, 2.0, -1.0, 0, 2.0, 0.5, 2000, None, _stream())
     for norm_type in (0.0, -2.0, float("nan")):
         with pytest.raises(ValueError, match="norm_type must be positive"):
-            _call("nt_amp_finalize", plan, c, None, norm_type, -1.0, 0, 2.0, 0.5, 2000, _stream())
+            _call("nt_amp_finalize", plan, c, None, norm_type, -1.0, 0, 2.0, 0.5, 2000, None, _stream())
     with pytest.raises(ValueError, match="unknown flags"):
-        _call("nt_amp_finalize", plan, c, None, 2.0, -1.0, 8, 2.0, 0.5, 2000, _stream())
+        _call("nt_amp_finalize", plan, c, None, 2.0, -1.0, 8, 2.0, 0.5, 2000, None, _stream())
     update = _native.NT_FINALIZE_SCALER_UPDATE
     for growth, backoff, interval in ((2.0, 0.5, 0), (1.0, 0.5, 10), (2.0, 1.0, 10), (2.0, 0.0, 10)):
         with pytest.raises(ValueError, match="growth/backoff"):
-            _call("nt_amp_finalize", plan, c, None, 2.0, -1.0, update, growth, backoff, interval, _stream())
+            _call("nt_amp_finalize", plan, c, None, 2.0, -1.0, update, growth, backoff, interval, None, _stream())
     with pytest.raises(ValueError, match="control block is NULL"):
         _call("nt_grad_norm_pow", plan, None, 3.0, -1.0, 1.0, 0, 0, 0, _stream())
     for norm_type in (float("inf"), 0.0):
@@ -265,7 +265,7 @@ def test_combine_arguments():
                                                           for t in tensors])
 
     def combine(pointers, n, carry_ptr=carry, norm_type=2.0, flags=0, growth=2.0, backoff=0.5, interval=2000):
-        _call("nt_amp_combine", pointers, n, carry_ptr, norm_type, 1.0, flags, growth, backoff, interval, _stream())
+        _call("nt_amp_combine", pointers, n, carry_ptr, norm_type, 1.0, flags, growth, backoff, interval, None, _stream())
 
     two = table(blocks[0], blocks[1])
     for n in (0, -1, _native.NT_MAX_COMBINE + 1):

@@ -12,7 +12,7 @@ import ctypes
 import pytest
 import torch
 
-from namitorch_amd import _native
+from namitorch_amd import _native, runtime
 
 pytestmark = pytest.mark.gpu
 
@@ -55,13 +55,19 @@ def test_finalize_with_carry_equals_carry_then_finalize(dtype, poison, flags, ma
         args = (2.0, max_norm, flags, 2.0, 0.5, 5)
         _native.call("nt_ctrl_carry", carried.data_ptr(), previous.data_ptr(), _stream())
         _native.call("nt_amp_prepass", plan, 1.0, 1, carried.data_ptr(), _stream())
-        _native.call("nt_amp_finalize", plan, carried.data_ptr(), None, *args, _stream())
+        _native.call("nt_amp_finalize", plan, carried.data_ptr(), None, *args, None, _stream())
         _native.call("nt_amp_prepass", plan, 1.0, 1, previous.data_ptr(), _stream())
-        _native.call("nt_amp_finalize", plan, direct.data_ptr(), previous.data_ptr(), *args, _stream())
+        mirror = runtime.take_mirror()
+        _native.call("nt_amp_finalize", plan, direct.data_ptr(), previous.data_ptr(), *args, ctypes.addressof(mirror),
+                     _stream())
         torch.cuda.synchronize()
     finally:
         _native.call("nt_plan_destroy", plan)
     assert torch.equal(carried.cpu(), direct.cpu())
+    # the finalize's host mirror holds the finished block, flagged ready
+    assert mirror.ready == 1
+    assert bytes(mirror.ctrl) == bytes(direct.cpu().numpy())
+    runtime.give_mirror(mirror)
     ctrl = _native.AmpCtrl.from_buffer_copy(bytes(direct.cpu().numpy()))
     assert ctrl.found_inf == int(poison) and ctrl.iterations == 8 and ctrl.skipped == 2 + int(poison)
     if flags & _native.NT_FINALIZE_SCALER_UPDATE:

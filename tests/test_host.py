@@ -304,9 +304,9 @@ def test_settled_device_step_never_stalls_the_unsettled_list():
     (done by every version read) always ends."""
     from namitorch_amd.amp import DeviceStep
     from namitorch_amd.tensor import _settle_device_steps, _unsettled_steps
-    step = DeviceStep.__new__(DeviceStep)           # host state only: no control block, no snapshot
+    step = DeviceStep.__new__(DeviceStep)           # host state only: no control block, no mirror
     step._reconciled = True
-    step.snapshot = None
+    step.mirror = None
     before = list(_unsettled_steps)
     _unsettled_steps.extend([step, step])
     try:

@@ -57,7 +57,7 @@ def _with_plan(grad, code, scale, unscale, carry, norm_type, max_norm, flags):
         carry_ptr = None if carry is None else carry.data_ptr()
         _native.call("nt_amp_prepass", handle, scale, unscale, carry_ptr, _stream())
         _native.call("nt_amp_finalize", handle, block.data_ptr(), carry_ptr, norm_type, max_norm, flags, 2.0, 0.5, 3,
-                     _stream())
+                     None, _stream())
         return _read(block)
     finally:
         torch.cuda.synchronize()
