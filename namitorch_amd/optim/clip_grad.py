@@ -29,6 +29,7 @@ gradients; ``.item()`` on either result waits for it.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from numbers import Real
 from itertools import repeat
@@ -36,7 +37,7 @@ from operator import attrgetter, eq, is_
 
 import numpy as np
 
-from .. import runtime
+from .. import _native, runtime
 from ..array import DeviceArray
 from ..backends import ensure_same_device, get_backend
 from ..backends._graph_capture import reject_during_capture
@@ -247,12 +248,24 @@ def grad_stats(gradients, norm_type: float = 2.0, remember: bool = True) -> tupl
         plan = backend.grad_plan(members, dtype, incoming=True)
         block = backend.empty_ctrl()                     # written whole by the finalize
         backend.grad_prepass(plan, scale)
-        backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0, carry_ptr=backend.neutral_ctrl().data_ptr())
-        launched.append((backend, dtype, members, block, scale))
+        # The finalize also writes the block to a host mirror, which the host
+        # waits for below (no copy back, nothing recorded on the stream).
+        mirror = runtime.take_mirror()
+        try:
+            backend.grad_finalize(plan, block.data_ptr(), norm_type=2.0, carry_ptr=backend.neutral_ctrl().data_ptr(),
+                                  mirror=mirror)
+        except BaseException:
+            runtime.give_mirror(mirror, launched=False)
+            raise
+        launched.append((backend, dtype, members, block, scale, mirror, backend.stream()))
     # Host work that does not need the results runs while the device works.
     snapshot = _stats_snapshot(gradients) if remember else None
-    for backend, dtype, members, block, scale in launched:
-        ctrl = backend.read_ctrl(block)
+    for backend, dtype, members, block, scale, mirror, stream in launched:
+        if not mirror.ready:
+            with backend.context():
+                _native.call("nt_mirror_wait", ctypes.addressof(mirror), stream)
+        ctrl = _native.AmpCtrl.from_buffer_copy(mirror)
+        runtime.give_mirror(mirror)
         stats.merge(GradStats(ctrl.sumsq, ctrl.amax, bool(ctrl.has_nan), bool(ctrl.found_inf and not ctrl.has_nan)))
         blocks[(backend, dtype)] = (members, block, scale)
     if remember:
@@ -267,8 +280,6 @@ def _pow_total(blocks, amax: float, order: float) -> float:
         plan = backend.grad_plan(members, dtype)         # deferred accumulations written back first
         ctrl = backend.read_ctrl(block)
         ctrl.amax = amax
-        import ctypes
-        from .. import _native
         with backend.context():
             _native.call("nt_memcpy_h2d", block.data_ptr(), ctypes.addressof(ctrl), ctypes.sizeof(ctrl), backend.stream())
         backend.grad_norm_pow(plan, block.data_ptr(), order, -1.0, scale)

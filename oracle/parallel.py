@@ -9,8 +9,17 @@ the GIL inside its ufuncs.  Reductions keep the oracle's own order:
 ``total_norm`` evaluates each gradient's sum whole (one tensor per task) and
 combines the sums in list order, exactly as ``clip.total_norm`` does.
 
+``total_norm_streamed`` takes gradients one at a time from a callback and
+splits each one's sum over the pool too: ``np.sum`` of a contiguous float64
+vector adds, in order, the pairwise sums of its consecutive blocks of
+``SUM_BLOCK`` (8192) elements (NumPy's reduction buffer), so ``exact_sum``
+sums those blocks on the pool and adds the block sums in order, which gives
+``np.sum``'s bits.
+
 Pinned by tests/test_oracle.py: every function here equals the plain oracle
-call bit for bit on random inputs whose sizes straddle the slice boundaries.
+call bit for bit on random inputs whose sizes straddle the slice boundaries;
+``exact_sum`` equals ``np.sum`` and ``total_norm_streamed`` equals
+``clip.total_norm`` on sizes around the block and slice boundaries.
 """
 
 from __future__ import annotations
@@ -116,6 +125,59 @@ def total_norm(pool: Pool, gradients, norm_type: float = 2.0) -> float:
     with np.errstate(over="ignore", divide="ignore", invalid="ignore", under="ignore"):
         for value in sums:
             total = total + value
+        result = scale * np.power(total, 1 / norm_type)
+        if not bool(np.isfinite(result)):
+            result = np.exp(np.log(scale) + np.log(total) / norm_type)
+    return float(result)
+
+
+SUM_BLOCK = 8192
+_SUM_SLICE = SUM_BLOCK * 128          # elements per pool task of exact_sum (a whole number of blocks)
+
+
+def exact_sum(pool: Pool, values: np.ndarray) -> np.float64:
+    """``np.sum(values, dtype=np.float64)`` of a contiguous float64 vector,
+    with its blocks summed on the pool."""
+    flat = np.ascontiguousarray(values, dtype=np.float64).reshape(-1)
+    size = flat.size
+    whole = size // SUM_BLOCK * SUM_BLOCK
+
+    def blocks(start: int, stop: int) -> np.ndarray:
+        return flat[start:stop].reshape(-1, SUM_BLOCK).sum(axis=1, dtype=np.float64)
+
+    parts = pool.run([lambda a=a: blocks(a, min(a + _SUM_SLICE, whole)) for a in range(0, whole, _SUM_SLICE)])
+    if whole < size:
+        parts.append(np.asarray([np.sum(flat[whole:], dtype=np.float64)]))
+    total = np.float64(0.0)
+    for part in parts:
+        for value in part:
+            total = total + value
+    return total
+
+
+def total_norm_streamed(pool: Pool, count: int, fetch, norm_type: float = 2.0) -> float:
+    """``clip.total_norm`` over `count` gradients that ``fetch(i)`` returns
+    one at a time (called twice per gradient: once for the maxima, once for
+    the sums), so the whole set is never held.  Each gradient's maximum and
+    sum run on the pool; the combination is ``total_norm``'s."""
+    scale = np.asarray(0.0, dtype=np.float64)
+    for index in range(count):
+        gradient = np.ascontiguousarray(fetch(index)).reshape(-1)
+        parts = pool.run([lambda part=part: np.max(np.abs(gradient[part]), initial=0)
+                          for part in pool._slices(gradient.size)])
+        value = np.max(np.abs(gradient[:0]), initial=0)
+        for part_max in parts:
+            value = np.maximum(value, part_max)
+        scale = np.maximum(scale, value)
+    if not bool(np.isfinite(scale)) or bool(scale == 0) or np.isinf(norm_type):
+        return float(scale)
+    total = np.asarray(0.0, dtype=np.float64)
+    with np.errstate(over="ignore", divide="ignore", invalid="ignore", under="ignore"):
+        for index in range(count):
+            gradient = fetch(index)
+            terms = pool.mapped(lambda g: np.power(np.abs(np.asarray(g, dtype=np.float64)) / scale, norm_type),
+                                np.ascontiguousarray(gradient).reshape(-1), np.float64)
+            total = total + exact_sum(pool, terms)
         result = scale * np.power(total, 1 / norm_type)
         if not bool(np.isfinite(result)):
             result = np.exp(np.log(scale) + np.log(total) / norm_type)

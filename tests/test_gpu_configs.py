@@ -10,12 +10,22 @@ pool by ``oracle.parallel``, which gives the oracle's bits):
 * C2: the full GPT-2-124M list (148 tensors, 124,439,808 parameters), float32
   AdamW in the two ``decay_parameter_groups`` groups (runner.py:83-90);
 * C3: the full GPT-2-124M list with AMP: bfloat16 model + float32 master,
-  float16 gradients f16(N(0, 1e-3) * 65536), one +inf (or NaN) at a seeded
-  (step, tensor, element), GradScaler(65536, x2, x0.5, 2000) and a
-  growth_interval 3 variant that grows within the run;
-* C4: the GPT-1.3B layout at its real width (d 2048, vocab 50304, ctx 2048)
-  with 2 layers (207.9 M parameters): float32 master, bfloat16
-  parameters/moments/gradients, clip_grad_norm_ at 1.0 (active every step).
+  float16 gradients f16(N(0, 1e-3) * 65536), one +inf in a matrix at step 3
+  (GradScaler(65536, x2, x0.5, 2000)) or one NaN in a vector at step 6 (a
+  growth_interval 3 variant that grows, backs off and grows again), at a
+  seeded element; the whole state is compared after the step that follows
+  the skipped one and after the last step;
+* C4: the full GPT-1.3B list (292 tensors, 1,315,819,520 parameters):
+  float32 master, bfloat16 parameters/moments/gradients, clip_grad_norm_ at
+  1.0 (active every step); both paths step in lockstep on the same
+  gradients, which come from the device's generator and are copied back for
+  the oracle;
+* C5: the full Llama-7B list (291 tensors, 6,738,415,616 parameters) through
+  ``fused_step`` for two steps: bfloat16 model + float32 master and moments,
+  bfloat16 gradients scaled by 65536, clip at 1.0.  The norm's oracle streams
+  the gradients back one tensor at a time (``parallel.total_norm_streamed``);
+  a seeded sample of whole tensors (the embedding, the head, the final norm
+  and five others) is stepped by the oracle and compared.
 
 Bars (the path's target tolerances): found_inf flags, skip decisions and the
 loss-scale sequence bit-exact; norms within 1e-12 relative; float32 master,
@@ -29,6 +39,7 @@ a rate below 1e-6.
 
 from __future__ import annotations
 
+import gc
 import math
 
 import numpy as np
@@ -36,9 +47,9 @@ import pytest
 import torch
 
 import namitorch_amd as nt
-from namitorch_amd.param_lists import decay_mask, gpt2_shapes, total_params
+from namitorch_amd.param_lists import decay_mask, gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes, total_params
 from oracle import clip as oclip
-from oracle import parallel
+from oracle import lowp, parallel
 from oracle import scaler as oscaler
 
 pytestmark = pytest.mark.gpu
@@ -89,6 +100,27 @@ def _compare(label, got, want, unit_bits=None, allow_rate=0.0):
     return int(bad.size)
 
 
+def _release():
+    """Return the device memory of finished runs (both allocators)."""
+    gc.collect()
+    torch.cuda.synchronize()
+    nt.runtime.empty_cache(0)
+    torch.cuda.empty_cache()
+
+
+def _device_normals(shapes, seed, sigma, dtype):
+    """dtype(N(0, sigma)) per tensor from the device's generator."""
+    generator = torch.Generator(device=DEV).manual_seed(seed)
+    return [torch.randn(shape, generator=generator, device=DEV, dtype=torch.float32).mul_(sigma).to(dtype)
+            for shape in shapes]
+
+
+def _host_bf16(pool, tensor):
+    """A bfloat16 device tensor as bfloat16-valued float32 on the host."""
+    bits = tensor.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    return pool.mapped(lowp.bf16_to_f32, bits, np.float32)
+
+
 def _groups(params, shapes, weight_decay=0.1):
     mask = decay_mask(shapes)
     return [{"params": [p for p, m in zip(params, mask) if m], "weight_decay": weight_decay},
@@ -123,15 +155,17 @@ def test_c2_full_gpt2_fp32_ten_steps(pool):
 
 
 # ---- C3 --------------------------------------------------------------------------------------------
-def _c3_oracle(pool, shapes, host, grads16, growth_interval):
-    """Oracle trajectory of the C3 recipe: flags, scales and final state."""
+def _c3_oracle(pool, shapes, host, grads16, growth_interval, snapshot_step):
+    """Oracle trajectory of the C3 recipe: flags, scales, the state after
+    step index `snapshot_step` (master, m, v, copies) and the final state."""
     master = [h.copy() for h in host]
     m = [np.zeros_like(h) for h in host]
     v = [np.zeros_like(h) for h in host]
     decays = [0.1 if k else 0.0 for k in decay_mask(shapes)]
     scaler = oscaler.Scaler(65536.0, 2.0, 0.5, growth_interval)
     finite_flags, scales, count = [], [], 0
-    for grads in grads16:
+    snapshot = None
+    for index, grads in enumerate(grads16):
         unscaled = [parallel.unscale(pool, g, scaler.scale, "float16") for g in grads]
         finite = parallel.finite(pool, unscaled)
         if finite:
@@ -141,16 +175,30 @@ def _c3_oracle(pool, shapes, host, grads16, growth_interval):
         scaler.update(not finite)
         finite_flags.append(finite)
         scales.append(scaler.scale)
+        if index == snapshot_step:
+            snapshot = ([x.copy() for x in master], [x.copy() for x in m], [x.copy() for x in v],
+                        [parallel.round_bf16(pool, x) for x in master], count)
     copies = [parallel.round_bf16(pool, x) for x in master]
-    return finite_flags, scales, master, m, v, copies, count
+    return finite_flags, scales, master, m, v, copies, count, snapshot
 
 
-@pytest.mark.parametrize("poison,growth_interval", [(np.inf, 2000), (np.nan, 3)])
-def test_c3_gpt2_amp_ten_steps(pool, poison, growth_interval):
+def _compare_c3_state(mode, params, optimizer, master, m, v, copies, count):
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        assert state["step"] == count
+        _compare(f"{mode} master[{i}]", state["master"].numpy(), master[i])
+        _compare(f"{mode} m[{i}]", state["exp_avg"].numpy(), m[i])
+        _compare(f"{mode} v[{i}]", state["exp_avg_sq"].numpy(), v[i])
+        _compare(f"{mode} copy[{i}]", p.numpy(), copies[i])
+
+
+@pytest.mark.parametrize("poison,growth_interval,bad_step,kind", [(np.inf, 2000, 3, "matrix"), (np.nan, 3, 6, "vector")])
+def test_c3_gpt2_amp_ten_steps(pool, poison, growth_interval, bad_step, kind):
     shapes = gpt2_shapes()
     host = [parallel.round_bf16(pool, h) for h in _normals(pool, shapes, 1337, 0.02)]
     pick = np.random.Generator(np.random.PCG64(7))
-    bad_step, bad_tensor = int(pick.integers(1, STEPS)), int(pick.integers(0, len(shapes)))
+    candidates = [i for i, shape in enumerate(shapes) if (len(shape) >= 2) == (kind == "matrix")]
+    bad_tensor = candidates[int(pick.integers(0, len(candidates)))]
     bad_element = int(pick.integers(0, int(np.prod(shapes[bad_tensor]))))
     grads16 = []
     for step in range(STEPS):
@@ -159,11 +207,14 @@ def test_c3_gpt2_amp_ten_steps(pool, poison, growth_interval):
         if step == bad_step:
             step_grads[bad_tensor].reshape(-1)[bad_element] = poison
         grads16.append(step_grads)
-    finite_flags, scales, master, m, v, copies, count = _c3_oracle(pool, shapes, host, grads16, growth_interval)
+    after = bad_step + 1                          # the step after the skipped one
+    finite_flags, scales, master, m, v, copies, count, snapshot = _c3_oracle(pool, shapes, host, grads16,
+                                                                             growth_interval, after)
     assert finite_flags.count(False) == 1 and not finite_flags[bad_step]
     if growth_interval == 3:
         assert max(scales) > 65536.0              # the run grows the scale
-    _say(f"C3 oracle done: skip at step {bad_step}, scales {scales}")
+        assert scales[bad_step] < scales[bad_step - 1]   # and backs off at the skip
+    _say(f"C3 oracle done: skip at step {bad_step} (tensor {bad_tensor}, {kind}), scales {scales}")
     for mode in ("api", "fused"):
         params = [nt.Parameter(h, dtype="bfloat16", device=DEV) for h in host]
         optimizer = nt.optim.AdamW(_groups(params, shapes), master_weights=True, **OPTIONS)
@@ -182,62 +233,119 @@ def test_c3_gpt2_amp_ten_steps(pool, poison, growth_interval):
                 finite, updated = result.finite, result.updated
             assert finite == finite_flags[step] and updated == finite_flags[step], (mode, step)
             assert scaler.get_scale() == scales[step], (mode, step)
-        for i, p in enumerate(params):
-            state = optimizer.state[id(p)]
-            assert state["step"] == count
-            _compare(f"{mode} master[{i}]", state["master"].numpy(), master[i])
-            _compare(f"{mode} m[{i}]", state["exp_avg"].numpy(), m[i])
-            _compare(f"{mode} v[{i}]", state["exp_avg_sq"].numpy(), v[i])
-            _compare(f"{mode} copy[{i}]", p.numpy(), copies[i])
-        _say(f"C3 {mode} matches the oracle")
+            if step == after:
+                _compare_c3_state(f"{mode} step {step}", params, optimizer, *snapshot)
+        _compare_c3_state(mode, params, optimizer, master, m, v, copies, count)
+        _say(f"C3 {mode} matches the oracle after step {after} and at the end")
         del params, optimizer
 
 
 # ---- C4 --------------------------------------------------------------------------------------------
-def test_c4_gpt1p3b_width_bf16_clip_ten_steps(pool):
-    shapes = gpt2_shapes(vocab=50304, ctx=2048, d=2048, layers=2, ffn=8192)
-    assert total_params(shapes) == 207_937_536
+def test_c4_full_gpt1p3b_bf16_clip_ten_steps(pool):
+    shapes = gpt_1p3b_shapes()
+    assert len(shapes) == 292 and total_params(shapes) == 1_315_819_520
     host = [parallel.round_bf16(pool, h) for h in _normals(pool, shapes, 1337, 0.02)]
-    grads = []
-    for step in range(STEPS):
-        grads.append([parallel.round_bf16(pool, g) for g in _normals(pool, shapes, 1337 + 1000 + step, 1e-3)])
-    # Oracle: clip at 1.0 (always active here), then the master step with bfloat16 moments.
     master = [h.copy() for h in host]
     m = [np.zeros_like(h) for h in host]
     v = [np.zeros_like(h) for h in host]
     decays = [0.1 if k else 0.0 for k in decay_mask(shapes)]
-    norms = []
-    for step, step_grads in enumerate(grads, start=1):
-        norm = parallel.total_norm(pool, step_grads)
+    modes = ("api", "fused")
+    params = {mode: [nt.Parameter(h, dtype="bfloat16", device=DEV) for h in host] for mode in modes}
+    del host
+    optimizers = {mode: nt.optim.AdamW(_groups(params[mode], shapes), master_weights=True, state_dtype="bfloat16",
+                                       **OPTIONS) for mode in modes}
+    for step in range(1, STEPS + 1):
+        grads = _device_normals(shapes, 1337 + 1000 + step, 1e-3, torch.bfloat16)
+        for mode in modes:
+            for p, g in zip(params[mode], grads):
+                p.grad = nt.Tensor(g)                 # a copy in the library's memory
+        got = {"api": nt.optim.clip_grad_norm_(params["api"], 1.0)}
+        optimizers["api"].step()
+        got["fused"] = nt.amp.fused_step(optimizers["fused"], None, max_norm=1.0).norm
+        # Oracle: clip at 1.0 (always active here), then the master step with bfloat16 moments.
+        host_grads = [_host_bf16(pool, g) for g in grads]
+        del grads
+        norm = parallel.total_norm_streamed(pool, len(host_grads), lambda i: host_grads[i])
         coefficient = oclip.clip_coefficient(1.0, norm)
         assert coefficient < 1
-        clipped = [parallel.clip_apply(pool, g, coefficient, "bfloat16") for g in step_grads]
-        for i, g in enumerate(clipped):
-            parallel.master_step(pool, master[i], g, m[i], v[i], step, weight_decay=decays[i], state_bf16=True,
+        for i, g in enumerate(host_grads):
+            clipped = parallel.clip_apply(pool, g, coefficient, "bfloat16")
+            parallel.master_step(pool, master[i], clipped, m[i], v[i], step, weight_decay=decays[i], state_bf16=True,
                                  **OPTIONS)
-        norms.append(norm)
-    copies = [parallel.round_bf16(pool, x) for x in master]
-    _say(f"C4 oracle done: norms {norms[0]:.6g} .. {norms[-1]:.6g}")
-    for mode in ("api", "fused"):
-        params = [nt.Parameter(h, dtype="bfloat16", device=DEV) for h in host]
-        optimizer = nt.optim.AdamW(_groups(params, shapes), master_weights=True, state_dtype="bfloat16", **OPTIONS)
-        for step, step_grads in enumerate(grads):
-            for p, g in zip(params, step_grads):
-                # bfloat16-valued float32 -> bfloat16 is exact; converted on the device.
-                p.grad = nt.Tensor(torch.from_numpy(g).to(DEV).to(torch.bfloat16))
-            if mode == "api":
-                norm = nt.optim.clip_grad_norm_(params, 1.0).item()
-                optimizer.step()
-            else:
-                norm = nt.amp.fused_step(optimizer, None, max_norm=1.0).norm
-            assert abs(norm - norms[step]) <= NORM_RTOL * norms[step], (mode, step, norm, norms[step])
+        del host_grads
+        for mode in modes:
+            value = got[mode].item() if mode == "api" else got[mode]
+            assert abs(value - norm) <= NORM_RTOL * norm, (mode, step, value, norm)
+        _say(f"C4 step {step}: norm {norm:.9g}")
+    for mode in modes:
         flips = 0
-        for i, p in enumerate(params):
-            state = optimizer.state[id(p)]
+        for i, p in enumerate(params[mode]):
+            state = optimizers[mode].state[id(p)]
             assert state["step"] == STEPS
             flips += _compare(f"{mode} master[{i}]", state["master"].numpy(), master[i], unit_bits=32, allow_rate=1e-6)
             flips += _compare(f"{mode} m[{i}]", state["exp_avg"].numpy(), m[i], unit_bits=16, allow_rate=1e-6)
             flips += _compare(f"{mode} v[{i}]", state["exp_avg_sq"].numpy(), v[i], unit_bits=16, allow_rate=1e-6)
-            flips += _compare(f"{mode} copy[{i}]", p.numpy(), copies[i], unit_bits=16, allow_rate=1e-6)
-        _say(f"C4 {mode} matches the oracle ({flips} elements one unit away)")
-        del params, optimizer
+            flips += _compare(f"{mode} copy[{i}]", p.numpy(), lowp.round_bf16(master[i]), unit_bits=16,
+                              allow_rate=1e-6)
+        _say(f"C4 {mode} matches the oracle over the full list ({flips} elements one unit away)")
+    del params, optimizers
+    _release()
+
+
+# ---- C5 --------------------------------------------------------------------------------------------
+def test_c5_full_llama7b_amp_clip_two_steps(pool):
+    """Two fused steps over the whole Llama-7B list; the norm, flags and scale
+    against the oracle over every gradient, the state of a seeded sample of
+    whole tensors against the oracle's steps of those tensors."""
+    shapes = llama7b_shapes()
+    assert len(shapes) == 291 and total_params(shapes) == 6_738_415_616
+    pick = np.random.Generator(np.random.PCG64(11))
+    sample = sorted({0, len(shapes) - 1, len(shapes) - 2}
+                    | {int(i) for i in pick.choice(np.arange(1, len(shapes) - 2), 5, replace=False)})
+    decays = [0.1 if k else 0.0 for k in decay_mask(shapes)]
+    scale = 65536.0
+    weights = _device_normals(shapes, 1337, 0.02, torch.bfloat16)
+    params = [nt.Parameter(w) for w in weights]
+    master = {i: _host_bf16(pool, weights[i]) for i in sample}
+    del weights
+    m = {i: np.zeros_like(master[i]) for i in sample}
+    v = {i: np.zeros_like(master[i]) for i in sample}
+    optimizer = nt.optim.AdamW(_groups(params, shapes), master_weights=True, **OPTIONS)
+    scaler = nt.GradScaler(init_scale=scale)
+    loss = nt.Tensor(np.float32(1.0), device=DEV)
+    for step in range(1, 3):
+        grads = _device_normals(shapes, 2337 + step, 1e-3 * scale, torch.bfloat16)
+        for p, g in zip(params, grads):
+            p.grad = nt.Tensor(g)
+        scaler.scale(loss)
+        result = nt.amp.fused_step(optimizer, scaler, max_norm=1.0)
+        kept = {}
+
+        def fetch(index):
+            unscaled = parallel.unscale(pool, _host_bf16(pool, grads[index]), scale, "bfloat16")
+            if index in sample:
+                kept[index] = unscaled
+            return unscaled
+
+        norm = parallel.total_norm_streamed(pool, len(shapes), fetch)
+        assert math.isfinite(norm)
+        coefficient = oclip.clip_coefficient(1.0, norm)
+        assert coefficient < 1
+        assert result.finite and result.updated and result.scale == scale
+        assert abs(result.norm - norm) <= NORM_RTOL * norm, (step, result.norm, norm)
+        for i in sample:
+            clipped = parallel.clip_apply(pool, kept[i], coefficient, "bfloat16")
+            parallel.master_step(pool, master[i], clipped, m[i], v[i], step, weight_decay=decays[i], **OPTIONS)
+        del grads, kept
+        _say(f"C5 step {step}: norm {norm:.9g}")
+    flips = 0
+    for i in sample:
+        state = optimizer.state[id(params[i])]
+        assert state["step"] == 2
+        flips += _compare(f"master[{i}]", state["master"].numpy(), master[i], unit_bits=32, allow_rate=1e-6)
+        flips += _compare(f"m[{i}]", state["exp_avg"].numpy(), m[i], unit_bits=32, allow_rate=1e-6)
+        flips += _compare(f"v[{i}]", state["exp_avg_sq"].numpy(), v[i], unit_bits=32, allow_rate=1e-6)
+        flips += _compare(f"copy[{i}]", params[i].numpy(), lowp.round_bf16(master[i]), unit_bits=16, allow_rate=1e-6)
+    _say(f"C5 sample {sample} matches the oracle ({flips} elements one unit away)")
+    del params, optimizer, scaler
+    _release()

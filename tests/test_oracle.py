@@ -415,3 +415,38 @@ def test_parallel_oracle_equals_plain_oracle():
             assert parallel.total_norm(pool, grads, order) == clip.total_norm(grads, order)
         grads[1][1] = np.nan
         assert math.isnan(parallel.total_norm(pool, grads)) and not parallel.finite(pool, grads)
+
+
+def test_parallel_exact_sum_and_streamed_norm():
+    """exact_sum equals np.sum of a float64 vector bit for bit (sizes around
+    NumPy's 8192-element reduction blocks and the pool's slices, values over
+    many magnitudes, so a different summation order shows), and
+    total_norm_streamed equals clip.total_norm for p = 2, 3 and inf, with
+    non-finite gradients, zeros and empty tensors.  A sum in another order
+    (plain pairwise over the whole vector) differs on the same inputs."""
+    from oracle import parallel
+    rng = np.random.default_rng(2024)
+    block = parallel.SUM_BLOCK
+    sizes = [0, 1, 7, block - 1, block, block + 1, 3 * block + 5, parallel._SUM_SLICE + 17, 2 * parallel._SUM_SLICE]
+    differs = 0
+    with parallel.Pool(4) as pool:
+        for n in sizes:
+            values = rng.standard_normal(n) * np.exp2(rng.integers(-40, 40, n))
+            assert parallel.exact_sum(pool, values) == np.sum(values, dtype=np.float64), n
+            if n > block:
+                halves = np.sum(values[: n // 2], dtype=np.float64) + np.sum(values[n // 2:], dtype=np.float64)
+                differs += halves != np.sum(values, dtype=np.float64)
+        assert differs > 0                                    # the check can tell orders apart
+        grads = [(rng.standard_normal(n) * 1e-3 * np.exp2(rng.integers(-8, 8))).astype(np.float32)
+                 for n in (block * 3 + 1, 5, 0, parallel.SLICE + 3, 70001)]
+        for order in (2.0, 3.0, np.inf):
+            got = parallel.total_norm_streamed(pool, len(grads), lambda i: grads[i], order)
+            assert got == clip.total_norm(grads, order), order
+        zeros = [np.zeros(10, np.float32), np.zeros(0, np.float32)]
+        assert parallel.total_norm_streamed(pool, 2, lambda i: zeros[i]) == clip.total_norm(zeros) == 0.0
+        for poison in (np.inf, np.nan):
+            bad = [g.copy() for g in grads]
+            bad[3][7] = poison
+            got = parallel.total_norm_streamed(pool, len(bad), lambda i: bad[i])
+            want = clip.total_norm(bad)
+            assert (math.isnan(got) and math.isnan(want)) or got == want
