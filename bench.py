@@ -633,8 +633,9 @@ def _baseline_record(total, steps, elapsed, bytes_per_param, sample, *, extrapol
 
 def cpu_baseline(min_seconds=10.0, max_steps=40):
     """C2 (the headline): NumPy oracle AdamW — the reference's NumPy path
-    (optim/adam.py:27-42) restated op for op — over the whole GPT-2-124M
-    list."""
+    (optim/adam.py:27-42) restated op for op, with its per-step
+    ``exp_avg_sq`` check and ``Tensor.copy_`` staging
+    (``oracle.adam.reference_step``) — over the whole GPT-2-124M list."""
     import numpy as np
     from namitorch_amd.param_lists import gpt2_shapes
     from oracle import adam as oadam
@@ -648,11 +649,13 @@ def cpu_baseline(min_seconds=10.0, max_steps=40):
 
     def step(k):
         for p, g, m, v, wd in zip(params, grads, ms, vs, wds):
-            oadam.adam_step(p, g, m, v, k, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+            oadam.reference_step(p, g, m, v, k, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
 
     steps, elapsed = _timed_steps(step, min_seconds, max_steps)
     return _baseline_record(total, steps, elapsed, 28,
-                            f"NumPy oracle AdamW over the full GPT-2-124M list ({len(shapes)} tensors, {total} params)")
+                            f"NumPy oracle AdamW over the full GPT-2-124M list ({len(shapes)} tensors, {total} params), "
+                            f"with the reference's per-step exp_avg_sq check and Tensor.copy_ staging of every write "
+                            f"(oracle.adam.reference_step)")
 
 
 def cpu_baselines_other(min_seconds=3.0):
@@ -675,8 +678,10 @@ def cpu_baselines_other(min_seconds=3.0):
     p, = _host_tensors([(4_194_304,)], 1337, 0.02)
     g, = _host_tensors([(4_194_304,)], 2337, 1e-3)
     m, v = np.zeros_like(p), np.zeros_like(p)
-    steps, elapsed = _timed_steps(lambda k: oadam.adam_step(p, g, m, v, k, weight_decay=0.1, **options), min_seconds, 200)
-    out["c1"] = _baseline_record(p.size, steps, elapsed, 28, "NumPy oracle AdamW, one flat fp32 tensor of 4,194,304")
+    steps, elapsed = _timed_steps(lambda k: oadam.reference_step(p, g, m, v, k, weight_decay=0.1, **options),
+                                  min_seconds, 200)
+    out["c1"] = _baseline_record(p.size, steps, elapsed, 28, "NumPy oracle AdamW, one flat fp32 tensor of 4,194,304, "
+                                 "with the reference's exp_avg_sq check and copy_ staging (oracle.adam.reference_step)")
     del p, g, m, v
 
     # C3 prefix: the first two GPT-2-124M layers, AMP: fp16 grads x 65536, fp32 master, bf16 model copy.
@@ -701,7 +706,7 @@ def cpu_baselines_other(min_seconds=3.0):
     steps, elapsed = _timed_steps(c3_step, min_seconds, 40)
     out["c3"] = _baseline_record(total_params(shapes), steps, elapsed, 30,
                                  f"NumPy oracle AMP step over layers 0-1 of the GPT-2-124M list "
-                                 f"({len(shapes)} tensors, {total_params(shapes)} params)",
+                                 f"({len(shapes)} tensors, {total_params(shapes)} params){OMITTED}",
                                  extrapolated_to=total_params(full))
     del masters, grads16, ms, vs
 
@@ -725,7 +730,7 @@ def cpu_baselines_other(min_seconds=3.0):
     steps, elapsed = _timed_steps(c4_step, min_seconds, 40)
     out["c4"] = _baseline_record(total_params(shapes), steps, elapsed, 22,
                                  f"NumPy oracle bf16 clip + master step over the attention tensors of GPT-1.3B "
-                                 f"layer 0 ({len(shapes)} tensors, {total_params(shapes)} params)",
+                                 f"layer 0 ({len(shapes)} tensors, {total_params(shapes)} params){OMITTED}",
                                  extrapolated_to=total_params(full))
     del masters, grads, ms, vs
 
@@ -753,9 +758,15 @@ def cpu_baselines_other(min_seconds=3.0):
     steps, elapsed = _timed_steps(c5_step, min_seconds, 40)
     out["c5"] = _baseline_record(total_params(shapes), steps, elapsed, 30,
                                  f"NumPy oracle AMP + clip + master step over the q projection of Llama-7B "
-                                 f"layer 0 ({len(shapes)} tensor, {total_params(shapes)} params)",
+                                 f"layer 0 ({len(shapes)} tensor, {total_params(shapes)} params){OMITTED}",
                                  extrapolated_to=total_params(full))
     return out
+
+
+# What the C3-C5 baselines (the fp32-master extension of the oracle) leave out
+# of the reference's path.
+OMITTED = ("; the oracle writes in place, without the reference's Tensor.copy_ staging (three copies per written "
+           "array) or its per-step exp_avg_sq check, so this overstates the reference's CPU rate")
 
 
 def pmc_traffic():

@@ -31,6 +31,10 @@ values, checked against torch's RNE conversion):
 * bfloat16 moments: stored moments widened to float32 before the step; the
   update uses the unrounded float32 moments; the stored moments are
   RNE(m), RNE(v).
+
+``reference_step`` is ``adam_step`` with the reference's staging copies and
+state check added, for the CPU baseline's timing; it is pinned to
+``adam_step`` bit for bit.
 """
 
 from __future__ import annotations
@@ -83,6 +87,49 @@ def adam_step(param, grad, exp_avg, exp_avg_sq, step: int, *, lr, betas, eps, we
         if decoupled and weight_decay != 0:
             values = values * scalar(dtype, 1 - lr * weight_decay)
         param[...] = values - scalar(dtype, lr) * update
+
+
+def _staged_write(target: np.ndarray, values: np.ndarray) -> None:
+    """``Tensor.copy_`` of a host array (tensor.py:1269-1287): ``Tensor(value)``
+    copies it (``_make_array(copy=True)``), ``__setitem__`` fills a staged
+    array from that copy and assigns the staged array to the storage."""
+    value = np.array(values, dtype=target.dtype, copy=True)
+    staged = np.empty(target.shape, dtype=target.dtype)
+    staged[...] = value
+    target[...] = staged
+
+
+def reference_step(param, grad, exp_avg, exp_avg_sq, step: int, *, lr, betas, eps, weight_decay,
+                   maximize=False, decoupled=True) -> None:
+    """``adam_step`` with the reference's memory traffic around the same
+    arithmetic, for timing the reference's CPU path: the per-step check that
+    ``exp_avg_sq`` holds no negative value (``_check_state`` with
+    ``runtime=True``, optim/_common.py:114 via :157), and every write through
+    ``Tensor.copy_``'s staging (``_staged_write``) for the two moments
+    (adam.py:35-36) and the parameter (_common.py:73).  Same results as
+    ``adam_step``."""
+    if np.any(np.less(exp_avg_sq, 0)):
+        raise ValueError("exp_avg_sq must be nonnegative.")
+    dtype = param.dtype
+    g = grad.copy()
+    if maximize:
+        np.negative(g, out=g)
+    if weight_decay != 0 and not decoupled:
+        g += scalar(dtype, weight_decay) * param
+    beta1, beta2 = betas
+    with np.errstate(over="ignore", under="ignore", invalid="ignore", divide="ignore"):
+        _staged_write(exp_avg, scalar(dtype, beta1) * exp_avg + scalar(dtype, 1 - beta1) * g)
+        _staged_write(exp_avg_sq, scalar(dtype, beta2) * exp_avg_sq + scalar(dtype, 1 - beta2) * g * g)
+        first_corrected = exp_avg / scalar(dtype, 1 - beta1 ** step)
+        second_corrected = exp_avg_sq / scalar(dtype, 1 - beta2 ** step)
+        denominator = np.sqrt(second_corrected) + scalar(dtype, eps)
+        update = first_corrected / denominator
+        if lr == 0:
+            return
+        values = param
+        if decoupled and weight_decay != 0:
+            values = values * scalar(dtype, 1 - lr * weight_decay)
+        _staged_write(param, values - scalar(dtype, lr) * update)
 
 
 def master_step(master, grad32, exp_avg, exp_avg_sq, step: int, *, lr, betas, eps, weight_decay,

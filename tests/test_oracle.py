@@ -450,3 +450,26 @@ def test_parallel_exact_sum_and_streamed_norm():
             got = parallel.total_norm_streamed(pool, len(bad), lambda i: bad[i])
             want = clip.total_norm(bad)
             assert (math.isnan(got) and math.isnan(want)) or got == want
+
+
+def test_reference_step_equals_adam_step():
+    """reference_step (adam_step plus the reference's copy_ staging and state
+    check, timed by the CPU baseline) gives adam_step's bits, float32 and
+    float16, decoupled and coupled decay, and raises on a negative
+    exp_avg_sq as the reference's state check does."""
+    rng = np.random.default_rng(5)
+    for dtype, decoupled in ((np.float32, True), (np.float32, False), (np.float16, True)):
+        p = (rng.standard_normal(1000) * 0.02).astype(dtype)
+        m = (rng.standard_normal(1000) * 1e-4).astype(dtype)
+        v = np.abs(rng.standard_normal(1000) * 1e-6).astype(dtype)
+        a = [p.copy(), m.copy(), v.copy()]
+        b = [p.copy(), m.copy(), v.copy()]
+        for step in range(1, 4):
+            g = (rng.standard_normal(1000) * 1e-3).astype(dtype)
+            options = dict(lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, decoupled=decoupled)
+            adam.adam_step(a[0], g, a[1], a[2], step, **options)
+            adam.reference_step(b[0], g, b[1], b[2], step, **options)
+            assert all(x.tobytes() == y.tobytes() for x, y in zip(a, b))
+    v[3] = -1.0
+    with pytest.raises(ValueError, match="nonnegative"):
+        adam.reference_step(p, p, m, v, 1, lr=3e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1)
