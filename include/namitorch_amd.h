@@ -177,6 +177,11 @@ const char *nt_last_error(void);
  * point's signature changes). */
 int32_t nt_abi_version(void);
 
+/* HIP_VERSION of the headers the library was compiled with, and that of the
+ * HIP runtime it is bound to in this process (hipRuntimeGetVersion; both
+ * major * 10^7 + minor * 10^5 + patch). */
+int32_t nt_hip_version(int32_t *built, int32_t *runtime);
+
 /* Number of visible HIP devices. */
 int32_t nt_device_count(int32_t *count);
 

@@ -133,6 +133,7 @@ assert ctypes.sizeof(GradXform) == 32
 SIGNATURES = {
     "nt_last_error": (ctypes.c_char_p, []),
     "nt_abi_version": (c_int32, []),
+    "nt_hip_version": (c_int32, [ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)]),
     "nt_device_count": (c_int32, [ctypes.POINTER(c_int32)]),
     "nt_device_arch": (c_int32, [c_int32, ctypes.c_char_p, c_int32]),
     "nt_set_device": (c_int32, [c_int32]),
@@ -269,8 +270,32 @@ def load() -> ctypes.CDLL:
             function.argtypes = argtypes
         if lib.nt_abi_version() != ABI_VERSION:
             raise NativeLibraryError(f"{LIB_PATH} has ABI {lib.nt_abi_version()}, expected {ABI_VERSION}; rebuild it.")
+        _check_runtime(lib)
         _lib = lib
         return lib
+
+
+HIP_VERSIONS = None     # (built, bound runtime), both HIP_VERSION-encoded, once loaded
+
+
+def _check_runtime(lib) -> None:
+    """The HIP runtime the library is bound to (PyTorch's bundled one or the
+    system's) must have the major version of the HIP headers the library was
+    built with: HIP keeps its runtime interface within a major version."""
+    global HIP_VERSIONS
+    built, runtime = c_int32(), c_int32()
+    if lib.nt_hip_version(ctypes.byref(built), ctypes.byref(runtime)) != NT_OK:
+        return                 # no runtime answer (no driver): nothing to compare, device calls fail on their own
+    HIP_VERSIONS = (built.value, runtime.value)
+    if built.value // 10_000_000 != runtime.value // 10_000_000:
+        raise NativeLibraryError(
+            f"{LIB_PATH} was built with HIP {_hip_text(built.value)} but is bound to HIP runtime "
+            f"{_hip_text(runtime.value)}: rebuild it with that ROCm, or set NT_SYSTEM_HIP_RUNTIME=1 to bind it to the "
+            f"system runtime.")
+
+
+def _hip_text(version: int) -> str:
+    return f"{version // 10_000_000}.{version // 100_000 % 100}.{version % 100_000}"
 
 
 _ERRORS = {NT_ERR_VALUE: ValueError, NT_ERR_TYPE: TypeError, NT_ERR_RUNTIME: RuntimeError, NT_ERR_HIP: RuntimeError}

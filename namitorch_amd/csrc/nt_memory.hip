@@ -290,6 +290,7 @@ int32_t nt_stream_create(int32_t device, void **out) {
         std::lock_guard<std::mutex> lock(d.lock);
         d.handles.erase(s);                         // the handle is live again
     }
+    device_pool().revive_stream(s);
     *out = s;
     return NT_OK;
 }
@@ -301,9 +302,13 @@ int32_t nt_stream_destroy(void *stream) {
     // blocks that were used on it need no ordering after it any more.
     NT_HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
     NT_HIP_TRY(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
-    DestroyedStreams &d = destroyed_streams();
-    std::lock_guard<std::mutex> lock(d.lock);
-    d.handles.insert(stream);
+    {
+        DestroyedStreams &d = destroyed_streams();
+        std::lock_guard<std::mutex> lock(d.lock);
+        d.handles.insert(stream);
+    }
+    // Its pool blocks become reusable on every stream.
+    device_pool().retire_stream(stream);
     return NT_OK;
 }
 

@@ -69,11 +69,14 @@ int32_t DevicePool::allocate(int32_t device, uint64_t bytes, void *stream, void 
     const uint64_t size = rounded(bytes);
     std::lock_guard<std::mutex> guard(lock_);
     Pool &pool = pools_[device];
-    // Smallest idle block of this stream that fits and wastes at most half of itself.
+    // Smallest idle block of this stream (or of a retired one) that fits and
+    // wastes at most half of itself.
     for (auto it = pool.idle.lower_bound(size); it != pool.idle.end() && it->first <= 2 * size; ++it) {
         Block *b = it->second;
-        if (b->device != device || b->stream != stream || !settled(b)) continue;
+        if (b->device != device || (b->stream != stream && !b->any_stream) || !settled(b)) continue;
         pool.idle.erase(it);
+        b->stream = stream;
+        b->any_stream = false;
         b->also_used.clear();
         live_[b->ptr] = b;
         pool.in_use += b->size;
@@ -143,8 +146,29 @@ int32_t DevicePool::release(void *ptr, std::string &error) {
         b->pending.push_back(event);
     }
     b->also_used.clear();
+    for (void *gone : retired_)
+        if (gone == b->stream) b->any_stream = true;
     pool.idle.emplace(b->size, b);
     return NT_OK;
+}
+
+void DevicePool::retire_stream(void *stream) {
+    std::lock_guard<std::mutex> guard(lock_);
+    for (auto &entry : pools_)
+        for (auto &idle : entry.second.idle)
+            if (idle.second->stream == stream) idle.second->any_stream = true;
+    for (void *gone : retired_)
+        if (gone == stream) return;
+    retired_.push_back(stream);
+}
+
+void DevicePool::revive_stream(void *stream) {
+    std::lock_guard<std::mutex> guard(lock_);
+    for (auto it = retired_.begin(); it != retired_.end(); ++it)
+        if (*it == stream) {
+            retired_.erase(it);
+            return;
+        }
 }
 
 void DevicePool::stats(int32_t device, uint64_t *in_use, uint64_t *reserved) {

@@ -9,7 +9,10 @@
 // those streams at free time has completed.  Blocks are never handed across
 // streams, so the pool never synchronizes, except when the device runs out
 // of memory: then idle blocks are released (after one device-wide wait) and
-// the allocation is retried.
+// the allocation is retried.  A stream destroyed after all its work completed
+// (retire_stream) leaves its blocks to every stream: its idle blocks, and
+// those freed later, are reused by allocations on any stream once their
+// events of other streams have completed.
 //
 // Host pool.  Page-locked buffers are kept after use: releasing page-locked
 // memory waits for the whole device.  Sizes are rounded up to a power of two
@@ -62,6 +65,11 @@ class DevicePool {
     // `stream` will also use the live block at `ptr`.
     int32_t record(void *ptr, void *stream, std::string &error);
     int32_t release(void *ptr, std::string &error);
+    // `stream` was destroyed after all its work completed: its blocks need no
+    // ordering after it any more.  revive_stream: the handle names a new
+    // stream again.
+    void retire_stream(void *stream);
+    void revive_stream(void *stream);
     void stats(int32_t device, uint64_t *in_use, uint64_t *reserved);
     // Return every idle block whose pending events have completed (waits for the device first).
     void trim(int32_t device);
@@ -72,6 +80,7 @@ class DevicePool {
         uint64_t size = 0;
         int32_t device = 0;
         void *stream = nullptr;                 // allocation stream: reuse happens only on it
+        bool any_stream = false;                // its allocation stream was retired: any stream may reuse it
         std::vector<void *> also_used;          // streams recorded with record()
         std::vector<void *> pending;            // events to complete before reuse
     };
@@ -87,6 +96,7 @@ class DevicePool {
     std::mutex lock_;
     std::map<int32_t, Pool> pools_;
     std::unordered_map<void *, Block *> live_;
+    std::vector<void *> retired_;               // destroyed stream handles not handed out again
 };
 
 class HostPool {

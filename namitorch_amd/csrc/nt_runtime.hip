@@ -92,6 +92,16 @@ const char *nt_last_error(void) { return g_last_error.c_str(); }
 
 int32_t nt_abi_version(void) { return 4; }
 
+int32_t nt_hip_version(int32_t *built, int32_t *runtime) {
+    clear_error();
+    if (built == nullptr || runtime == nullptr) return fail(NT_ERR_VALUE, "nt_hip_version: NULL output");
+    *built = HIP_VERSION;
+    int version = 0;
+    NT_HIP_TRY(hipRuntimeGetVersion(&version), "hipRuntimeGetVersion");
+    *runtime = version;
+    return NT_OK;
+}
+
 int32_t nt_device_count(int32_t *count) {
     clear_error();
     if (count == nullptr) return fail(NT_ERR_VALUE, "count is NULL");

@@ -257,11 +257,50 @@ static void test_host_pool() {
     CHECK(ops.events.empty());
 }
 
+static void test_retired_stream_blocks_serve_every_stream() {
+    FakeOps ops;
+    std::string error;
+    {
+        DevicePool pool(ops);
+        void *a = nullptr, *b = nullptr, *c = nullptr, *d = nullptr, *e = nullptr, *f = nullptr;
+        CHECK(pool.allocate(0, 4096, S(5), &a, error) == NT_OK);
+        CHECK(pool.allocate(0, 4096, S(5), &b, error) == NT_OK);
+        CHECK(pool.allocate(0, 8192, S(5), &c, error) == NT_OK);
+        CHECK(pool.record(c, S(6), error) == NT_OK);
+        CHECK(pool.release(a, error) == NT_OK);          // idle on stream 5 before it is destroyed
+        CHECK(pool.release(c, error) == NT_OK);          // idle, also waiting for stream 6
+        pool.retire_stream(S(5));
+        CHECK(pool.release(b, error) == NT_OK);          // freed after the destroy
+        // Another stream reuses both 4 KiB blocks; nothing new is allocated.
+        CHECK(pool.allocate(0, 4096, S(7), &d, error) == NT_OK && (d == a || d == b));
+        CHECK(pool.allocate(0, 4096, S(8), &e, error) == NT_OK && (e == a || e == b) && e != d);
+        CHECK(ops.device_allocs == 3);
+        // The 8 KiB block still waits for stream 6.
+        CHECK(pool.allocate(0, 8192, S(7), &f, error) == NT_OK && f != c);
+        ops.complete(S(6));
+        void *g = nullptr;
+        CHECK(pool.allocate(0, 8192, S(9), &g, error) == NT_OK && g == c);
+        // A block handed to stream 7 belongs to stream 7 from then on.
+        CHECK(pool.release(d, error) == NT_OK);
+        void *h = nullptr;
+        CHECK(pool.allocate(0, 4096, S(8), &h, error) == NT_OK && h != d);
+        // A handle that names a new stream again is ordinary: its blocks stay with it.
+        pool.revive_stream(S(5));
+        void *k = nullptr, *l = nullptr;
+        CHECK(pool.allocate(0, 1024, S(5), &k, error) == NT_OK);
+        CHECK(pool.release(k, error) == NT_OK);
+        CHECK(pool.allocate(0, 1024, S(7), &l, error) == NT_OK && l != k);
+        for (void *p : {e, f, g, h, l}) CHECK(pool.release(p, error) == NT_OK);
+    }
+    CHECK(ops.events.empty());
+}
+
 int main() {
     test_rounding();
     test_stream_ordered_reuse();
     test_other_streams_gate_reuse();
     test_out_of_memory_trims();
+    test_retired_stream_blocks_serve_every_stream();
     test_errors();
     test_host_pool();
     if (failures == 0) std::printf("pools: all checks passed\n");

@@ -249,3 +249,40 @@ def test_stream_destroyed_before_its_plan_and_block():
         again, _ = two_steps()
         assert again.numpy().tobytes() == values.tobytes()
     fresh.synchronize()
+
+
+def test_destroyed_stream_blocks_serve_other_streams():
+    """Blocks of a destroyed library stream are reused by allocations on
+    other streams: the idle ones at once, one freed after the destroy as
+    well, while the pool reserves no more memory.  The data written through
+    a reused block is intact."""
+    import ctypes
+    from namitorch_amd import _native
+    size = 3 << 20                                             # a 4 MiB pool block
+    torch.cuda.synchronize()
+    nt.runtime.empty_cache(0)                                  # no idle block of other tests competes
+    stream = nt.runtime.Stream(0)
+    first, second = ctypes.c_void_p(), ctypes.c_void_p()
+    _native.call("nt_malloc", 0, size, stream.handle, ctypes.byref(first))
+    _native.call("nt_malloc", 0, size, stream.handle, ctypes.byref(second))
+    _native.call("nt_fill", first.value, size // 4, 4, 0x3F800000, stream.handle)
+    _native.call("nt_free", first.value)                       # idle before the destroy
+    reserved = nt.runtime.memory_stats(0)["reserved"]
+    _native.call("nt_stream_destroy", stream.handle)
+    stream._owned = False
+    _native.call("nt_free", second.value)                      # freed after the destroy
+    other = nt.runtime.Stream(0)
+    got = []
+    for _ in range(2):
+        block = ctypes.c_void_p()
+        _native.call("nt_malloc", 0, size, other.handle, ctypes.byref(block))
+        got.append(block.value)
+    assert sorted(got) == sorted([first.value, second.value])
+    assert nt.runtime.memory_stats(0)["reserved"] == reserved
+    _native.call("nt_fill", got[0], size // 4, 4, 0x40000000, other.handle)
+    out = np.empty(size // 4, np.float32)
+    _native.call("nt_memcpy_d2h", out.ctypes.data, got[0], size, other.handle)
+    assert np.all(out == 2.0)
+    for block in got:
+        _native.call("nt_free", block)
+    other.synchronize()

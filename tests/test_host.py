@@ -345,3 +345,30 @@ def test_registered_cache_sees_a_parameter_moved_between_groups():
     cache = optimizer.__dict__["_registered_cache"]
     assert optimizer._registered_parameters()[0] is optimizer.param_groups[0]["params"][0]
     assert optimizer.__dict__["_registered_cache"] is not cache
+
+
+def test_runtime_major_version_mismatch_is_refused():
+    """The library refuses a HIP runtime of another major version than the
+    headers it was built with (PyTorch's bundled runtime could be one), with
+    a message naming both and the way out; a newer minor version passes."""
+    import ctypes
+
+    from namitorch_amd import _native
+
+    class FakeLibrary:
+        def __init__(self, built, runtime):
+            self.values = (built, runtime)
+
+        def nt_hip_version(self, built, runtime):
+            ctypes.cast(built, ctypes.POINTER(ctypes.c_int32))[0] = self.values[0]
+            ctypes.cast(runtime, ctypes.POINTER(ctypes.c_int32))[0] = self.values[1]
+            return _native.NT_OK
+
+    saved = _native.HIP_VERSIONS
+    try:
+        _native._check_runtime(FakeLibrary(70226015, 70051831))        # 7.2 headers, 7.0 runtime
+        assert _native.HIP_VERSIONS == (70226015, 70051831)
+        with pytest.raises(_native.NativeLibraryError, match=r"built with HIP 7\.2\.26015 but is bound to HIP runtime 6\.4\.0.*NT_SYSTEM_HIP_RUNTIME=1"):
+            _native._check_runtime(FakeLibrary(70226015, 60400000))
+    finally:
+        _native.HIP_VERSIONS = saved
