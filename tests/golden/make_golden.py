@@ -523,7 +523,60 @@ def device_cases(nt):
 
 # Fixture sets that write their own files (and keep their records there);
 # `--only name,...` regenerates just those.
-STANDALONE = {"scalar_ops": scalar_cases, "clip_f64": clip_f64_cases, "devices": device_cases}
+def package_checkpoint_case(nt):
+    """The format's other direction: ``checkpoint_package.nt`` is written by
+    this package's save_checkpoint (namitorch_amd/checkpoint.py) from the
+    seeded host state of ``package_state.build``, and the reference's
+    load_checkpoint (training/checkpoint.py:131-174) restores it into the
+    reference's own model, AdamW, WarmupCosine and GradScaler.  What the
+    reference restored is stored: the arrays in ``package_checkpoint.npz``,
+    the rest in ``package_checkpoint.json``."""
+    sys.path.insert(0, str(HERE.parents[1]))
+    sys.path.insert(0, str(HERE))
+    import namitorch_amd as ours
+    import package_state
+    from namitorch_amd import checkpoint as our_checkpoint
+    from namitorch.optim.lr_scheduler import WarmupCosine
+    from namitorch.training.checkpoint import load_checkpoint
+
+    named, optimizer, scheduler, scaler = package_state.build(ours)
+    path = HERE / "checkpoint_package.nt"
+    our_checkpoint.save_checkpoint(path, named, optimizer, scheduler, scaler=scaler, **package_state.SAVE)
+
+    class Tiny(nt.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.weight = nt.nn.Parameter(np.zeros((40, 48), np.float32))
+            self.bias = nt.nn.Parameter(np.zeros(40, np.float32))
+
+    model = Tiny()
+    theirs = nt.optim.AdamW([{"params": [model.weight], "weight_decay": 0.1},
+                             {"params": [model.bias], "weight_decay": 0.0}], lr=2e-3, betas=(0.9, 0.95), eps=1e-8)
+    their_scheduler = WarmupCosine(theirs, 3, 12, min_lr=1e-4)
+    their_scaler = nt.amp.GradScaler()
+    info = load_checkpoint(path, model, theirs, their_scheduler, scaler=their_scaler)
+    arrays = {}
+    groups = []
+    for index, (name, parameter) in enumerate((("weight", model.weight), ("bias", model.bias))):
+        state = theirs.state[id(parameter)]
+        arrays[f"{name}"] = parameter._data.copy()
+        arrays[f"{name}_exp_avg"] = state["exp_avg"]._data.copy()
+        arrays[f"{name}_exp_avg_sq"] = state["exp_avg_sq"]._data.copy()
+        arrays[f"{name}_step"] = np.int64(state["step"])
+    for group in theirs.param_groups:
+        groups.append({key: (list(value) if isinstance(value, tuple) else value)
+                       for key, value in group.items() if key != "params"})
+    np.savez(HERE / "package_checkpoint.npz", **arrays)
+    record = dict(info={key: value for key, value in info.items() if key != "load_result"},
+                  load_result=repr(info["load_result"]), param_groups=groups,
+                  scheduler=their_scheduler.state_dict(), last_lr=their_scheduler.get_last_lr(),
+                  scaler=their_scaler.state_dict(), scale=their_scaler.get_scale())
+    (HERE / "package_checkpoint.json").write_text(json.dumps(record, indent=1, sort_keys=True) + "\n")
+    return record
+
+
+STANDALONE = {"scalar_ops": scalar_cases, "clip_f64": clip_f64_cases, "devices": device_cases,
+              "package_checkpoint": package_checkpoint_case}
 
 
 def main(reference: str, only: list[str] | None = None) -> None:

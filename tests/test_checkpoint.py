@@ -239,3 +239,62 @@ def test_checkpoint_written_here_has_the_reference_layout(tmp_path):
         assert ours["state"][key]["step"] == values["step"]
         for buffer in ("exp_avg", "exp_avg_sq"):
             assert ours["state"][key][buffer].numpy().tobytes() == values[buffer].numpy().tobytes()
+
+
+def _same_tree(a, b, where="checkpoint"):
+    """Equal archive trees: the same keys, values and types; Tensors and
+    arrays with the same dtype, shape and bytes."""
+    if isinstance(a, nt.Tensor) or isinstance(b, nt.Tensor):
+        assert isinstance(a, nt.Tensor) and isinstance(b, nt.Tensor), where
+        assert a.dtype is b.dtype and a.shape == b.shape, where
+        assert a.numpy().tobytes() == b.numpy().tobytes(), where
+    elif isinstance(a, np.ndarray) or isinstance(b, np.ndarray):
+        assert isinstance(a, np.ndarray) and isinstance(b, np.ndarray), where
+        assert a.dtype == b.dtype and a.shape == b.shape and a.tobytes() == b.tobytes(), where
+    elif isinstance(a, dict):
+        assert isinstance(b, dict) and set(a) == set(b), where
+        for key in a:
+            _same_tree(a[key], b[key], f"{where}[{key!r}]")
+    elif isinstance(a, (list, tuple)):
+        assert type(a) is type(b) and len(a) == len(b), where
+        for index, (x, y) in enumerate(zip(a, b)):
+            _same_tree(x, y, f"{where}[{index}]")
+    else:
+        assert type(a) is type(b) and a == b, (where, a, b)
+
+
+def test_checkpoint_written_here_restores_in_the_reference(tmp_path):
+    """The format's other direction.  checkpoint_package.nt was written by
+    this package's save_checkpoint from package_state.build's seeded state,
+    and the reference's load_checkpoint (training/checkpoint.py:131-174)
+    restored it (tests/golden/make_golden.py, package_checkpoint_case): the
+    parameters, moments, step counts, group options, schedule and scaler it
+    restored are exactly the saved state, and the writer still writes that
+    file's contents for that state."""
+    import json
+    import sys
+    sys.path.insert(0, str(GOLDEN))
+    import package_state
+    named, optimizer, scheduler, scaler = package_state.build(nt)
+    path = tmp_path / "again.nt"
+    ck.save_checkpoint(path, named, optimizer, scheduler, scaler=scaler, **package_state.SAVE)
+    _same_tree(ser.load(path), ser.load(GOLDEN / "checkpoint_package.nt"))
+    restored = np.load(GOLDEN / "package_checkpoint.npz")
+    record = json.loads((GOLDEN / "package_checkpoint.json").read_text())
+    for name in ("weight", "bias"):
+        parameter = named[name]
+        state = optimizer.state[id(parameter)]
+        assert restored[name].tobytes() == parameter.numpy().tobytes()
+        for buffer in ("exp_avg", "exp_avg_sq"):
+            assert restored[f"{name}_{buffer}"].tobytes() == state[buffer].numpy().tobytes(), (name, buffer)
+        assert int(restored[f"{name}_step"]) == state["step"] == 7
+    saved = package_state.SAVE
+    assert record["info"] == {"step": saved["step"], "epoch": saved["epoch"], "config": saved["config"],
+                              "cumulative_tokens": saved["cumulative_tokens"]}
+    assert record["load_result"] == "LoadStateDictResult(missing_keys=[], unexpected_keys=[])"
+    groups = [{key: (list(value) if isinstance(value, tuple) else value) for key, value in group.items()
+               if key != "params"} for group in optimizer.param_groups]
+    assert record["param_groups"] == groups
+    assert record["scheduler"] == json.loads(json.dumps(scheduler.state_dict()))
+    assert record["last_lr"] == scheduler.get_last_lr()
+    assert record["scaler"] == scaler.state_dict() and record["scale"] == scaler.get_scale() == 2048.0
