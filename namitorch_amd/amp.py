@@ -31,10 +31,9 @@ from .backends._graph_capture import reject_during_capture
 from .dtype import float32, float64, promote_with_scalar
 from .optim import clip_grad
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
-from .tensor import GradTransform, _unsettled_steps, check_addends, is_grad_enabled
+from .tensor import GradTransform, _requires_grad_changes, _unsettled_steps, check_addends, is_grad_enabled
 
 _REQUIRES = attrgetter("_requires_grad")
-_WRITABLE = attrgetter("_writable")
 _PENDING = attrgetter("_pending")
 _COUNTER = attrgetter("_version_counter")
 _VALUE = attrgetter("value")
@@ -362,12 +361,15 @@ class GradScaler:
         return gradients
 
     @staticmethod
-    def _entry_inputs(optimizer):
+    def _entry_inputs(optimizer, known=None):
         """What an optimizer's gradient entries are a pure function of
         (``Optimizer._grad_entries``): its registered-parameter cache (a new
         object whenever the groups change), the parameters' requires_grad
         flags and their gradient objects; None for an optimizer without that
-        cache."""
+        cache.  Returned as (cache, requires_grad change count, flags,
+        gradients).  With `known`, an earlier result, the flags are taken
+        from it when the cache is the same object and no requires_grad flag
+        has changed anywhere since (the count is unchanged)."""
         registered_of = getattr(optimizer, "_registered_parameters", None)
         if not callable(registered_of) or not callable(getattr(optimizer, "_grad_entries", None)):
             return None
@@ -375,7 +377,12 @@ class GradScaler:
         cache = getattr(optimizer, "__dict__", {}).get("_registered_cache")
         if cache is None:
             return None
-        return cache, tuple(map(_REQUIRES, registered)), tuple(map(_GRAD, registered))
+        changes = _requires_grad_changes.value
+        if known is not None and known[0] is cache and known[1] == changes:
+            requires = known[2]
+        else:
+            requires = tuple(map(_REQUIRES, registered))
+        return cache, changes, requires, tuple(map(_GRAD, registered))
 
     @staticmethod
     def _finite(gradients) -> bool:
@@ -404,7 +411,7 @@ class GradScaler:
         self._optimizer_states[identity] = state
         transform = GradTransform(scale=self._scale)
         grads = tuple(map(_SECOND_OF, gradients))
-        if (any(map(_REQUIRES, grads)) and is_grad_enabled()) or not all(map(_WRITABLE, grads)):
+        if any(map(_REQUIRES, grads)) and is_grad_enabled():
             for gradient in grads:
                 gradient._ensure_inplace_allowed()            # raises the matching error
         if any(map(_PENDING, grads)):
@@ -443,11 +450,13 @@ class GradScaler:
         if inputs is not None:
             # The entries are those of unscale_ when what they are a function
             # of is unchanged (three passes instead of collecting them again).
-            now = self._entry_inputs(optimizer)
-            if now is not None and now[0] is inputs[0] and now[1] == inputs[1] and all(map(is_, now[2], inputs[2])):
+            now = self._entry_inputs(optimizer, inputs)
+            if now is not None and now[0] is inputs[0] and now[2] == inputs[2] and all(map(is_, now[3], inputs[3])):
                 current = previous
                 grads = tuple(map(_SECOND_OF, current))
-                if any(map(_REQUIRES, grads)):
+                # unscale_ refused gradients that required grad; these are
+                # the same objects, so only a flag changed since can matter.
+                if now[1] != inputs[1] and any(map(_REQUIRES, grads)):
                     raise RuntimeError("GradScaler requires detached floating gradients.")
         if current is None:
             current = self._gradients(optimizer)
@@ -602,7 +611,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     device_step.scheduler = scheduler
     device_step.error_if_nonfinite = refuse
     transform = GradTransform(device=device_step)
-    if (any(map(_REQUIRES, gradients)) and is_grad_enabled()) or not all(map(_WRITABLE, gradients)):
+    if any(map(_REQUIRES, gradients)) and is_grad_enabled():
         for gradient in gradients:
             gradient._ensure_inplace_allowed()            # raises the matching error
     check_addends(gradients)                              # before any bookkeeping changes
@@ -730,7 +739,7 @@ def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers, 
         return _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers, error_if_nonfinite)
     backend = keys[0][0]
     for gradients in gathered:
-        if (any(map(_REQUIRES, gradients)) and is_grad_enabled()) or not all(map(_WRITABLE, gradients)):
+        if any(map(_REQUIRES, gradients)) and is_grad_enabled():
             for gradient in gradients:
                 gradient._ensure_inplace_allowed()        # raises the matching error
         check_addends(gradients)                          # before any bookkeeping changes

@@ -22,6 +22,7 @@ from __future__ import annotations
 import atexit
 import ctypes
 import math
+import operator
 import threading
 import weakref
 from collections import OrderedDict
@@ -499,6 +500,9 @@ class HIPBackend:
             return bool(flag.download()[0])
 
 
+_INCOMING_OF = operator.attrgetter("_incoming")
+
+
 def incoming_pointers(gradients) -> list | None:
     """The incoming-gradient column for `gradients` (0 where nothing is
     deferred), or None when no gradient has a deferred accumulation.
@@ -508,10 +512,6 @@ def incoming_pointers(gradients) -> list | None:
     from ..tensor import check_addends
     check_addends(gradients)
     return [0 if gradient._incoming is None else gradient._incoming[0]._ptr for gradient in gradients]
-
-
-def _INCOMING_OF(gradient):
-    return gradient._incoming
 
 
 def _is_device(value) -> bool:

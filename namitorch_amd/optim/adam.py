@@ -310,7 +310,6 @@ class Adam(_FirstOrderOptimizer):
 
 _GRAD = attrgetter("_grad")
 _REQUIRES = attrgetter("_requires_grad")
-_WRITABLE = attrgetter("_writable")
 _PENDING = attrgetter("_pending")
 _INCOMING = attrgetter("_incoming")
 _CLEAN = attrgetter("_clean_version")
@@ -509,9 +508,7 @@ class _Replay:
                 return False
         except KeyError:
             return False
-        buffers = self.buffers
-        if (not flags_seen and any(map(_REQUIRES, buffers))) or not all(map(_WRITABLE, buffers)) \
-                or not all(map(_WRITABLE, self.members)):
+        if not flags_seen and any(map(_REQUIRES, self.buffers)):
             return False
         self.requires_checked = changes
         if not all(map(eq, map(_CLEAN, self.seconds), map(_VALUE, self.second_counters))):

@@ -332,12 +332,6 @@ def get_grad_norm(parameters, norm_type: float = 2) -> Tensor:
     return _norm_tensor(_total_norm(gradients, order), gradients)
 
 
-def _require_writable(gradients: list[Tensor]) -> None:
-    if any(not gradient._writable for gradient in gradients):
-        raise RuntimeError("Cannot clip read-only gradient storage.")
-
-
-_WRITABLE = attrgetter("_writable")
 _VALUE = attrgetter("value")
 # Device-decided clips not yet settled by an optimizer step or a version
 # read: past this many, the oldest is settled at the next clip (its finalize
@@ -390,11 +384,9 @@ def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
     below 1: it is taken optimistically and undone when the step is settled.
 
     None (the host path decides) unless no host decision of the reference
-    can raise or differ: ``_norm_on_device``'s conditions, and every
-    gradient writable, so a rewrite cannot fail.
+    can raise or differ: ``_norm_on_device``'s conditions.  (The rewrite
+    itself cannot fail: every Tensor here is writable.)
     """
-    if not all(map(_WRITABLE, gradients)):
-        return None
     launched = _norm_on_device(gradients, order, maximum, with_mirror=True)
     if launched is None:
         return None
@@ -436,7 +428,6 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
     with np.errstate(invalid="ignore", divide="ignore"):
         coefficient = float(np.divide(np.float64(maximum), np.add(np.float64(norm), _NORM_EPS)))
     if coefficient < 1:
-        _require_writable(gradients)
         # One shared clip transform per prior pending transform object (usually
         # the single unscale transform of unscale_, or none), found by
         # identity; the dict keeps each base alive, so identities stay unique.
@@ -447,8 +438,8 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
         if pendings and all(map(is_, pendings, repeat(pendings[0]))) and (
                 pendings[0] is None or (pendings[0].clip is None and pendings[0].device is None)):
             # Common case, one shared prior transform (or none): the loop below
-            # with C-level passes.  Inside no_grad only writability can fail the
-            # in-place check, and _require_writable has checked it.
+            # with C-level passes.  Inside no_grad the in-place check cannot
+            # fail (only writability could, and every Tensor is writable).
             base = unscaled_none if pendings[0] is None else pendings[0]
             transform = base.then_clip(coefficient)
             keep = tuple(map(eq, map(_FINITE_VERSION, gradients), map(_VERSION_VALUE, gradients)))
@@ -479,8 +470,7 @@ def clip_grad_norm_(parameters, max_norm: float, norm_type: float = 2, error_if_
 
 def clip_grad_value_(parameters, clip_value: float) -> None:
     bound = _nonnegative(clip_value, "clip_value")
-    gradients = _gradients(parameters)
-    _require_writable(gradients)
+    _gradients(parameters)
     raise NotImplementedError(
         f"clip_grad_value_ (bound {bound}) is outside the optimizer-step path this package accelerates."
     )

@@ -306,9 +306,16 @@ def _assign_host(target: np.ndarray, source: object, dtype: DType, source_dtype:
 class Tensor:
     __slots__ = (
         "_storage", "_dtype", "_device", "_requires_grad", "_grad", "_version_counter",
-        "_writable", "_pending", "_incoming", "_is_leaf", "_ptr", "_numel", "_shape", "_clean_version",
+        "_pending", "_incoming", "_is_leaf", "_ptr", "_numel", "_shape", "_clean_version",
         "_finite_version", "__weakref__",
     )
+    # Every Tensor here may be written in place: device storage always, and
+    # host arrays through NumPy, which refuses writes to read-only arrays by
+    # itself.  The reference's read-only Tensors (expand views, read-only
+    # arrays; tensor.py:348,1012) do not exist, so the flag is a class
+    # constant that no instance can change, and the per-step paths do not
+    # test it.
+    _writable = True
 
     def __init__(self, data: object, dtype: object = None, requires_grad: builtins.bool = False, *, device=None):
         resolved = _resolve_dtype(data, dtype)
@@ -349,7 +356,6 @@ class Tensor:
         self._requires_grad = requires_grad
         self._grad = None
         self._version_counter = version_counter if version_counter is not None else _VersionCounter()
-        self._writable = True
         self._pending = None
         self._incoming = None
         self._is_leaf = True
