@@ -328,6 +328,17 @@ def test_requires_grad_changes_are_counted():
     assert _requires_grad_changes.value == before + 2
 
 
+def test_writability_is_a_constant():
+    """Every Tensor may be written in place and no instance can say
+    otherwise: the per-step paths (step replay, GradScaler, clip) rely on
+    it instead of scanning the flag."""
+    for tensor in (nt.Tensor(np.zeros(3, np.float32)), nt.Parameter(nt.Tensor(np.zeros(3, np.float32)))):
+        assert tensor._writable is True
+        with pytest.raises(AttributeError):
+            tensor._writable = False
+        assert tensor._writable is True
+
+
 def test_registered_cache_sees_a_parameter_moved_between_groups():
     """Moving the last parameter of one group to the front of the next keeps
     the flattened order but changes group membership (and so the options a
