@@ -25,7 +25,10 @@ pool by ``oracle.parallel``, which gives the oracle's bits):
   bfloat16 gradients scaled by 65536, clip at 1.0.  The norm's oracle streams
   the gradients back one tensor at a time (``parallel.total_norm_streamed``);
   a seeded sample of whole tensors (the embedding, the head, the final norm
-  and five others) is stepped by the oracle and compared.
+  and five others) is stepped by the oracle and compared;
+* C4/8 and C5/8: one rank's slices of an 8-way sharded step (every tensor's
+  flat storage cut in eight) through ``fused_step``, the whole state of every
+  slice compared.
 
 Bars (the path's target tolerances): found_inf flags, skip decisions and the
 loss-scale sequence bit-exact; norms within 1e-12 relative; float32 master,
@@ -347,5 +350,72 @@ def test_c5_full_llama7b_amp_clip_two_steps(pool):
         flips += _compare(f"v[{i}]", state["exp_avg_sq"].numpy(), v[i], unit_bits=32, allow_rate=1e-6)
         flips += _compare(f"copy[{i}]", params[i].numpy(), lowp.round_bf16(master[i]), unit_bits=16, allow_rate=1e-6)
     _say(f"C5 sample {sample} matches the oracle ({flips} elements one unit away)")
+    del params, optimizer, scaler
+    _release()
+
+
+# ---- C4/8 and C5/8: one GPU's share of an 8-way sharded step ------------------------------------------
+@pytest.mark.parametrize("config", ["c4s8", "c5s8"])
+def test_sharded_slices_fused(pool, config):
+    """One rank's slices of an 8-way sharded step (every tensor's flat storage
+    cut in eight; the benchmark's C4/8 and C5/8): each slice keeps its
+    tensor's weight-decay group.  C4/8 (292 slices, 164 M parameters):
+    bfloat16 moments, clip at 1.0, four fused steps.  C5/8 (291 slices, 842 M
+    parameters): float32 moments, AMP at 65536 with clip at 1.0, three fused
+    steps.  The whole state against the oracle."""
+    from namitorch_amd.param_lists import shard_shapes
+    full = gpt_1p3b_shapes() if config == "c4s8" else llama7b_shapes()
+    shapes = shard_shapes(full, 8)
+    amp = config == "c5s8"
+    steps = 3 if amp else 4
+    assert len(shapes) == len(full) and total_params(shapes) == (164_477_440 if config == "c4s8" else 842_301_952)
+    decays = [0.1 if k else 0.0 for k in decay_mask(full)]
+    scale = 65536.0 if amp else 1.0
+    weights = _device_normals(shapes, 4242, 0.02, torch.bfloat16)
+    params = [nt.Parameter(w) for w in weights]
+    master = [_host_bf16(pool, w) for w in weights]
+    del weights
+    m = [np.zeros_like(h) for h in master]
+    v = [np.zeros_like(h) for h in master]
+    groups = [{"params": [p for p, d in zip(params, decays) if d], "weight_decay": 0.1},
+              {"params": [p for p, d in zip(params, decays) if not d], "weight_decay": 0.0}]
+    optimizer = nt.optim.AdamW(groups, master_weights=True, state_dtype="bfloat16" if not amp else None, **OPTIONS)
+    scaler = nt.GradScaler(init_scale=scale) if amp else None
+    loss = nt.Tensor(np.float32(1.0), device=DEV)
+    for step in range(1, steps + 1):
+        grads = _device_normals(shapes, 5242 + step, 1e-3 * scale, torch.bfloat16)
+        for p, g in zip(params, grads):
+            p.grad = nt.Tensor(g)
+        if amp:
+            scaler.scale(loss)
+        result = nt.amp.fused_step(optimizer, scaler, max_norm=1.0)
+        host = [_host_bf16(pool, g) for g in grads]
+        del grads
+        if amp:
+            host = [parallel.unscale(pool, g, scale, "bfloat16") for g in host]
+        norm = parallel.total_norm_streamed(pool, len(host), lambda i: host[i])
+        assert math.isfinite(norm)
+        coefficient = oclip.clip_coefficient(1.0, norm)
+        assert coefficient < 1
+        assert result.finite and result.updated
+        assert abs(result.norm - norm) <= NORM_RTOL * norm, (step, result.norm, norm)
+        if amp:
+            assert result.scale == scale
+        for i, g in enumerate(host):
+            clipped = parallel.clip_apply(pool, g, coefficient, "bfloat16")
+            parallel.master_step(pool, master[i], clipped, m[i], v[i], step, weight_decay=decays[i],
+                                 state_bf16=not amp, **OPTIONS)
+        del host
+        _say(f"{config} step {step}: norm {norm:.9g}")
+    moment_bits = 32 if amp else 16
+    flips = 0
+    for i, p in enumerate(params):
+        state = optimizer.state[id(p)]
+        assert state["step"] == steps
+        flips += _compare(f"master[{i}]", state["master"].numpy(), master[i], unit_bits=32, allow_rate=1e-6)
+        flips += _compare(f"m[{i}]", state["exp_avg"].numpy(), m[i], unit_bits=moment_bits, allow_rate=1e-6)
+        flips += _compare(f"v[{i}]", state["exp_avg_sq"].numpy(), v[i], unit_bits=moment_bits, allow_rate=1e-6)
+        flips += _compare(f"copy[{i}]", p.numpy(), lowp.round_bf16(master[i]), unit_bits=16, allow_rate=1e-6)
+    _say(f"{config} matches the oracle over every slice ({flips} elements one unit away)")
     del params, optimizer, scaler
     _release()
