@@ -153,8 +153,60 @@ __device__ __forceinline__ bool xform_from_ctrl(const nt_amp_ctrl *ctrl, int hon
     return true;
 }
 
+// One whole kPassSlice-element slice on one wave, one 4-element group per
+// lane, for the common case: an aligned tensor without a deferred addend,
+// Adam/AdamW without maximize or coupled decay, the parameter updated, fp32
+// rounding.  The gradient transform is fixed at compile time (UNSCALE as
+// Xform::unscale, CLIP), so the element code has no branches on it.  The
+// arithmetic is the general path's (adamw_mt_kernel) for those settings,
+// operation for operation.
+template <class P, class G, class S, class C, bool HAS_COPY, int UNSCALE, bool CLIP>
+__device__ __forceinline__ void lean_slice(const DevTensor &d, const nt_adamw_coefs &c, const Xform &xf,
+                                           uint64_t start) {
+    auto *pp = reinterpret_cast<typename P::raw *>(d.param);
+    auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
+    auto *ap = reinterpret_cast<typename S::raw *>(d.exp_avg);
+    auto *bp = reinterpret_cast<typename S::raw *>(d.exp_avg_sq);
+    auto *cp = reinterpret_cast<typename C::raw *>(d.model_copy);
+    const uint64_t i = start + (uint64_t)threadIdx.x * kVec;
+    float p[kVec], g[kVec], a[kVec], b[kVec];
+    Vec4IO<G, true>::load(gp, i, g);
+    Vec4IO<S, true>::load(ap, i, a);
+    Vec4IO<S, true>::load(bp, i, b);
+    Vec4IO<P, true>::load(pp, i, p);
+    const bool decay = c.weight_decay != 0.0f;
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) {
+        float gk = g[k];
+        if constexpr (UNSCALE == 1) gk = G::round_f32(gk / xf.scale);
+        if constexpr (UNSCALE == 2) gk = G::round_f32(gk * xf.inv_scale);
+        if constexpr (CLIP) gk = G::to_f32(G::from_f64((double)gk * xf.clip_coef));
+        a[k] = (c.beta1 * a[k]) + (c.complement1 * gk);
+        b[k] = (c.beta2 * b[k]) + ((c.complement2 * gk) * gk);
+        const float value = decay ? p[k] * c.decay_factor : p[k];
+        const float corrected = a[k] / c.correction1;
+        const float denominator = __builtin_sqrtf(b[k] / c.correction2) + c.eps;
+        p[k] = value - c.lr * (corrected / denominator);
+    }
+    Vec4IO<S, true>::store(ap, i, a);
+    Vec4IO<S, true>::store(bp, i, b);
+    Vec4IO<P, true>::store(pp, i, p);
+    if constexpr (HAS_COPY) Vec4IO<C, true>::store(cp, i, p);
+}
+
+template <class P, class G, class S, class C, bool HAS_COPY, bool CLIP>
+__device__ __forceinline__ void lean_slice_unscale(const DevTensor &d, const nt_adamw_coefs &c, const Xform &xf,
+                                                   uint64_t start) {
+    if (xf.unscale == 2) lean_slice<P, G, S, C, HAS_COPY, 2, CLIP>(d, c, xf, start);
+    else if (xf.unscale == 1) lean_slice<P, G, S, C, HAS_COPY, 1, CLIP>(d, c, xf, start);
+    else lean_slice<P, G, S, C, HAS_COPY, 0, CLIP>(d, c, xf, start);
+}
+
 // BLOCK lanes per workgroup, UNROLL 4-element groups in flight per lane;
-// each workgroup takes one slice of a task (task_slice).
+// each workgroup takes one slice of a task (task_slice).  A whole one-wave
+// slice in the common case runs lean_slice; everything else (tensor tails,
+// unaligned tensors, deferred addends, maximize, coupled decay, lr == 0,
+// fp16 rounding, the whole-task shape) the general loop below.
 template <class P, class G, class S, class C, class R, bool HAS_COPY, int BLOCK, int UNROLL>
 __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__restrict__ tensors,
                                                          const Task *__restrict__ tasks, MtArgs args) {
@@ -167,6 +219,14 @@ __global__ __launch_bounds__(BLOCK) void adamw_mt_kernel(const DevTensor *__rest
     const DevTensor d = *dp;
     const nt_adamw_coefs c = args.slots[d.slot];
     const uint64_t start = slice.start, end = slice.end;
+    if constexpr (BLOCK == 64 && UNROLL == 1 && std::is_same<R, RoundF32>::value) {
+        if (end - start == (uint64_t)kPassSlice && (d.flags & kAligned16) != 0u && d.incoming == nullptr &&
+            !c.maximize && !c.coupled_weight_decay && c.update_parameter) {
+            if (xf.clip) lean_slice_unscale<P, G, S, C, HAS_COPY, true>(d, c, xf, start);
+            else lean_slice_unscale<P, G, S, C, HAS_COPY, false>(d, c, xf, start);
+            return;
+        }
+    }
 
     auto *pp = reinterpret_cast<typename P::raw *>(d.param);
     auto *gp = reinterpret_cast<const typename G::raw *>(d.grad);
