@@ -477,15 +477,21 @@ def bench_ceilings(nt, torch, steps, warmup):
     fp32 master/m/v + a bf16 copy written: 14 B each way); *_inplace
     variants rewrite the streams they read, as the passes do; r4w0 is a
     multi-stream read like the pre-pass.  HIP-event timed on the launch
-    stream; every stream is a fresh allocation of this process."""
+    stream; every stream is a fresh allocation of this process, filled with
+    random values (N(0, 0.02) fp32, N(0, 1e-3) bf16)."""
     import ctypes
     from namitorch_amd import _native
     handle = torch.cuda.current_stream().cuda_stream
     result = {"elements_per_stream": {"C2": C2_STREAM, "large": LARGE_STREAM}}
     for count in (C2_STREAM, LARGE_STREAM):
         mixes = [m for m in PROBE_MIXES if m[5] == count]
-        wide = [torch.zeros(count, dtype=torch.float32, device="cuda") for _ in range(max(m[1] + m[3] for m in mixes))]
-        narrow = [torch.zeros(count, dtype=torch.bfloat16, device="cuda") for _ in range(max(m[2] + m[4] for m in mixes))]
+        # Random values of the passes' magnitudes, not constant bytes: the
+        # bandwidth of these write-heavy mixes depends on the values moved.
+        generator = torch.Generator(device="cuda").manual_seed(4242)
+        wide = [torch.randn(count, generator=generator, device="cuda").mul_(0.02)
+                for _ in range(max(m[1] + m[3] for m in mixes))]
+        narrow = [torch.randn(count, generator=generator, device="cuda").mul_(1e-3).to(torch.bfloat16)
+                  for _ in range(max(m[2] + m[4] for m in mixes))]
         for name, r32, r16, w32, w16, _, inplace in mixes:
             reads = wide[:r32] + narrow[:r16]
             writes = wide[r32:r32 + w32] + narrow[r16:r16 + w16] if w32 + w16 else wide[-1:]
