@@ -1,5 +1,6 @@
-"""Host unit tests of the library's plain C++ parts — the plan-table builder
-and the caching memory pools — compiled with g++ under AddressSanitizer and
+"""Host unit tests of the library's plain C++ parts — the plan-table builder,
+the caching memory pools and the GradScaler / clip decisions the finalize
+kernels make — compiled with g++ under AddressSanitizer and
 UndefinedBehaviorSanitizer (no GPU involved)."""
 
 from __future__ import annotations
@@ -13,12 +14,12 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 
 
-def _run_sanitized(tmp_path, test_source: str, library_source: str) -> None:
+def _run_sanitized(tmp_path, test_source: str, library_source: str | None) -> None:
     binary = tmp_path / Path(test_source).stem
+    library = [] if library_source is None else [str(ROOT / "namitorch_amd" / "csrc" / library_source)]
     compile_cmd = ["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
-                   "-fno-sanitize-recover=undefined", "-Wall", "-Wextra", "-Werror",
-                   str(ROOT / "tests" / "host" / test_source),
-                   str(ROOT / "namitorch_amd" / "csrc" / library_source), "-o", str(binary)]
+                   "-fno-sanitize-recover=undefined", "-ffp-contract=off", "-Wall", "-Wextra", "-Werror",
+                   str(ROOT / "tests" / "host" / test_source), *library, "-o", str(binary)]
     built = subprocess.run(compile_cmd, capture_output=True, text=True)
     assert built.returncode == 0, built.stderr
     ran = subprocess.run([str(binary)], capture_output=True, text=True, timeout=60,
@@ -36,3 +37,10 @@ def test_plan_tables_under_sanitizers(tmp_path):
 @pytest.mark.skipif(shutil.which("g++") is None, reason="g++ is not installed")
 def test_memory_pools_under_sanitizers(tmp_path):
     _run_sanitized(tmp_path, "pool_test.cpp", "nt_pool.cpp")
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ is not installed")
+def test_scaler_decisions_under_sanitizers(tmp_path):
+    """Header-only: nt_scaler.hpp is the code the finalize and combine kernels
+    run for the norm, clip, skip and loss-scale decisions."""
+    _run_sanitized(tmp_path, "scaler_test.cpp", None)
