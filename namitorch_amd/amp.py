@@ -31,7 +31,8 @@ from .backends._graph_capture import reject_during_capture
 from .dtype import float32, float64, promote_with_scalar
 from .optim import clip_grad
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
-from .tensor import GradTransform, _requires_grad_changes, _unsettled_steps, check_addends, is_grad_enabled
+from .tensor import (GradTransform, _requires_grad_changes, _settle_lock, _unsettled_steps, check_addends,
+                     is_grad_enabled)
 
 _REQUIRES = attrgetter("_requires_grad")
 _PENDING = attrgetter("_pending")
@@ -121,10 +122,19 @@ class DeviceStep:
             pass
 
     def _forget(self) -> None:
-        """Leave the list of unsettled steps (every entry of this step)."""
-        _unsettled_steps[:] = [pending for pending in _unsettled_steps if pending is not self]
+        """Leave the list of unsettled steps (every entry of this step).  One
+        removal at a time: an entry another thread appends meanwhile stays."""
+        while True:
+            try:
+                _unsettled_steps.remove(self)
+            except ValueError:
+                return
 
     def ctrl(self) -> _native.AmpCtrl:
+        with _settle_lock:                    # one reader takes the mirror and gives it back
+            return self._read_ctrl()
+
+    def _read_ctrl(self) -> _native.AmpCtrl:
         if self._ctrl is None:
             mirror = self.mirror
             if mirror is None:
@@ -140,6 +150,10 @@ class DeviceStep:
         return self._ctrl
 
     def reconcile(self) -> None:
+        with _settle_lock:                    # the rollback below runs once, on one thread
+            self._reconcile()
+
+    def _reconcile(self) -> None:
         if self._reconciled:
             self._forget()                    # settled: never left waiting in the unsettled list
             return
@@ -189,7 +203,11 @@ class DeviceStep:
         if self.error_if_nonfinite:
             self.reconcile()
             if self.error is not None:
-                _error_watch[:] = [step for step in _error_watch if step is not self]
+                while True:
+                    try:
+                        _error_watch.remove(self)
+                    except ValueError:
+                        break
                 raise self.error
 
 
@@ -199,8 +217,11 @@ _error_watch: list = []
 
 
 def _raise_deferred_errors() -> None:
-    while _error_watch:
-        device_step = _error_watch.pop(0)
+    while True:
+        try:
+            device_step = _error_watch.pop(0)
+        except IndexError:                    # empty, or emptied by another thread
+            return
         device_step.raise_error()
 
 

@@ -339,6 +339,14 @@ _VALUE = attrgetter("value")
 _UNSETTLED_LIMIT = 64
 
 
+def _settle_oldest(pending: list) -> None:
+    try:
+        oldest = pending[0]
+    except IndexError:                    # another thread settled them all meanwhile
+        return
+    oldest.reconcile()
+
+
 def _norm_on_device(gradients, order: float, maximum: float, with_mirror: bool = False):
     """Queue the pre-pass and a finalize over `gradients` and a device copy
     of the norm, with no host wait: (backend, control block, 0-d float64
@@ -407,7 +415,7 @@ def _clip_on_device(gradients, maximum: float, order: float) -> Tensor | None:
             gradient._finite_version = counter.value
     clip_bumps.extend(zip(gradients, map(_VALUE, counters)))
     if len(_unsettled_steps) >= _UNSETTLED_LIMIT:
-        _unsettled_steps[0].reconcile()
+        _settle_oldest(_unsettled_steps)
     _unsettled_steps.append(device_step)                 # version reads settle it first
     return Tensor._from_storage(norm, False)
 

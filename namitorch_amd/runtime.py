@@ -240,12 +240,20 @@ _MIRROR_SLAB = 256
 _mirror_lock = threading.Lock()
 _mirror_idle: list = []            # addresses free for reuse
 _mirror_waiting: list = []         # given back before their writer was seen to finish
+_mirror_returned: list = []        # (address, launched) given back, not yet sorted
 _mirror_slabs: list = []
 
 
 def take_mirror():
     """A cleared ``_native.AmpMirror`` (``ready`` == 0) for the next finalize."""
     with _mirror_lock:
+        while True:
+            try:
+                address, launched = _mirror_returned.pop()
+            except IndexError:
+                break
+            ready = _native.AmpMirror.from_address(address).ready
+            (_mirror_idle if ready or not launched else _mirror_waiting).append(address)
         if not _mirror_idle and _mirror_waiting:
             still = []
             for address in _mirror_waiting:
@@ -265,10 +273,10 @@ def take_mirror():
 
 def give_mirror(mirror, launched: bool = True) -> None:
     """Return a mirror of :func:`take_mirror`.  `launched`: a kernel was
-    queued to write it (it is reused once its flag shows that write done)."""
-    address = ctypes.addressof(mirror)
-    with _mirror_lock:
-        (_mirror_idle if mirror.ready or not launched else _mirror_waiting).append(address)
+    queued to write it (it is reused once its flag shows that write done).
+    Takes no lock (one list append), so a finalizer may give a mirror back
+    while this thread is inside :func:`take_mirror`; the next take sorts it."""
+    _mirror_returned.append((ctypes.addressof(mirror), launched))
 
 
 def memory_stats(device: int = 0) -> dict:

@@ -74,19 +74,28 @@ class _VersionCounter:
 
 # Device-decided optimizer steps (namitorch_amd.amp.fused_step) whose host
 # bookkeeping (version counters, step counts) is still optimistic, oldest
-# first; each removes itself when reconciled.
+# first; each removes itself when reconciled.  Entries are added by a plain
+# append and removed one by one, so threads never lose each other's entries.
 _unsettled_steps: list = []
+
+# Held while a step is reconciled or its control block is read: each step's
+# rollback runs once, whichever thread settles it (its own optimizer's next
+# step, a result access, or an in-place write on any thread).  Re-entrant:
+# settling all pending steps holds it around each step's own reconcile.
+_settle_lock = threading.RLock()
 
 
 # Bumped whenever ``requires_grad`` changes on an existing Tensor (its only
 # route after creation), so memoized checks of the flag can skip re-reading
 # it while the count is unchanged.
 _requires_grad_changes = _VersionCounter()
+_requires_grad_lock = threading.Lock()
 
 
 def _settle_device_steps() -> None:
-    while _unsettled_steps:
-        _unsettled_steps[0].reconcile()
+    with _settle_lock:
+        while _unsettled_steps:
+            _unsettled_steps[0].reconcile()
 
 
 def check_addends(gradients) -> None:
@@ -432,7 +441,8 @@ class Tensor:
         if not self._is_leaf:
             raise ValueError("requires_grad can only be changed on leaf tensors.")
         self._requires_grad = value
-        _requires_grad_changes.value += 1
+        with _requires_grad_lock:            # no increment lost to another thread's
+            _requires_grad_changes.value += 1
 
     def requires_grad_(self, mode: builtins.bool = True) -> "Tensor":
         self.requires_grad = mode

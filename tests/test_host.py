@@ -317,6 +317,74 @@ def test_settled_device_step_never_stalls_the_unsettled_list():
     assert _unsettled_steps == before
 
 
+def test_device_step_rollback_runs_once_across_threads():
+    """A skipped device-decided step is rolled back once when two threads
+    settle it at the same time (its optimizer's next step on one, a version
+    read on another) while its control block is still being waited for: the
+    second finds it settled instead of undoing the bookkeeping again."""
+    import threading
+    import time
+
+    from namitorch_amd.amp import DeviceStep
+    from namitorch_amd.tensor import _unsettled_steps
+
+    class SlowStep(DeviceStep):
+        def _read_ctrl(self):
+            time.sleep(0.05)                # the wait for the finalize (GIL released)
+            return self.preset
+
+    gradient = nt.Tensor(np.zeros(4, np.float32))
+    gradient._version_counter.value = 7     # the optimistic bump of a clip that did not happen
+    step = SlowStep(None, None, unscale=True, honor_skip=True, clip_bumps=[(gradient, 7)])
+    step.preset = _native.AmpCtrl()
+    step.preset.skip = 1
+    step.preset.found_inf = 1
+    step.preset.clip = 0
+    parameter, first, second = (nt.Tensor(np.zeros(4, np.float32)) for _ in range(3))
+    for tensor in (parameter, first, second):
+        tensor._version_counter.value = 3   # the optimistic bump of the skipped step included
+    state = {"step": 5}
+    step.records.append((parameter, state, first, second, None, 5, True, True))
+    _unsettled_steps.append(step)
+    barrier = threading.Barrier(2)
+    errors = []
+
+    def settle():
+        try:
+            barrier.wait()
+            step.reconcile()
+        except Exception as error:          # pragma: no cover - reported below
+            errors.append(error)
+
+    threads = [threading.Thread(target=settle) for _ in range(2)]
+    for thread in threads:
+        thread.start()
+    for thread in threads:
+        thread.join(10)
+    assert not errors
+    assert state["step"] == 4
+    assert [tensor._version_counter.value for tensor in (parameter, first, second)] == [2, 2, 2]
+    assert first._clean_version == 2 and second._clean_version == 2
+    assert gradient._version_counter.value == 6
+    assert not any(pending is step for pending in _unsettled_steps)
+
+
+def test_mirror_return_takes_no_lock():
+    """Giving a host mirror back takes no lock, so a finalizer that returns
+    one while its thread is inside take_mirror (garbage collection can run
+    there) cannot deadlock on the pool's lock."""
+    from namitorch_amd import runtime
+    mirror = _native.AmpMirror()
+    address = ctypes.addressof(mirror)
+    try:
+        with runtime._mirror_lock:
+            runtime.give_mirror(mirror, launched=False)
+        assert (address, False) in runtime._mirror_returned
+    finally:
+        # never hand this host-owned struct to a kernel
+        runtime._mirror_returned[:] = [entry for entry in runtime._mirror_returned if entry[0] != address]
+
+
 def test_requires_grad_changes_are_counted():
     """Every change of requires_grad on an existing Tensor moves the count
     that memoized flag checks (the optimizer's step replay) compare."""
