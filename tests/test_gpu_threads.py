@@ -1,8 +1,10 @@
 """Threads: launches go to the calling thread's current stream, plans are
 cached per stream, and the step memo and control blocks belong to their
 optimizer and scaler.  Two threads stepping their own optimizers on their
-own streams at the same time (plain AdamW, and the AMP fused step) give
-results bit-identical to the same work run one after the other."""
+own streams at the same time (plain AdamW, and the AMP fused step with a
+skipped step and clip decisions settled from both threads) give results,
+step counts and version counters identical to the same work run one after
+the other."""
 
 from __future__ import annotations
 
@@ -46,7 +48,11 @@ def _work(seed: int, amp: bool, steps: int = 8):
     out = [p.numpy() for p in params] + [s["exp_avg"].numpy() for s in states] + [s["exp_avg_sq"].numpy() for s in states]
     if amp:
         out += [s["master"].numpy() for s in states] + [np.float64(scaler.get_scale())]
-    return out + [np.array([s["step"] for s in states])]
+    # Version reads settle every pending device-decided step, the other
+    # thread's included: each step's rollback must still run once.
+    versions = [t._version for t in params + [p.grad for p in params]]
+    versions += [s[key]._version for s in states for key in ("exp_avg", "exp_avg_sq")]
+    return out + [np.array([s["step"] for s in states]), np.array(versions)]
 
 
 @pytest.mark.parametrize("amp", [False, True])
