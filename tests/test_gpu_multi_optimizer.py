@@ -14,7 +14,8 @@ synchronizing API, with one float32 optimizer and one bfloat16-model /
 float32-master optimizer: finite/updated flags, the loss-scale sequence,
 step counts and versions exact; the norm within 1e-12 of the oracle's and
 bit-equal to the synchronizing path's; parameters, master weights and
-moments bit-exact.
+moments bit-exact.  Eight optimizers (one device combine's limit) and nine
+(the synchronizing fallback) match the reference loop too.
 """
 
 from __future__ import annotations
@@ -225,3 +226,58 @@ def test_refusals_match_the_reference():
     assert all(len(first.state.get(id(p), {})) == 0 for p in params)
     results = nt.amp.fused_step([first], scaler)                  # a one-element list is one iteration too
     assert [r.updated for r in results] == [True]
+
+
+@pytest.mark.parametrize("count", [8, 9])
+def test_combine_limit(count):
+    """Eight optimizers are the most one device combine takes; a ninth makes
+    fused_step take the synchronizing API.  Both give the reference loop's
+    flags, scales, states and versions bit for bit, with one optimizer's
+    gradients non-finite at step 2 (only it skips, the scale backs off)."""
+    rng = np.random.default_rng(53 + count)
+    sizes = [257 + 64 * i for i in range(count)]
+    values = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in sizes]
+
+    def build():
+        params = [nt.Parameter(v, device=DEV) for v in values]
+        return params, [nt.optim.AdamW([p], **KW) for p in params]
+
+    (params_f, opts_f), (params_s, opts_s) = build(), build()
+    scaler_f = nt.GradScaler(init_scale=1024.0, growth_interval=2)
+    scaler_s = nt.GradScaler(init_scale=1024.0, growth_interval=2)
+    loss = nt.Tensor(np.float32(1.0), device=DEV)
+    for k in range(5):
+        grads = [(rng.standard_normal(n) * 1e-3 * scaler_s.get_scale()).astype(np.float32) for n in sizes]
+        if k == 2:
+            grads[5][11] = np.inf
+        for params in (params_f, params_s):
+            for p, g in zip(params, grads):
+                p.grad = nt.Tensor(g, device=DEV)
+        scaler_f.scale(loss)
+        results = nt.amp.fused_step(opts_f, scaler_f, max_norm=0.02)
+        assert all((r._device_step is not None) == (count <= _native_max()) for r in results), k
+        scaler_s.scale(loss)
+        finite = [scaler_s.unscale_(opt) for opt in opts_s]
+        norm = nt.optim.clip_grad_norm_(params_s, 0.02).item() if all(finite) else None
+        updated = [scaler_s.step(opt) for opt in opts_s]
+        scaler_s.update()
+        assert [r.finite for r in results] == finite, k
+        assert [r.updated for r in results] == updated, k
+        assert updated == [not (k == 2 and i == 5) for i in range(count)], k
+        if norm is not None:
+            assert all(_f64_bits(r.norm) == _f64_bits(norm) for r in results), k
+        assert results[0].scale == scaler_s.get_scale() == scaler_f.get_scale(), k
+    for i, (p, q) in enumerate(zip(params_f, params_s)):
+        sf, ss = opts_f[i].state[id(p)], opts_s[i].state[id(q)]
+        assert sf["step"] == ss["step"] == (4 if i == 5 else 5), i
+        _same(f"param {i}", p.numpy(), q.numpy())
+        _same(f"exp_avg {i}", sf["exp_avg"].numpy(), ss["exp_avg"].numpy())
+        _same(f"exp_avg_sq {i}", sf["exp_avg_sq"].numpy(), ss["exp_avg_sq"].numpy())
+        assert p._version == q._version and p.grad._version == q.grad._version, i
+    # growth_interval 2: growth after steps 0-1, backoff at 2, growth after 3-4
+    assert scaler_f.get_scale() == 2048.0
+
+
+def _native_max() -> int:
+    from namitorch_amd import _native
+    return _native.NT_MAX_COMBINE
