@@ -16,7 +16,6 @@ present the norm is inf or NaN and the sum has no defined value.
 import ctypes
 import math
 
-import numpy as np
 import pytest
 import torch
 
