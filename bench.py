@@ -68,8 +68,8 @@ def parse_args():
     parser.add_argument("--profile", default=None, choices=sorted(MIXED),
                         help="only this config's step (for profilers): --warmup untimed, --steps timed")
     parser.add_argument("--profile-modes", default="fused",
-                        help="with --profile: the step paths to run in turn, 'fused' and/or 'api' (the reference "
-                             "call sequence), comma-separated")
+                        help="with --profile: the step paths to run in turn, 'fused', 'api' (the reference "
+                             "call sequence) and/or 'step' (scale, step, update; c3 only), comma-separated")
     return parser.parse_args()
 
 
@@ -315,6 +315,11 @@ def bench_mixed(nt, torch, name, shapes, *, param_dtype, grad_dtype, state_dtype
                 if amp:
                     scaler.scale(loss)
                 nt.amp.fused_step(optimizer, scaler, max_norm=max_norm)
+            elif mode == "step":
+                # the reference API without unscale_ (no clip): step unscales itself
+                scaler.scale(loss)
+                scaler.step(optimizer)
+                scaler.update()
             elif amp:
                 scaler.scale(loss)
                 finite = scaler.unscale_(optimizer)
@@ -792,7 +797,8 @@ def _mixed_configs(nt):
     from namitorch_amd.param_lists import decay_mask, gpt2_shapes, gpt_1p3b_shapes, llama7b_shapes, shard_shapes
     return {
         "c3": ("c3_gpt2_amp", dict(shapes=gpt2_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.float16,
-                                   state_dtype=None, amp=True, max_norm=None, bytes_per_param=30, evict=True)),
+                                   state_dtype=None, amp=True, max_norm=None, bytes_per_param=30, evict=True,
+                                   modes=("fused", "api", "step"))),
         "c4": ("c4_gpt1p3b_bf16_clip", dict(shapes=gpt_1p3b_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.bfloat16,
                                             state_dtype=nt.bfloat16, amp=False, max_norm=1.0, bytes_per_param=22)),
         "c5": ("c5_llama7b_amp_clip", dict(shapes=llama7b_shapes(), param_dtype=nt.bfloat16, grad_dtype=nt.bfloat16,
@@ -830,8 +836,10 @@ def main():
     if args.profile:
         key, spec = _mixed_configs(nt)[args.profile]
         modes = tuple(args.profile_modes.split(","))
-        if not modes or any(mode not in ("fused", "api") for mode in modes):
-            raise SystemExit("--profile-modes takes 'fused' and/or 'api', comma-separated")
+        if not modes or any(mode not in ("fused", "api", "step") for mode in modes):
+            raise SystemExit("--profile-modes takes 'fused', 'api' and/or 'step', comma-separated")
+        if "step" in modes and (not spec["amp"] or spec["max_norm"] is not None):
+            raise SystemExit("'step' mode (scale, step, update) is for the AMP config without a clip (c3)")
         spec = dict(spec, modes=modes, evict=False)
         shapes = spec.pop("shapes")
         log(f"{args.profile} {' then '.join(modes)} steps only ({args.warmup} untimed, {args.steps} timed each)")

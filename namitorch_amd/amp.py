@@ -30,6 +30,7 @@ from .backends import get_backend
 from .backends._graph_capture import reject_during_capture
 from .dtype import float32, float64, promote_with_scalar
 from .optim import clip_grad
+from .optim.adam import Adam
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
 from .tensor import (GradTransform, _requires_grad_changes, _settle_lock, _unsettled_steps, check_addends,
                      is_grad_enabled)
@@ -462,6 +463,9 @@ class GradScaler:
             return True
         identity = id(optimizer)
         if identity not in self._optimizer_states:
+            stepped = self._step_on_device(optimizer)
+            if stepped is not None:
+                return stepped
             self.unscale_(optimizer)
         state = self._optimizer_states[identity]
         if state["stage"] != "unscaled":
@@ -496,6 +500,67 @@ class GradScaler:
             return True
         state["stage"] = "stepped"
         return False
+
+    def _step_on_device(self, optimizer):
+        """``step`` without an earlier ``unscale_``, which the reference's
+        ``step`` then calls itself (amp.py:194-196).  The unscale, the finite
+        check and the AdamW pass are queued together, the pass skipping on
+        the device when a gradient is non-finite, and the host waits once,
+        for the finalize, after the pass is queued: the device does not idle
+        while the host prepares the pass, as it does after ``unscale_``'s
+        wait.  Returns the step's bool, or None before any change where the
+        host path (``unscale_``, then ``step``) runs instead: an optimizer
+        other than this package's Adam/AdamW, gradients on several devices
+        or of several dtypes, float64 gradients.
+
+        The reference calls ``optimizer.step()`` only after a finite
+        unscale.  Here it runs first; if it raises, the error is raised only
+        when the gradients turn out finite, and otherwise dropped with the
+        step reported skipped, as the reference would not have stepped."""
+        self._reconcile()
+        if not self._scale_used:
+            raise RuntimeError("Call scale(loss) and backward before unscale_.")
+        if not isinstance(optimizer, Adam):
+            return None
+        gradients = self._gradients(optimizer)
+        if not gradients:
+            raise RuntimeError("No gradients were found for this optimizer.")
+        previous = {id(parameter) for state in self._optimizer_states.values() for parameter, _ in state["gradients"]}
+        if previous and any(id(parameter) in previous for parameter, _ in gradients):
+            raise RuntimeError("Optimizers cannot share gradients in the same GradScaler iteration.")
+        grads = list(map(_SECOND_OF, gradients))
+        groups = _device_groups(grads)
+        if len(groups) != 1:
+            return None
+        (backend, dtype), _ = next(iter(groups.items()))
+        if dtype is float64 or backend.adamw is None:
+            return None
+        state = {"optimizer": optimizer, "stage": "unscaling", "gradients": gradients, "finite": False,
+                 "inputs": None}
+        self._optimizer_states[id(optimizer)] = state
+        # The block the finalize carries from holds the host's scale, which
+        # the pre-pass unscales by and the pass reads back as scale_used; no
+        # scaler update on the device (update() makes it on the host).
+        carry = backend.new_ctrl(self._scale, self._growth_tracker)
+        device_step = _queue_decisions(backend, dtype, grads, carry, amp=True, maximum=None, order=2.0, flags=0,
+                                       growth=self._growth_factor, backoff=self._backoff_factor,
+                                       interval=self._growth_interval, honor_skip=True)
+        state["stage"] = "stepping"
+        try:
+            optimizer.step()                              # the AdamW pass reads the control block
+        except Exception:
+            _unsettled_steps.append(device_step)
+            state["finite"] = not device_step.ctrl().found_inf
+            device_step.reconcile()
+            if state["finite"]:
+                raise
+            state["stage"] = "stepped"
+            return False
+        _unsettled_steps.append(device_step)              # version reads settle it first
+        state["finite"] = not device_step.ctrl().found_inf     # waits for the finalize, not the pass
+        device_step.reconcile()
+        state["stage"] = "stepped"
+        return state["finite"]
 
     def update(self):
         reject_during_capture("GradScaler")
@@ -619,18 +684,49 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
             previous = latest.block_for_current_stream()
     else:
         previous = backend.neutral_ctrl()
-    block = backend.empty_ctrl()
-    clip_bumps: list = []
     # error_if_nonfinite without a scaler: a non-finite norm skips the clip and the step.
     refuse = error_if_nonfinite and not amp and maximum is not None
+    flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
+    if refuse:
+        flags |= _native.NT_FINALIZE_CLIP_IF_FINITE
+    growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)
+    device_step = _queue_decisions(backend, dtype, gradients, previous, amp=amp, maximum=maximum, order=order,
+                                   flags=flags, growth=growth, backoff=backoff, interval=interval,
+                                   honor_skip=amp or refuse)
+    device_step.scheduler = scheduler
+    device_step.error_if_nonfinite = refuse
+    if amp:
+        scaler._reconcile()                               # earlier fused steps: their finalize already ran
+        scaler._device_blocks[backend] = device_step
+        scaler._device_steps.append(device_step)
+        scaler._scale_used = False
+    optimizer.step()                                      # the AdamW pass reads the control block
+    optimizer._track_device_step(device_step)
+    _unsettled_steps.append(device_step)                  # version reads settle it first
+    if refuse:
+        _error_watch.append(device_step)
+    return StepResult(device_step)
+
+
+def _queue_decisions(backend, dtype, gradients, previous, *, amp, maximum, order, flags, growth, backoff, interval,
+                     honor_skip) -> DeviceStep:
+    """Queue the pre-pass and the finalize over one (backend, dtype) group of
+    gradients, carrying the scaler state of the control block `previous`
+    (whose scale the pre-pass unscales by when `amp`), and give the
+    gradients the device-decided transform that the AdamW pass applies:
+    the unscale, the clip to `maximum` (when given) and, with `honor_skip`,
+    the skip.  Host bookkeeping is set as if the outcome were known: one
+    version bump for the unscale and one for the clip, the latter undone at
+    reconciliation when the device does not clip.  Returns the DeviceStep,
+    captured on the current stream; nothing is launched if a check raises."""
+    block = backend.empty_ctrl()
+    clip_bumps: list = []
     # float64 gradients may get a second norm pass after the finalize: that
     # block is read back with a copy instead of the finalize's mirror.
     mirror = None if dtype is float64 and order == 2.0 else runtime.take_mirror()
-    device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp or refuse, clip_bumps=clip_bumps,
+    device_step = DeviceStep(backend, block, unscale=amp, honor_skip=honor_skip, clip_bumps=clip_bumps,
                              mirror=mirror)
     device_step.clip_requested = maximum is not None
-    device_step.scheduler = scheduler
-    device_step.error_if_nonfinite = refuse
     transform = GradTransform(device=device_step)
     if any(map(_REQUIRES, gradients)) and is_grad_enabled():
         for gradient in gradients:
@@ -652,10 +748,6 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         clip_bumps.extend(zip(gradients, map(_VALUE, map(_COUNTER, gradients))))
     plan = backend.grad_plan(gradients, dtype, incoming=True)
     backend.grad_prepass(plan, None, previous.data_ptr(), unscale=amp)
-    flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
-    if refuse:
-        flags |= _native.NT_FINALIZE_CLIP_IF_FINITE
-    growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp else (2.0, 0.5, 1)
     backend.grad_finalize(plan, block.data_ptr(), order, -1.0 if maximum is None else maximum, flags,
                           growth, backoff, interval, carry_ptr=previous.data_ptr(), mirror=mirror)
     if dtype is float64 and order == 2.0:
@@ -665,17 +757,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
         backend.grad_norm_pow(plan, block.data_ptr(), 2.0, -1.0 if maximum is None else maximum, None,
                               scale_from_ctrl=amp, flags=_native.NT_NORM_POW_GUARD)
     device_step.capture()
-    if amp:
-        scaler._reconcile()                               # earlier fused steps: their finalize already ran
-        scaler._device_blocks[backend] = device_step
-        scaler._device_steps.append(device_step)
-        scaler._scale_used = False
-    optimizer.step()                                      # the AdamW pass reads the control block
-    optimizer._track_device_step(device_step)
-    _unsettled_steps.append(device_step)                  # version reads settle it first
-    if refuse:
-        _error_watch.append(device_step)
-    return StepResult(device_step)
+    return device_step
 
 
 def _check_scheduler(scheduler, optimizer) -> None:
