@@ -5,8 +5,9 @@ queued.  Checked bit for bit against the host path (``unscale_``, then
 ``step``) over sequences with inf and NaN iterations, growth and backoff:
 return values, scales, parameters, master weights, moments, step counts,
 version counters and the unscaled gradients; with two optimizers stepped
-separately in one iteration; and for an optimizer whose ``step`` raises,
-which the reference reaches only after a finite unscale."""
+separately in one iteration; with a deferred last micro-batch; and for an
+optimizer whose ``step`` raises, which the reference reaches only after a
+finite unscale."""
 
 from __future__ import annotations
 
@@ -198,3 +199,42 @@ def test_optimizer_errors_only_after_a_finite_unscale():
         with pytest.raises(RuntimeError, match="Call step\\(\\) for every unscaled optimizer before update\\(\\)."):
             scaler.update()
     assert errors[0] == errors[1]
+
+
+def test_deferred_accumulation_through_step_alone():
+    """The last micro-batch's deferred accumulation (accumulate_grads(...,
+    defer=True)) is added inside the pre-pass and the pass of step alone,
+    with the values, versions and skip of the host path."""
+    rng = np.random.default_rng(65)
+    values = [(rng.standard_normal(s) * 0.02).astype(np.float32) for s in SHAPES]
+    loss = nt.Tensor(np.float32(1.0), device=DEV)
+    runs = []
+    for explicit in (False, True):
+        params, optimizer = _build(values, "c3")
+        scaler = nt.GradScaler(init_scale=512.0, growth_interval=2)
+        draw = np.random.default_rng(66)
+        out = []
+        for k in range(5):
+            micro = [[(draw.standard_normal(s) * 5e-4 * scaler.get_scale()).astype(np.float32) for s in SHAPES]
+                     for _ in range(2)]
+            if k == 3:
+                micro[1][0].reshape(-1)[9] = np.inf               # in the deferred micro-batch
+            for p in params:
+                p.grad = None
+            nt.accumulate_grads(params, [nt.Tensor(g, dtype="float16", device=DEV) for g in micro[0]])
+            nt.accumulate_grads(params, [nt.Tensor(g, dtype="float16", device=DEV) for g in micro[1]], defer=True)
+            scaler.scale(loss)
+            if explicit:
+                scaler.unscale_(optimizer)
+            out.append(scaler.step(optimizer))
+            scaler.update()
+            out.append(scaler.get_scale())
+        state = [optimizer.state[id(p)] for p in params]
+        runs.append((out, [p.numpy() for p in params] + [s["master"].numpy() for s in state]
+                     + [p.grad.numpy() for p in params],
+                     [(p._version, p.grad._version, s["step"]) for p, s in zip(params, state)]))
+    (device, device_arrays, device_counts), (host, host_arrays, host_counts) = runs
+    assert device == host and device[6] is False
+    for i, (a, b) in enumerate(zip(device_arrays, host_arrays)):
+        _same(f"array {i}", a, b)
+    assert device_counts == host_counts
