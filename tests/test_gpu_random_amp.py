@@ -1,8 +1,9 @@
 """Seeded random AMP training sequences against the oracle.
 
-Each run mixes, step by step, ``amp.fused_step`` and the reference's call
+Each run mixes, step by step, ``amp.fused_step``, the reference's call
 sequence (``unscale_`` -> ``clip_grad_norm_`` if finite -> ``step`` ->
-``update``, training/runner.py:240-254) on one optimizer and one
+``update``, training/runner.py:240-254) and, without a clip, ``step`` ->
+``update`` alone (``step`` unscales by itself) on one optimizer and one
 GradScaler, with a warmup-cosine schedule that advances only after steps
 that updated (runner.py:250-253; ``fused_step(..., scheduler=)`` on the
 fused steps).  Along the way it injects inf/NaN gradients, changes the clip
@@ -84,6 +85,8 @@ def test_random_amp_sequence(seed, tmp_path):
     for step in range(STEPS):
         path = str(rng.choice(["api", "fused"]))
         max_norm = None if rng.random() < 0.4 else float(rng.choice([1e-3, 0.05, 10.0]))
+        if path == "api" and max_norm is None and step % 2 == 0:
+            path = "step"                                   # step() unscales by itself: nothing to clip between
         grads = [rng.standard_normal(s) * 1e-3 for s in shapes]
         stored = []
         for g in grads:
@@ -113,7 +116,12 @@ def test_random_amp_sequence(seed, tmp_path):
         scaler.scale(loss)
         for p, s in zip(params, stored):
             p.grad = nt.Tensor(s, dtype=gdtype, device=DEV)
-        if path == "api":
+        if path == "step":
+            updated = got_finite = scaler.step(optimizer)
+            scaler.update()
+            if updated:
+                scheduler.step()
+        elif path == "api":
             got_finite = scaler.unscale_(optimizer)
             if got_finite and max_norm is not None:
                 nt.optim.clip_grad_norm_(params, max_norm)
