@@ -30,7 +30,7 @@ from .backends import get_backend
 from .backends._graph_capture import reject_during_capture
 from .dtype import float32, float64, promote_with_scalar
 from .optim import clip_grad
-from .optim.adam import Adam
+from .optim.adam import Adam, AdamW
 from .optim.clip_grad import _device_groups, _nonnegative, _norm_type, clip_grad_norm_, grad_stats
 from .tensor import (GradTransform, _requires_grad_changes, _settle_lock, _unsettled_steps, check_addends,
                      is_grad_enabled)
@@ -510,8 +510,9 @@ class GradScaler:
         while the host prepares the pass, as it does after ``unscale_``'s
         wait.  Returns the step's bool, or None before any change where the
         host path (``unscale_``, then ``step``) runs instead: an optimizer
-        other than this package's Adam/AdamW, gradients on several devices
-        or of several dtypes, float64 gradients.
+        other than this package's Adam/AdamW (subclasses included),
+        gradients on several devices or of several dtypes, float64
+        gradients.
 
         The reference calls ``optimizer.step()`` only after a finite
         unscale.  Here it runs first; if it raises, the error is raised only
@@ -520,7 +521,7 @@ class GradScaler:
         self._reconcile()
         if not self._scale_used:
             raise RuntimeError("Call scale(loss) and backward before unscale_.")
-        if not isinstance(optimizer, Adam):
+        if type(optimizer) not in (Adam, AdamW):          # a subclass may read the gradients itself
             return None
         gradients = self._gradients(optimizer)
         if not gradients:
