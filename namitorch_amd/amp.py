@@ -665,7 +665,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
     if not gradients:
         raise RuntimeError("No gradients were found for this optimizer.")
     groups = _device_groups(gradients)
-    if len(groups) != 1:
+    if len(groups) != 1 or type(optimizer) not in (Adam, AdamW):   # a subclass may read the gradients itself
         result = _fused_step_host(optimizer, scaler, amp, maximum, order, [p for p, _ in pairs],
                                   error_if_nonfinite)
         if scheduler is not None and result.updated:
@@ -835,11 +835,12 @@ def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers, 
     refuse = error_if_nonfinite and not amp and maximum is not None
     if (refuse or not distinct or len(optimizers) > _native.NT_MAX_COMBINE or any(key is None for key in keys)
             or len({id(key[0]) for key in keys}) != 1 or any(key[1] is float64 for key in keys)
-            or keys[0][0].adamw is None):
+            or keys[0][0].adamw is None or any(type(optimizer) not in (Adam, AdamW) for optimizer in optimizers)):
         # Several devices, mixed dtypes within an optimizer, float64 (its
         # guarded second norm pass), repeated optimizers, more optimizers
-        # than one combine takes, or a clip that may raise without a scaler:
-        # the synchronizing API gives the same results.
+        # than one combine takes, a clip that may raise without a scaler, or
+        # an optimizer subclass (which may read the gradients itself): the
+        # synchronizing API gives the same results.
         return _fused_step_host_many(optimizers, scaler, amp, maximum, order, schedulers, error_if_nonfinite)
     backend = keys[0][0]
     for gradients in gathered:

@@ -238,3 +238,46 @@ def test_deferred_accumulation_through_step_alone():
     for i, (a, b) in enumerate(zip(device_arrays, host_arrays)):
         _same(f"array {i}", a, b)
     assert device_counts == host_counts
+
+
+def test_optimizer_subclasses_take_the_synchronizing_path():
+    """A subclass of AdamW may do its own work in step(): GradScaler.step and
+    fused_step call it only after a finite unscale, as the reference does,
+    and give the exact class's results."""
+
+    class Counted(nt.optim.AdamW):
+        calls = 0
+
+        def step(self, *args, **kwargs):
+            type(self).calls += 1
+            return super().step(*args, **kwargs)
+
+    rng = np.random.default_rng(67)
+    values = [(rng.standard_normal(s) * 0.02).astype(np.float32) for s in SHAPES]
+    loss = nt.Tensor(np.float32(1.0), device=DEV)
+    finals = []
+    for use_fused in (False, True):
+        for cls in (Counted, nt.optim.AdamW):
+            Counted.calls = 0
+            params = [nt.Parameter(v, device=DEV) for v in values]
+            optimizer = cls(params, **KW)
+            scaler = nt.GradScaler(init_scale=128.0)
+            draw = np.random.default_rng(68)
+            for k in range(4):
+                grads = [(draw.standard_normal(s) * 1e-3 * 128.0).astype(np.float32) for s in SHAPES]
+                if k == 1:
+                    grads[2][3] = np.nan
+                for p, g in zip(params, grads):
+                    p.grad = nt.Tensor(g, device=DEV)
+                scaler.scale(loss)
+                if use_fused:
+                    assert nt.amp.fused_step(optimizer, scaler).updated == (k != 1)
+                else:
+                    assert scaler.step(optimizer) == (k != 1)
+                    scaler.update()
+            if cls is Counted:
+                assert Counted.calls == 3, use_fused               # not called on the skipped step
+            finals.append([p.numpy() for p in params] + [scaler.get_scale()])
+    for a, b in zip(finals[0][:-1] + finals[2][:-1], finals[1][:-1] + finals[3][:-1]):
+        _same("subclass against AdamW", a, b)
+    assert finals[0][-1] == finals[1][-1] and finals[2][-1] == finals[3][-1]
