@@ -2,6 +2,7 @@
 // descriptor packing, task maps, alignment flags, error codes and pointer-column
 // checks.  Built by tests/test_host_tables.py with g++ and AddressSanitizer/UBSan;
 // runs without a GPU (the pointers are never dereferenced).
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <string>
@@ -133,11 +134,70 @@ static void test_pointer_columns() {
     CHECK(column_offset(5) == offsetof(DevTensor, incoming) && column_offset(5) == 56 && column_offset(4) == 32);
 }
 
+// Fixed-seed random tensor lists: every tensor's elements are covered by its
+// tasks exactly once, tasks are tensor-major and chunk-minor, the element
+// count adds up, and the 16-byte flag is set exactly when every pointer is
+// 16-byte aligned.
+static void test_random_lists() {
+    uint64_t state = 0x9e3779b97f4a7c15ull;
+    auto next = [&state](uint64_t bound) {
+        state = state * 6364136223846793005ull + 1442695040888963407ull;
+        return (state >> 33) % bound;
+    };
+    const nt_mt_layout layout{NT_F32, NT_BF16, NT_F32, NT_BF16};
+    const uint64_t sizes[5] = {4, 2, 4, 4, 2};
+    const uint64_t edges[] = {0, 1, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 8193};
+    const int64_t chunks[] = {0, 2048, 4096, 6144, 8192};
+    for (int round = 0; round < 300; ++round) {
+        const int n = 1 + (int)next(12);
+        std::vector<nt_mt_tensor> rows;
+        std::vector<bool> aligned;
+        for (int t = 0; t < n; ++t) {
+            const uint64_t numel = next(3) == 0 ? edges[next(10)] : next(50000);
+            uintptr_t pointer[5];
+            bool all16 = true;
+            for (int c = 0; c < 5; ++c) {
+                const uint64_t offset = next(2) == 0 ? 16 * next(4) : sizes[c] * next(8);
+                pointer[c] = (uintptr_t)(0x1000000ull * (uint64_t)(5 * t + c + 1) + offset);
+                all16 = all16 && pointer[c] % 16 == 0;
+            }
+            rows.push_back(tensor(pointer[0], pointer[1], pointer[2], pointer[3], numel, (uint32_t)next(NT_MAX_SLOTS)));
+            rows.back().model_copy = ptr(pointer[4]);
+            aligned.push_back(all16);
+        }
+        const int64_t requested = chunks[next(5)];
+        PlanTables out;
+        std::string error;
+        CHECK(build_plan_tables(rows.data(), n, &layout, requested, out, error) == NT_OK);
+        const uint64_t chunk = (uint64_t)out.chunk;
+        CHECK(chunk == (requested == 0 ? (uint64_t)kDefaultChunk : (uint64_t)requested));
+        uint64_t total = 0;
+        size_t task = 0;
+        for (int t = 0; t < n; ++t) {
+            const uint64_t numel = rows[(size_t)t].numel;
+            total += numel;
+            uint64_t covered = 0;
+            for (uint64_t c = 0; c * chunk < numel; ++c, ++task) {
+                CHECK(task < out.tasks.size());
+                if (task >= out.tasks.size()) return;
+                CHECK(out.tasks[task].tensor == (uint32_t)t && out.tasks[task].chunk == (uint32_t)c);
+                covered += std::min(chunk, numel - c * chunk);
+            }
+            CHECK(covered == numel);
+            CHECK((out.tensors[(size_t)t].flags == kAligned16) == aligned[(size_t)t]);
+            CHECK(out.tensors[(size_t)t].numel == numel && out.tensors[(size_t)t].slot == rows[(size_t)t].slot);
+        }
+        CHECK(task == out.tasks.size());
+        CHECK(out.numel == total);
+    }
+}
+
 int main() {
     test_packing_and_tasks();
     test_chunks();
     test_errors();
     test_pointer_columns();
+    test_random_lists();
     if (failures == 0) std::printf("plan tables: all checks passed\n");
     return failures == 0 ? 0 : 1;
 }
