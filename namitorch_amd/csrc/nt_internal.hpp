@@ -49,46 +49,15 @@ struct nt_plan {
 
 namespace nt {
 
-// ---- split launches ----------------------------------------------------------------------
-// A plan task of `chunk` elements may run on 2**shift workgroups, each taking
-// a slice of chunk >> shift elements: workgroup b covers slice
-// (b mod 2**shift) of task (b >> shift).  Streaming kernels use it to pick
-// the workgroup shape that moves their read/write mix fastest while the task
-// map stays as built.
-struct Slice {
-    uint64_t start, end;
-};
-
-// The dispatcher deals the workgroups of a grid to the eight XCDs in turn
-// (workgroup b runs on XCD b mod 8).  With per_xcd > 0 the grid's work is
-// renumbered so that it is walked in groups of 8 * per_xcd workgroups and,
-// within a group, each XCD takes one contiguous run of per_xcd (a short last
-// group is split the same way, the first n mod 8 XCDs taking one more): each
-// XCD then streams contiguous address ranges while the group front still
-// moves through memory in order.  A bijection on [0, n); per_xcd == 0 keeps
-// the launch order.
-__device__ __forceinline__ uint32_t xcd_grouped(uint32_t b, uint32_t n, uint32_t per_xcd) {
-    if (per_xcd == 0u) return b;
-    const uint32_t size = 8u * per_xcd;
-    const uint32_t base = b / size * size;
-    const uint32_t m = min(n - base, size), w = b - base;
-    const uint32_t q = m / 8u, r = m % 8u, x = w % 8u;
-    return base + x * q + min(x, r) + w / 8u;
-}
-
 // This workgroup's slice; false when it starts past the end of its tensor
 // (the last task of a tensor may be short).  `per_xcd` as in xcd_grouped.
 __device__ __forceinline__ bool task_slice(const DevTensor *__restrict__ tensors, const Task *__restrict__ tasks,
                                            int64_t chunk, int32_t shift, const DevTensor *&d, Slice &slice,
                                            uint32_t per_xcd = 0u) {
     const uint32_t b = xcd_grouped(blockIdx.x, gridDim.x, per_xcd);
-    const uint32_t part = b & ((1u << shift) - 1u);
     const Task task = tasks[b >> shift];
     d = &tensors[task.tensor];
-    const uint64_t width = (uint64_t)chunk >> shift;
-    slice.start = (uint64_t)task.chunk * (uint64_t)chunk + (uint64_t)part * width;
-    slice.end = min(slice.start + width, d->numel);
-    return slice.start < d->numel;
+    return slice_of(task, b & ((1u << shift) - 1u), d->numel, chunk, shift, slice);
 }
 
 // log2(chunk / slice) when that is a power of two in [1, 64] and the grid

@@ -46,4 +46,50 @@ static_assert(sizeof(Task) == 8, "task layout");
 constexpr int64_t kChunkQuantum = 2048;   // chunk sizes are multiples of this (16-byte aligned starts)
 constexpr int64_t kDefaultChunk = 4096;
 
+// The workgroup -> element arithmetic of the kernels, plain integer code
+// that also builds with the host compiler (its unit test checks it at full
+// grid sizes).
+#if defined(__HIPCC__)
+#define NT_LAYOUT_FN __host__ __device__ inline __attribute__((always_inline))
+#else
+#define NT_LAYOUT_FN inline
+#endif
+
+// ---- split launches ----------------------------------------------------------------------
+// A plan task of `chunk` elements may run on 2**shift workgroups, each taking
+// a slice of chunk >> shift elements: workgroup b covers slice
+// (b mod 2**shift) of task (b >> shift).  Streaming kernels use it to pick
+// the workgroup shape that moves their read/write mix fastest while the task
+// map stays as built.
+struct Slice {
+    uint64_t start, end;
+};
+
+// The dispatcher deals the workgroups of a grid to the eight XCDs in turn
+// (workgroup b runs on XCD b mod 8).  With per_xcd > 0 the grid's work is
+// renumbered so that it is walked in groups of 8 * per_xcd workgroups and,
+// within a group, each XCD takes one contiguous run of per_xcd (a short last
+// group is split the same way, the first n mod 8 XCDs taking one more): each
+// XCD then streams contiguous address ranges while the group front still
+// moves through memory in order.  A bijection on [0, n); per_xcd == 0 keeps
+// the launch order.
+NT_LAYOUT_FN uint32_t xcd_grouped(uint32_t b, uint32_t n, uint32_t per_xcd) {
+    if (per_xcd == 0u) return b;
+    const uint32_t size = 8u * per_xcd;
+    const uint32_t base = b / size * size;
+    const uint32_t m = n - base < size ? n - base : size, w = b - base;
+    const uint32_t q = m / 8u, r = m % 8u, x = w % 8u;
+    return base + x * q + (x < r ? x : r) + w / 8u;
+}
+
+// Slice `part` of `task` in a tensor of `numel` elements; false when it
+// starts past the tensor's end (the last task of a tensor may be short).
+NT_LAYOUT_FN bool slice_of(const Task &task, uint32_t part, uint64_t numel, int64_t chunk, int32_t shift,
+                           Slice &slice) {
+    const uint64_t width = (uint64_t)chunk >> shift;
+    slice.start = (uint64_t)task.chunk * (uint64_t)chunk + (uint64_t)part * width;
+    slice.end = slice.start + width < numel ? slice.start + width : numel;
+    return slice.start < numel;
+}
+
 }  // namespace nt

@@ -13,7 +13,7 @@
 #include "../../include/namitorch_amd.h"
 
 #if defined(__HIPCC__)
-#define NT_SCALER_FN __host__ __device__ __forceinline__
+#define NT_SCALER_FN __host__ __device__ inline __attribute__((always_inline))
 #else
 #define NT_SCALER_FN inline
 #endif

@@ -1,7 +1,8 @@
 """Host unit tests of the library's plain C++ parts — the plan-table builder,
-the caching memory pools and the GradScaler / clip decisions the finalize
-kernels make — compiled with g++ under AddressSanitizer and
-UndefinedBehaviorSanitizer (no GPU involved)."""
+the caching memory pools, the GradScaler / clip decisions the finalize
+kernels make and the kernels' workgroup -> element arithmetic — compiled
+with g++ under AddressSanitizer and UndefinedBehaviorSanitizer (no GPU
+involved)."""
 
 from __future__ import annotations
 
@@ -44,3 +45,10 @@ def test_scaler_decisions_under_sanitizers(tmp_path):
     """Header-only: nt_scaler.hpp is the code the finalize and combine kernels
     run for the norm, clip, skip and loss-scale decisions."""
     _run_sanitized(tmp_path, "scaler_test.cpp", None)
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ is not installed")
+def test_workgroup_layout_under_sanitizers(tmp_path):
+    """Header-only: nt_layout.hpp's XCD-grouped grid renumbering (a bijection
+    for every grid size) and task slicing (each element exactly once)."""
+    _run_sanitized(tmp_path, "layout_test.cpp", None)
