@@ -710,7 +710,7 @@ def fused_step(optimizer, scaler: GradScaler | None = None, *, max_norm=None, no
 
 
 def _queue_decisions(backend, dtype, gradients, previous, *, amp, maximum, order, flags, growth, backoff, interval,
-                     honor_skip) -> DeviceStep:
+                     honor_skip, combined=False) -> DeviceStep:
     """Queue the pre-pass and the finalize over one (backend, dtype) group of
     gradients, carrying the scaler state of the control block `previous`
     (whose scale the pre-pass unscales by when `amp`), and give the
@@ -719,7 +719,12 @@ def _queue_decisions(backend, dtype, gradients, previous, *, amp, maximum, order
     the skip.  Host bookkeeping is set as if the outcome were known: one
     version bump for the unscale and one for the clip, the latter undone at
     reconciliation when the device does not clip.  Returns the DeviceStep,
-    captured on the current stream; nothing is launched if a check raises."""
+    captured on the current stream; nothing is launched if a check raises.
+
+    `combined`: one of several optimizers of an iteration.  The finalize
+    then only gathers this optimizer's statistics (no clip, flags or host
+    copy); ``nt_amp_combine`` makes the decisions into every block, writes
+    the mirrors, and the caller captures the steps after it."""
     block = backend.empty_ctrl()
     clip_bumps: list = []
     # float64 gradients may get a second norm pass after the finalize: that
@@ -749,6 +754,10 @@ def _queue_decisions(backend, dtype, gradients, previous, *, amp, maximum, order
         clip_bumps.extend(zip(gradients, map(_VALUE, map(_COUNTER, gradients))))
     plan = backend.grad_plan(gradients, dtype, incoming=True)
     backend.grad_prepass(plan, None, previous.data_ptr(), unscale=amp)
+    if combined:
+        backend.grad_finalize(plan, block.data_ptr(), order, -1.0, 0, growth, backoff, interval,
+                              carry_ptr=previous.data_ptr())
+        return device_step
     backend.grad_finalize(plan, block.data_ptr(), order, -1.0 if maximum is None else maximum, flags,
                           growth, backoff, interval, carry_ptr=previous.data_ptr(), mirror=mirror)
     if dtype is float64 and order == 2.0:
@@ -854,34 +863,16 @@ def _fused_step_many(optimizers: list, scaler, max_norm, norm_type, schedulers, 
             else latest.block_for_current_stream()
     else:
         previous = backend.neutral_ctrl()
-    device_steps = []
-    for gradients, (_, dtype), scheduler in zip(gathered, keys, schedulers):
-        block = backend.empty_ctrl()
-        clip_bumps: list = []
-        device_step = DeviceStep(backend, block, unscale=amp, honor_skip=amp, clip_bumps=clip_bumps,
-                                 mirror=runtime.take_mirror())
-        device_step.clip_requested = maximum is not None
-        device_step.scheduler = scheduler
-        transform = GradTransform(device=device_step)
-        if any(map(_PENDING, gradients)):
-            for gradient in gradients:
-                if gradient._pending is not None:
-                    gradient._materialize()
-        bumps = int(amp) + int(maximum is not None)
-        deque(map(setattr, gradients, repeat("_pending"), repeat(transform)), 0)
-        counters = tuple(map(_COUNTER, gradients))
-        for counter in counters:
-            counter.value += bumps
-        deque(map(setattr, gradients, repeat("_finite_version"), map(_VALUE, counters)), 0)
-        if maximum is not None:
-            clip_bumps.extend(zip(gradients, map(_VALUE, counters)))
-        plan = backend.grad_plan(gradients, dtype, incoming=True)
-        backend.grad_prepass(plan, None, previous.data_ptr(), unscale=amp)
-        backend.grad_finalize(plan, block.data_ptr(), order, -1.0, 0, carry_ptr=previous.data_ptr())
-        device_steps.append(device_step)
     flags = (_native.NT_FINALIZE_SCALER_UPDATE | _native.NT_FINALIZE_CLIP_IF_FINITE) if amp else 0
     growth, backoff, interval = (scaler._growth_factor, scaler._backoff_factor, scaler._growth_interval) if amp \
         else (2.0, 0.5, 1)
+    device_steps = []
+    for gradients, (_, dtype), scheduler in zip(gathered, keys, schedulers):
+        device_step = _queue_decisions(backend, dtype, gradients, previous, amp=amp, maximum=maximum, order=order,
+                                       flags=flags, growth=growth, backoff=backoff, interval=interval,
+                                       honor_skip=amp, combined=True)
+        device_step.scheduler = scheduler
+        device_steps.append(device_step)
     backend.grad_combine([device_step.block for device_step in device_steps], previous, order,
                          -1.0 if maximum is None else maximum, flags, growth, backoff, interval,
                          mirrors=[device_step.mirror for device_step in device_steps])
