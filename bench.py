@@ -19,9 +19,9 @@ same workload on this host, one core.
 
 The other configurations (C1 flat 4M fp32 hot and MALL-flushed, C3 AMP
 GPT-2, C4 GPT-1.3B bf16 + clip, C5 Llama-7B AMP + clip) are reported under
-``extra`` with their own B/param accounting, each through ``fused_step``
-(``fused``) and the reference call sequence (``api``: unscale_, clip when
-finite, step, update); C3 also through ``step`` alone (``step``: scale,
+``extra`` with their own B/param accounting; C3, C4 and C5 each through
+``fused_step`` (``fused``) and the reference call sequence (``api``:
+unscale_, clip when finite, step, update), C3 also through ``step`` alone (``step``: scale,
 step, update, the reference API without unscale_), together with one GPU's share
 of an 8-way sharded C4 and C5 step (``c4s8``, ``c5s8``: every tensor split
 into 8 contiguous slices, the local work between the collectives).
