@@ -319,8 +319,11 @@ def _norm_tensor(norm: float, gradients) -> Tensor:
         return Tensor._from_storage(np.array(norm, dtype=np.float64), False)
     # A fill with the value's bits as a kernel argument: no host-to-device copy to wait for.
     storage = DeviceArray.empty((), float64, device)
-    storage.fill_bits(int(np.float64(norm).view(np.uint64)))
-    return Tensor._from_storage(storage, False)
+    value = np.float64(norm)
+    storage.fill_bits(int(value.view(np.uint64)))
+    result = Tensor._from_storage(storage, False)
+    result._known_item = (value.item(), result._version_counter.value)   # .item() needs no device read
+    return result
 
 
 def get_grad_norm(parameters, norm_type: float = 2) -> Tensor:

@@ -316,7 +316,7 @@ class Tensor:
     __slots__ = (
         "_storage", "_dtype", "_device", "_requires_grad", "_grad", "_version_counter",
         "_pending", "_incoming", "_is_leaf", "_ptr", "_numel", "_shape", "_clean_version",
-        "_finite_version", "__weakref__",
+        "_finite_version", "_known_item", "__weakref__",
     )
     # Every Tensor here may be written in place: device storage always, and
     # host arrays through NumPy, which refuses writes to read-only arrays by
@@ -370,6 +370,7 @@ class Tensor:
         self._is_leaf = True
         self._clean_version = None      # version at which a state buffer was last known nonnegative
         self._finite_version = None     # version at which GradScaler last knew the gradient's finiteness
+        self._known_item = None         # (value, version): the host knows the value this device scalar was filled with
 
     @classmethod
     def _from_storage(cls, storage, requires_grad: builtins.bool = False, version_counter=None,
@@ -548,6 +549,12 @@ class Tensor:
         reject_during_capture("Host Tensor reads")
         if self.size != 1:
             raise ValueError(f"item() requires exactly one element, got {self.size}.")
+        # A device scalar filled from a host value (the norm clip_grad_norm_
+        # returns) and not written since: the same value without a device
+        # round trip.  Every write through this package bumps the version.
+        known = self._known_item
+        if known is not None and known[1] == self._version_counter.value:
+            return known[0]
         return self.numpy().reshape(()).item()
 
     def detach(self) -> "Tensor":

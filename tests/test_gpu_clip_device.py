@@ -437,3 +437,34 @@ def test_versions_when_a_write_lands_before_the_clip_settles(write):
             assert np.allclose(got, np.asarray(g, np.float32), rtol=1e-6, atol=0), write
         else:
             assert _same(got, np.asarray(g, np.float32)), write
+
+
+def test_host_known_norm_reads_without_a_device_round_trip(monkeypatch):
+    """After unscale_ the norm is known on the host: clip_grad_norm_'s
+    returned device scalar hands it to .item() without reading the device,
+    with the bits the device holds; once written in place, .item() reads the
+    device again."""
+    rng = np.random.default_rng(91)
+    params = [nt.Parameter((rng.standard_normal(s) * 0.02).astype(np.float32), device=DEV) for s in SHAPES]
+    for p in params:
+        p.grad = nt.Tensor((rng.standard_normal(p.shape) * 64.0).astype(np.float32), device=DEV)
+    optimizer = nt.optim.AdamW(params)
+    scaler = nt.GradScaler(init_scale=1024.0)
+    scaler.scale(nt.Tensor(np.float32(1.0), device=DEV))
+    assert scaler.unscale_(optimizer)
+    norm = nt.optim.clip_grad_norm_(params, 0.5, error_if_nonfinite=True)
+    reads = []
+    original = nt.Tensor.numpy
+
+    def counted(self):
+        reads.append(self)
+        return original(self)
+    monkeypatch.setattr(nt.Tensor, "numpy", counted)
+    value = norm.item()
+    assert reads == []
+    assert isinstance(value, float)
+    assert np.float64(value).view(np.uint64) == original(norm).view(np.uint64)   # what the device holds
+    norm.copy_(nt.Tensor(np.float64(3.25), device=DEV))
+    assert norm.item() == 3.25 and len(reads) == 1
+    scaler.step(optimizer)
+    scaler.update()
